@@ -1,0 +1,664 @@
+// Optimizer and gradient-bucket kernels: fused AdamW (flat and multi-tensor),
+// bucket flatten, fixed-order replica average with fused sum of squares,
+// deterministic sum of squares and the clip factor.
+//
+// All of these are HBM-bound streaming kernels: 16-byte vector loads and stores
+// (float4 / double2) when every operand is 16-byte aligned, several vectors in
+// flight per thread, and grid-stride loops over a grid that depends only on the
+// problem size (so per-block partial sums, and therefore results, are the same
+// on every run and every device).
+//
+// Bit-exactness: this file is compiled with -ffp-contract=off and every update
+// below is written as the same sequence of IEEE operations NumPy performs for
+// dtrain's expressions, so F64 (and F32) results equal NumPy's bit for bit.
+#include <cmath>
+#include <vector>
+
+#include "common.h"
+
+namespace dtmi {
+
+template <typename T>
+struct V16;
+template <>
+struct V16<float> {
+  using type = float4;
+  static constexpr int N = 4;
+};
+template <>
+struct V16<double> {
+  using type = double2;
+  static constexpr int N = 2;
+};
+
+template <typename T>
+__device__ __forceinline__ T vget(const typename V16<T>::type& v, int i);
+template <>
+__device__ __forceinline__ float vget<float>(const float4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+template <>
+__device__ __forceinline__ double vget<double>(const double2& v, int i) {
+  return i == 0 ? v.x : v.y;
+}
+template <typename T>
+__device__ __forceinline__ void vset(typename V16<T>::type& v, int i, T x);
+template <>
+__device__ __forceinline__ void vset<float>(float4& v, int i, float x) {
+  if (i == 0) v.x = x;
+  else if (i == 1) v.y = x;
+  else if (i == 2) v.z = x;
+  else v.w = x;
+}
+template <>
+__device__ __forceinline__ void vset<double>(double2& v, int i, double x) {
+  if (i == 0) v.x = x;
+  else v.y = x;
+}
+
+// --------------------------------------------------------------- AdamW
+template <typename T>
+struct AdamWScalars {
+  T lr, b1, b2, eps, wd, c1, c2, b1t, b2t, gscale;
+};
+
+template <typename T>
+static AdamWScalars<T> make_scalars(double lr, double b1, double b2, double eps, double wd, double c1, double c2,
+                                    double b1t, double b2t, double gscale) {
+  // Host rounding double -> T (round to nearest), as NumPy does for a weak
+  // Python float meeting an array of dtype T.
+  return AdamWScalars<T>{(T)lr, (T)b1, (T)b2, (T)eps, (T)wd, (T)c1, (T)c2, (T)b1t, (T)b2t, (T)gscale};
+}
+
+// dtrain/optim.py:28-33, one element, in NumPy's operation order:
+//   g = g * s                                  (train.py:159, the clip pre-scale)
+//   m *= b1 ; m += (1 - b1) * g
+//   v *= b2 ; v += (1 - b2) * (g * g)
+//   p -= lr * (wd * p)
+//   p -= lr * (m / b1t) / (sqrt(v / b2t) + eps)
+template <typename T>
+__device__ __forceinline__ void adamw_elem(T& p, T g, T& m, T& v, const AdamWScalars<T>& s, T gs) {
+  g = g * gs;
+  m = m * s.b1;
+  T t1 = s.c1 * g;
+  m = m + t1;
+  v = v * s.b2;
+  T gg = g * g;
+  T t2 = s.c2 * gg;
+  v = v + t2;
+  T d = s.wd * p;
+  d = s.lr * d;
+  p = p - d;
+  T mh = m / s.b1t;
+  T num = s.lr * mh;
+  T vh = v / s.b2t;
+  T den = sqrt(vh);
+  den = den + s.eps;
+  T step = num / den;
+  p = p - step;
+}
+
+template <typename T>
+__device__ __forceinline__ T load_gscale(const AdamWScalars<T>& s, const double* gdev) {
+  return gdev ? (T)(*gdev) : s.gscale;
+}
+
+constexpr int kUnroll = 4;
+
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(256) adamw_flat_kernel(T* __restrict__ p, const T* __restrict__ g,
+                                                          T* __restrict__ m, T* __restrict__ v, int64_t n,
+                                                          AdamWScalars<T> s, const double* gdev) {
+  const T gs = load_gscale(s, gdev);
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+  if (VEC) {
+    using VT = typename V16<T>::type;
+    constexpr int N = V16<T>::N;
+    const int64_t nv = n / N;
+    VT* pv = reinterpret_cast<VT*>(p);
+    const VT* gv = reinterpret_cast<const VT*>(g);
+    VT* mv = reinterpret_cast<VT*>(m);
+    VT* vv = reinterpret_cast<VT*>(v);
+    int64_t i = tid;
+    for (; i + (kUnroll - 1) * nthreads < nv; i += kUnroll * nthreads) {
+      VT P[kUnroll], G[kUnroll], M[kUnroll], W[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        int64_t k = i + u * nthreads;
+        P[u] = pv[k];
+        G[u] = gv[k];
+        M[u] = mv[k];
+        W[u] = vv[k];
+      }
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          T pe = vget<T>(P[u], e), me = vget<T>(M[u], e), ve = vget<T>(W[u], e);
+          adamw_elem<T>(pe, vget<T>(G[u], e), me, ve, s, gs);
+          vset<T>(P[u], e, pe);
+          vset<T>(M[u], e, me);
+          vset<T>(W[u], e, ve);
+        }
+        int64_t k = i + u * nthreads;
+        pv[k] = P[u];
+        mv[k] = M[u];
+        vv[k] = W[u];
+      }
+    }
+    for (; i < nv; i += nthreads) {
+      VT P = pv[i], G = gv[i], M = mv[i], W = vv[i];
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        T pe = vget<T>(P, e), me = vget<T>(M, e), ve = vget<T>(W, e);
+        adamw_elem<T>(pe, vget<T>(G, e), me, ve, s, gs);
+        vset<T>(P, e, pe);
+        vset<T>(M, e, me);
+        vset<T>(W, e, ve);
+      }
+      pv[i] = P;
+      mv[i] = M;
+      vv[i] = W;
+    }
+    for (int64_t k = nv * N + tid; k < n; k += nthreads) adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);
+  } else {
+    for (int64_t k = tid; k < n; k += nthreads) adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);
+  }
+}
+
+static int stream_grid(int64_t units, int per_thread) {
+  int64_t b = cdiv(units, 256LL * per_thread);
+  if (b < 1) b = 1;
+  // At least a few waves per CU on the largest problems; never more blocks
+  // than there is work for.
+  const int64_t cap = 2048;
+  return (int)(b < cap ? b : cap);
+}
+
+template <typename T>
+static int launch_adamw_flat(void* p, const void* g, void* m, void* v, int64_t n, const AdamWScalars<T>& s,
+                             const double* gdev) {
+  bool vec = aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16);
+  int grid = stream_grid(vec ? n / V16<T>::N + 1 : n, vec ? kUnroll : 4);
+  TimedLaunch tl(DTMI_FAM_ADAMW, 7.0 * (double)n * sizeof(T));
+  if (vec)
+    adamw_flat_kernel<T, true><<<grid, 256, 0, stream()>>>((T*)p, (const T*)g, (T*)m, (T*)v, n, s, gdev);
+  else
+    adamw_flat_kernel<T, false><<<grid, 256, 0, stream()>>>((T*)p, (const T*)g, (T*)m, (T*)v, n, s, gdev);
+  LAUNCH_CHECK("adamw_flat_kernel");
+  return DTMI_OK;
+}
+
+// Multi-tensor table: one entry per tensor; chunk c of the launch belongs to
+// the entry e with e.chunk_begin <= c < next.chunk_begin.
+constexpr int64_t kChunk = 32768;
+
+struct MTAdamEntry {
+  void* p;
+  const void* g;
+  void* m;
+  void* v;
+  int64_t n;
+  int64_t chunk_begin;
+  int64_t vec;
+};
+
+__device__ __forceinline__ int find_entry(const int64_t* begins, int stride_i64, int count, int64_t c) {
+  // largest e with begins[e * stride] <= c (entries sorted by chunk_begin)
+  int lo = 0, hi = count - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if (begins[(int64_t)mid * stride_i64] <= c)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) adamw_multi_kernel(const MTAdamEntry* __restrict__ tab, int count,
+                                                           AdamWScalars<T> s, const double* gdev) {
+  const int64_t c = blockIdx.x;
+  const int e = find_entry(&tab[0].chunk_begin, sizeof(MTAdamEntry) / sizeof(int64_t), count, c);
+  const MTAdamEntry ent = tab[e];
+  const T gs = load_gscale(s, gdev);
+  const int64_t lo = (c - ent.chunk_begin) * kChunk;
+  const int64_t hi = lo + kChunk < ent.n ? lo + kChunk : ent.n;
+  T* p = (T*)ent.p;
+  const T* g = (const T*)ent.g;
+  T* m = (T*)ent.m;
+  T* v = (T*)ent.v;
+  if (ent.vec) {
+    using VT = typename V16<T>::type;
+    constexpr int N = V16<T>::N;
+    // lo is a multiple of kChunk (a multiple of N); only the last chunk has a tail.
+    const int64_t nv = (hi - lo) / N;
+    VT* pv = reinterpret_cast<VT*>(p + lo);
+    const VT* gv = reinterpret_cast<const VT*>(g + lo);
+    VT* mv = reinterpret_cast<VT*>(m + lo);
+    VT* vv = reinterpret_cast<VT*>(v + lo);
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+      VT P = pv[i], G = gv[i], M = mv[i], W = vv[i];
+#pragma unroll
+      for (int el = 0; el < N; ++el) {
+        T pe = vget<T>(P, el), me = vget<T>(M, el), ve = vget<T>(W, el);
+        adamw_elem<T>(pe, vget<T>(G, el), me, ve, s, gs);
+        vset<T>(P, el, pe);
+        vset<T>(M, el, me);
+        vset<T>(W, el, ve);
+      }
+      pv[i] = P;
+      mv[i] = M;
+      vv[i] = W;
+    }
+    for (int64_t k = lo + nv * N + threadIdx.x; k < hi; k += blockDim.x) adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);
+  } else {
+    for (int64_t k = lo + threadIdx.x; k < hi; k += blockDim.x) adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);
+  }
+}
+
+// ------------------------------------------------------------- flatten
+struct FlatEntry {
+  const void* src;  // NULL: write zeros
+  int64_t n;
+  int64_t dst_off;
+  int64_t chunk_begin;
+  int64_t vec;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) flatten_kernel(T* __restrict__ dst, const FlatEntry* __restrict__ tab,
+                                                       int count) {
+  const int64_t c = blockIdx.x;
+  const int e = find_entry(&tab[0].chunk_begin, sizeof(FlatEntry) / sizeof(int64_t), count, c);
+  const FlatEntry ent = tab[e];
+  const int64_t lo = (c - ent.chunk_begin) * kChunk;
+  const int64_t hi = lo + kChunk < ent.n ? lo + kChunk : ent.n;
+  const T* src = (const T*)ent.src;
+  T* out = dst + ent.dst_off;
+  if (ent.vec) {
+    using VT = typename V16<T>::type;
+    constexpr int N = V16<T>::N;
+    const int64_t nv = (hi - lo) / N;
+    VT* ov = reinterpret_cast<VT*>(out + lo);
+    if (src) {
+      const VT* sv = reinterpret_cast<const VT*>(src + lo);
+      for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) ov[i] = sv[i];
+    } else {
+      VT z;
+      for (int el = 0; el < N; ++el) vset<T>(z, el, T(0));
+      for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) ov[i] = z;
+    }
+    for (int64_t k = lo + nv * N + threadIdx.x; k < hi; k += blockDim.x) out[k] = src ? src[k] : T(0);
+  } else {
+    for (int64_t k = lo + threadIdx.x; k < hi; k += blockDim.x) out[k] = src ? src[k] : T(0);
+  }
+}
+
+// ------------------------------------------------------ block reduction
+// Deterministic sum of one double per thread across a 256-thread block:
+// butterfly within each wave (fixed pattern), then wave results in order.
+__device__ __forceinline__ double block_sum_256(double x, double* lds4) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) lds4[wave] = x;
+  __syncthreads();
+  double r = 0.0;
+  if (threadIdx.x == 0) r = ((lds4[0] + lds4[1]) + lds4[2]) + lds4[3];
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ double sq64(T x) {
+  double d = (double)x;
+  return d * d;
+}
+
+// ------------------------------------------------- fixed-order average
+template <typename T, bool VEC, bool SUMSQ>
+__global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out, const T* __restrict__ rep,
+                                                              int world, int64_t n, int64_t stride, T inv,
+                                                              double* __restrict__ partials) {
+  __shared__ double lds[4];
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+  double acc = 0.0;
+  if (VEC) {
+    using VT = typename V16<T>::type;
+    constexpr int N = V16<T>::N;
+    const int64_t nv = n / N;
+    for (int64_t i = tid; i < nv; i += nthreads) {
+      VT a = reinterpret_cast<const VT*>(rep)[i];
+      for (int r = 1; r < world; ++r) {
+        VT b = reinterpret_cast<const VT*>(rep + (int64_t)r * stride)[i];
+#pragma unroll
+        for (int e = 0; e < N; ++e) vset<T>(a, e, vget<T>(a, e) + vget<T>(b, e));
+      }
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        T o = vget<T>(a, e) * inv;
+        vset<T>(a, e, o);
+        if (SUMSQ) acc += sq64(o);
+      }
+      reinterpret_cast<VT*>(out)[i] = a;
+    }
+    for (int64_t k = nv * N + tid; k < n; k += nthreads) {
+      T a = rep[k];
+      for (int r = 1; r < world; ++r) a = a + rep[(int64_t)r * stride + k];
+      T o = a * inv;
+      out[k] = o;
+      if (SUMSQ) acc += sq64(o);
+    }
+  } else {
+    for (int64_t k = tid; k < n; k += nthreads) {
+      T a = rep[k];
+      for (int r = 1; r < world; ++r) a = a + rep[(int64_t)r * stride + k];
+      T o = a * inv;
+      out[k] = o;
+      if (SUMSQ) acc += sq64(o);
+    }
+  }
+  if (SUMSQ) {
+    double b = block_sum_256(acc, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = b;
+  }
+}
+
+static int average_grid(int64_t n) {
+  // Function of n only: the per-block partial sums must not depend on the device.
+  int64_t b = cdiv(n, 256LL * 16);
+  if (b < 1) b = 1;
+  return (int)(b < 2048 ? b : 2048);
+}
+
+// -------------------------------------------------------- sum of squares
+struct SumsqEntry {
+  const void* p;
+  int64_t n;
+  int64_t chunk_begin;
+  int64_t vec;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) sumsq_multi_kernel(const SumsqEntry* __restrict__ tab, int count,
+                                                           double* __restrict__ partials) {
+  __shared__ double lds[4];
+  const int64_t c = blockIdx.x;
+  const int e = find_entry(&tab[0].chunk_begin, sizeof(SumsqEntry) / sizeof(int64_t), count, c);
+  const SumsqEntry ent = tab[e];
+  const int64_t lo = (c - ent.chunk_begin) * kChunk;
+  const int64_t hi = lo + kChunk < ent.n ? lo + kChunk : ent.n;
+  const T* x = (const T*)ent.p;
+  double acc = 0.0;
+  if (ent.vec) {
+    using VT = typename V16<T>::type;
+    constexpr int N = V16<T>::N;
+    const int64_t nv = (hi - lo) / N;
+    const VT* xv = reinterpret_cast<const VT*>(x + lo);
+    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+      VT a = xv[i];
+#pragma unroll
+      for (int el = 0; el < N; ++el) acc += sq64(vget<T>(a, el));
+    }
+    for (int64_t k = lo + nv * N + threadIdx.x; k < hi; k += blockDim.x) acc += sq64(x[k]);
+  } else {
+    for (int64_t k = lo + threadIdx.x; k < hi; k += blockDim.x) acc += sq64(x[k]);
+  }
+  double b = block_sum_256(acc, lds);
+  if (threadIdx.x == 0) partials[c] = b;
+}
+
+// One block of 1024 threads sums `count` partials: thread t adds partials
+// t, t+1024, ... in order, then a fixed tree.
+__global__ void __launch_bounds__(1024) sumsq_finish_kernel(const double* __restrict__ partials, int64_t count,
+                                                             double* __restrict__ out, int accumulate) {
+  __shared__ double lds[16];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < count; i += 1024) acc += partials[i];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double r = 0.0;
+    for (int w = 0; w < 16; ++w) r += lds[w];
+    *out = accumulate ? *out + r : r;
+  }
+}
+
+__global__ void clip_scale_kernel(const double* sq, double max_norm, double* scale, double* norm) {
+  double n = sqrt(*sq);
+  double s = (n <= max_norm || n == 0.0) ? 1.0 : max_norm / (n + 1e-6);
+  *scale = s;
+  if (norm) *norm = n;
+}
+
+}  // namespace dtmi
+
+using namespace dtmi;
+
+DTMI_EXPORT int dtmi_adamw(int dtype, void* p, const void* g, void* m, void* v, int64_t n, double lr, double b1,
+                           double b2, double eps, double wd, double c1, double c2, double b1t, double b2t,
+                           double gscale, const double* gscale_dev) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(n >= 0, "dtmi_adamw: negative size");
+  if (n == 0) return DTMI_OK;
+  DTMI_CHECK(p && g && m && v, "dtmi_adamw: NULL pointer");
+  if (dtype == DTMI_F32)
+    return launch_adamw_flat<float>(p, g, m, v, n, make_scalars<float>(lr, b1, b2, eps, wd, c1, c2, b1t, b2t, gscale),
+                                    gscale_dev);
+  return launch_adamw_flat<double>(p, g, m, v, n, make_scalars<double>(lr, b1, b2, eps, wd, c1, c2, b1t, b2t, gscale),
+                                   gscale_dev);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_adamw_multi(int dtype, int ntensors, void* const* p, const void* const* g, void* const* m,
+                                 void* const* v, const int64_t* n, double lr, double b1, double b2, double eps,
+                                 double wd, double c1, double c2, double b1t, double b2t, double gscale,
+                                 const double* gscale_dev) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(ntensors >= 0, "dtmi_adamw_multi: negative tensor count");
+  DTMI_CHECK(ntensors == 0 || (p && g && m && v && n), "dtmi_adamw_multi: NULL table");
+  const size_t es = dtype == DTMI_F32 ? 4 : 8;
+  std::vector<MTAdamEntry> tab;
+  tab.reserve(ntensors);
+  int64_t chunks = 0;
+  double bytes = 0;
+  for (int i = 0; i < ntensors; ++i) {
+    DTMI_CHECK(n[i] >= 0, "dtmi_adamw_multi: tensor %d has negative size", i);
+    if (g[i] == nullptr || n[i] == 0) continue;  // optim.py:26-27: no gradient, no update
+    DTMI_CHECK(p[i] && m[i] && v[i], "dtmi_adamw_multi: tensor %d has a NULL p/m/v", i);
+    bool vec = aligned(p[i], 16) && aligned(g[i], 16) && aligned(m[i], 16) && aligned(v[i], 16);
+    tab.push_back(MTAdamEntry{p[i], g[i], m[i], v[i], n[i], chunks, vec ? 1 : 0});
+    chunks += cdiv(n[i], kChunk);
+    bytes += 7.0 * (double)n[i] * es;
+  }
+  if (tab.empty()) return DTMI_OK;
+  DTMI_CHECK(chunks < (int64_t)1 << 31, "dtmi_adamw_multi: too many chunks");
+  void* dtab = nullptr;
+  int rc = upload_table(tab.data(), tab.size() * sizeof(MTAdamEntry), &dtab);
+  if (rc) return rc;
+  {
+    TimedLaunch tl(DTMI_FAM_ADAMW, bytes);
+    if (dtype == DTMI_F32)
+      adamw_multi_kernel<float><<<(unsigned)chunks, 256, 0, stream()>>>(
+          (const MTAdamEntry*)dtab, (int)tab.size(), make_scalars<float>(lr, b1, b2, eps, wd, c1, c2, b1t, b2t, gscale),
+          gscale_dev);
+    else
+      adamw_multi_kernel<double><<<(unsigned)chunks, 256, 0, stream()>>>(
+          (const MTAdamEntry*)dtab, (int)tab.size(),
+          make_scalars<double>(lr, b1, b2, eps, wd, c1, c2, b1t, b2t, gscale), gscale_dev);
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(dtab);
+  if (le != hipSuccess) return fail_hip(le, "adamw_multi_kernel", __FILE__, __LINE__);
+  return DTMI_OK;
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_bucket_flatten(int dtype, void* dst, const void* const* srcs, const int64_t* counts, int nsrc) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(nsrc >= 0, "dtmi_bucket_flatten: negative source count");
+  if (nsrc == 0) return DTMI_OK;
+  DTMI_CHECK(dst && srcs && counts, "dtmi_bucket_flatten: NULL argument");
+  const size_t es = dtype == DTMI_F32 ? 4 : 8;
+  std::vector<FlatEntry> tab;
+  tab.reserve(nsrc);
+  int64_t off = 0, chunks = 0;
+  double bytes = 0;
+  for (int i = 0; i < nsrc; ++i) {
+    DTMI_CHECK(counts[i] >= 0, "dtmi_bucket_flatten: source %d has negative size", i);
+    if (counts[i] > 0) {
+      char* d = static_cast<char*>(dst) + off * es;
+      bool vec = aligned(d, 16) && (srcs[i] == nullptr || aligned(srcs[i], 16));
+      tab.push_back(FlatEntry{srcs[i], counts[i], off, chunks, vec ? 1 : 0});
+      chunks += cdiv(counts[i], kChunk);
+      bytes += (srcs[i] ? 2.0 : 1.0) * (double)counts[i] * es;
+    }
+    off += counts[i];
+  }
+  if (tab.empty()) return DTMI_OK;
+  DTMI_CHECK(chunks < (int64_t)1 << 31, "dtmi_bucket_flatten: too many chunks");
+  void* dtab = nullptr;
+  int rc = upload_table(tab.data(), tab.size() * sizeof(FlatEntry), &dtab);
+  if (rc) return rc;
+  {
+    TimedLaunch tl(DTMI_FAM_FLATTEN, bytes);
+    if (dtype == DTMI_F32)
+      flatten_kernel<float><<<(unsigned)chunks, 256, 0, stream()>>>((float*)dst, (const FlatEntry*)dtab,
+                                                                    (int)tab.size());
+    else
+      flatten_kernel<double><<<(unsigned)chunks, 256, 0, stream()>>>((double*)dst, (const FlatEntry*)dtab,
+                                                                     (int)tab.size());
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(dtab);
+  if (le != hipSuccess) return fail_hip(le, "flatten_kernel", __FILE__, __LINE__);
+  return DTMI_OK;
+  DTMI_BODY_END
+}
+
+template <typename T>
+static int launch_average(void* out, const void* rep, int world, int64_t n, int64_t stride, double inv_w,
+                          double* partials) {
+  bool vec = aligned(out, 16) && aligned(rep, 16) && ((stride * (int64_t)sizeof(T)) % 16 == 0);
+  int grid = average_grid(n);
+  TimedLaunch tl(DTMI_FAM_BUCKET_AVG, (double)(world + 1) * (double)n * sizeof(T));
+  T inv = (T)inv_w;
+  if (vec) {
+    if (partials)
+      bucket_average_kernel<T, true, true><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride, inv,
+                                                                       partials);
+    else
+      bucket_average_kernel<T, true, false><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride,
+                                                                        inv, partials);
+  } else {
+    if (partials)
+      bucket_average_kernel<T, false, true><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride, inv,
+                                                                        partials);
+    else
+      bucket_average_kernel<T, false, false><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride,
+                                                                         inv, partials);
+  }
+  LAUNCH_CHECK("bucket_average_kernel");
+  return DTMI_OK;
+}
+
+DTMI_EXPORT int dtmi_bucket_average(int dtype, void* out, const void* replicas, int world, int64_t n,
+                                    int64_t replica_stride, double inv_w, double* sumsq_partials, int64_t* nblocks) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(n >= 0, "dtmi_bucket_average: negative size");
+  if (nblocks) *nblocks = n > 0 ? average_grid(n) : 0;
+  if (sumsq_partials == nullptr && nblocks != nullptr && out == nullptr) return DTMI_OK;  // size query
+  if (n == 0) return DTMI_OK;
+  DTMI_CHECK(world >= 1, "dtmi_bucket_average: world must be >= 1 (got %d)", world);
+  DTMI_CHECK(out && replicas, "dtmi_bucket_average: NULL pointer");
+  DTMI_CHECK(world == 1 || replica_stride >= n, "dtmi_bucket_average: replica_stride %lld < n %lld",
+             (long long)replica_stride, (long long)n);
+  if (dtype == DTMI_F32) return launch_average<float>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials);
+  return launch_average<double>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_sumsq(int dtype, const void* const* ptrs, const int64_t* counts, int nt, double* out_dev) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(out_dev != nullptr, "dtmi_sumsq: NULL output");
+  DTMI_CHECK(nt >= 0 && (nt == 0 || (ptrs && counts)), "dtmi_sumsq: bad table");
+  const size_t es = dtype == DTMI_F32 ? 4 : 8;
+  std::vector<SumsqEntry> tab;
+  int64_t chunks = 0;
+  double bytes = 0;
+  for (int i = 0; i < nt; ++i) {
+    DTMI_CHECK(counts[i] >= 0, "dtmi_sumsq: tensor %d has negative size", i);
+    if (ptrs[i] == nullptr || counts[i] == 0) continue;
+    tab.push_back(SumsqEntry{ptrs[i], counts[i], chunks, aligned(ptrs[i], 16) ? 1 : 0});
+    chunks += cdiv(counts[i], kChunk);
+    bytes += (double)counts[i] * es;
+  }
+  if (tab.empty()) {
+    // empty sum = 0.0
+    double zero = 0.0;
+    return dtmi_memcpy_h2d(out_dev, &zero, sizeof(double));
+  }
+  DTMI_CHECK(chunks < (int64_t)1 << 31, "dtmi_sumsq: too many chunks");
+  void* dtab = nullptr;
+  int rc = upload_table(tab.data(), tab.size() * sizeof(SumsqEntry), &dtab);
+  if (rc) return rc;
+  void* parts = nullptr;
+  rc = pool_alloc(&parts, (size_t)chunks * sizeof(double));
+  if (rc) {
+    pool_free(dtab);
+    return rc;
+  }
+  {
+    TimedLaunch tl(DTMI_FAM_SUMSQ, bytes);
+    if (dtype == DTMI_F32)
+      sumsq_multi_kernel<float><<<(unsigned)chunks, 256, 0, stream()>>>((const SumsqEntry*)dtab, (int)tab.size(),
+                                                                        (double*)parts);
+    else
+      sumsq_multi_kernel<double><<<(unsigned)chunks, 256, 0, stream()>>>((const SumsqEntry*)dtab, (int)tab.size(),
+                                                                         (double*)parts);
+    sumsq_finish_kernel<<<1, 1024, 0, stream()>>>((const double*)parts, chunks, out_dev, 0);
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(dtab);
+  pool_free(parts);
+  if (le != hipSuccess) return fail_hip(le, "sumsq kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_sumsq_finish(const double* partials, int64_t count, double* out_dev, int accumulate) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_CHECK(out_dev != nullptr, "dtmi_sumsq_finish: NULL output");
+  DTMI_CHECK(count >= 0 && (count == 0 || partials), "dtmi_sumsq_finish: bad partials");
+  TimedLaunch tl(DTMI_FAM_SUMSQ, (double)count * 8);
+  sumsq_finish_kernel<<<1, 1024, 0, stream()>>>(partials, count, out_dev, accumulate);
+  LAUNCH_CHECK("sumsq_finish_kernel");
+  return DTMI_OK;
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_clip_scale(const double* sumsq_dev, double max_norm, double* scale_dev, double* norm_dev) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_CHECK(sumsq_dev && scale_dev, "dtmi_clip_scale: NULL pointer");
+  clip_scale_kernel<<<1, 1, 0, stream()>>>(sumsq_dev, max_norm, scale_dev, norm_dev);
+  LAUNCH_CHECK("clip_scale_kernel");
+  return DTMI_OK;
+  DTMI_BODY_END
+}

@@ -1,0 +1,253 @@
+"""Typed wrappers: DeviceArray arguments in, libdtmi launches out.
+
+Each function checks shapes/dtypes on the host (so a mismatched launch never
+reaches the GPU), then calls the C ABI with raw device pointers. Outputs are
+allocated here unless passed in.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from .device import DeviceArray, empty
+
+_c = _lib.call
+
+
+def _dt(*arrays: DeviceArray) -> int:
+    d = arrays[0].dtype
+    for a in arrays[1:]:
+        if a.dtype != d:
+            raise TypeError(f"dtype mismatch: {d} vs {a.dtype}")
+    return _lib.dtype_code(d)
+
+
+def _contig(*arrays: DeviceArray):
+    for a in arrays:
+        if not a.is_contiguous:
+            raise ValueError("kernel operand must be contiguous")
+
+
+def _shape_arr(shape):
+    return _lib.i64_array(shape)
+
+
+# ------------------------------------------------------------- fills/copies
+def fill(x: DeviceArray, value: float):
+    if x.is_contiguous:
+        _c("dtmi_fill", _lib.dtype_code(x.dtype), x.ptr, float(value), x.size)
+    else:
+        tmp = empty(x.shape, x.dtype)
+        _c("dtmi_fill", _lib.dtype_code(x.dtype), tmp.ptr, float(value), tmp.size)
+        copy_into(x, tmp)
+
+
+def copy_into(dst: DeviceArray, src: DeviceArray):
+    if dst.shape != src.shape:
+        raise ValueError(f"copy shape mismatch {src.shape} -> {dst.shape}")
+    if dst.dtype != src.dtype:
+        raise TypeError("copy dtype mismatch")
+    if src.size == 0:
+        return
+    if dst.is_contiguous and src.is_contiguous:
+        _c("dtmi_memcpy_d2d", dst.ptr, src.ptr, dst.nbytes)
+        return
+    if dst.dtype not in (np.float32, np.float64):
+        raise TypeError("strided copies support float32/float64")
+    nd = dst.ndim
+    _c("dtmi_copy_strided", _lib.dtype_code(dst.dtype), dst.ptr, _shape_arr(dst.strides), src.ptr,
+       _shape_arr(src.strides), nd, _shape_arr(dst.shape))
+
+
+# --------------------------------------------------------------- binary ops
+_OPS = {"add": 0, "sub": 1, "mul": 2}
+
+
+def broadcast_shape(a, b):
+    return tuple(np.broadcast_shapes(tuple(a), tuple(b)))
+
+
+def _bstrides(x: DeviceArray, shape):
+    """Element strides of x broadcast to `shape` (0 on broadcast axes)."""
+    nd = len(shape)
+    pad = nd - x.ndim
+    st = []
+    for d in range(nd):
+        if d < pad:
+            st.append(0)
+        else:
+            s = x.shape[d - pad]
+            st.append(0 if (s == 1 and shape[d] != 1) else x.strides[d - pad])
+    return st
+
+
+def binary(op: str, a: DeviceArray, b: DeviceArray, out: DeviceArray | None = None) -> DeviceArray:
+    dt = _dt(a, b)
+    shape = broadcast_shape(a.shape, b.shape)
+    if out is None:
+        out = empty(shape, a.dtype)
+    elif out.shape != shape or not out.is_contiguous:
+        raise ValueError("binary: bad output")
+    if out.size == 0:
+        return out
+    if len(shape) == 0:
+        shape_c, sa, sb = (1,), [0], [0]
+    else:
+        shape_c, sa, sb = shape, _bstrides(a, shape), _bstrides(b, shape)
+    _c("dtmi_binary", dt, _OPS[op], out.ptr, a.ptr, _shape_arr(sa), b.ptr, _shape_arr(sb), len(shape_c),
+       _shape_arr(shape_c))
+    return out
+
+
+def scale(x: DeviceArray, alpha: float = 1.0, alpha_dev: DeviceArray | None = None,
+          out: DeviceArray | None = None) -> DeviceArray:
+    _contig(x)
+    if alpha_dev is not None and (alpha_dev.dtype != x.dtype or alpha_dev.size != 1):
+        raise TypeError("scale: device scalar must be a 1-element array of the same dtype")
+    out = out if out is not None else empty(x.shape, x.dtype)
+    _c("dtmi_scale", _dt(x, out), out.ptr, x.ptr, x.size, float(alpha),
+       alpha_dev.ptr if alpha_dev is not None else None)
+    return out
+
+
+def neg(x: DeviceArray) -> DeviceArray:
+    return scale(x.contiguous(), -1.0)
+
+
+# ---------------------------------------------------------- activations
+def gelu_fwd(x: DeviceArray) -> DeviceArray:
+    _contig(x)
+    y = empty(x.shape, x.dtype)
+    _c("dtmi_gelu_fwd", _dt(x), y.ptr, x.ptr, x.size)
+    return y
+
+
+def gelu_bwd(x: DeviceArray, dy: DeviceArray) -> DeviceArray:
+    _contig(x, dy)
+    if x.shape != dy.shape:
+        raise ValueError("gelu_bwd shape mismatch")
+    dx = empty(x.shape, x.dtype)
+    _c("dtmi_gelu_bwd", _dt(x, dy), dx.ptr, x.ptr, dy.ptr, x.size)
+    return dx
+
+
+def relu_fwd(x: DeviceArray) -> DeviceArray:
+    _contig(x)
+    y = empty(x.shape, x.dtype)
+    _c("dtmi_relu_fwd", _dt(x), y.ptr, x.ptr, x.size)
+    return y
+
+
+def relu_bwd(x: DeviceArray, dy: DeviceArray) -> DeviceArray:
+    _contig(x, dy)
+    dx = empty(x.shape, x.dtype)
+    _c("dtmi_relu_bwd", _dt(x, dy), dx.ptr, x.ptr, dy.ptr, x.size)
+    return dx
+
+
+# ------------------------------------------------------------- reductions
+def reduce_sum(x: DeviceArray, axes, keepdims=False) -> DeviceArray:
+    axes = sorted({a % x.ndim for a in axes}) if x.ndim else []
+    kept = [s for d, s in enumerate(x.shape) if d not in axes]
+    out = empty(tuple(kept), x.dtype)
+    if out.size == 0:
+        pass
+    elif x.ndim == 0:
+        _c("dtmi_memcpy_d2d", out.ptr, x.ptr, x.nbytes)
+    else:
+        mask = (C.c_int * x.ndim)(*[1 if d in axes else 0 for d in range(x.ndim)])
+        _c("dtmi_reduce_sum", _dt(x), out.ptr, x.ptr, _shape_arr(x.strides), x.ndim, _shape_arr(x.shape), mask)
+    if keepdims:
+        out = out.reshape(tuple(1 if d in axes else s for d, s in enumerate(x.shape)))
+    return out
+
+
+def colsum(x2d: DeviceArray, out: DeviceArray | None = None, accumulate=False) -> DeviceArray:
+    _contig(x2d)
+    rows, cols = x2d.shape
+    out = out if out is not None else empty((cols,), x2d.dtype)
+    _c("dtmi_colsum", _dt(x2d, out), out.ptr, x2d.ptr, rows, cols, 1 if accumulate else 0)
+    return out
+
+
+# ------------------------------------------------------ optimizer / buckets
+def adamw(p, g, m, v, lr, b1, b2, eps, wd, b1t, b2t, gscale=1.0, gscale_dev=None):
+    _contig(p, g, m, v)
+    if not (p.size == g.size == m.size == v.size):
+        raise ValueError("adamw: size mismatch")
+    _c("dtmi_adamw", _dt(p, g, m, v), p.ptr, g.ptr, m.ptr, v.ptr, p.size, float(lr), float(b1), float(b2),
+       float(eps), float(wd), float(1 - b1), float(1 - b2), float(b1t), float(b2t), float(gscale),
+       gscale_dev.ptr if gscale_dev is not None else None)
+
+
+def adamw_multi(ps, gs, ms, vs, lr, b1, b2, eps, wd, b1t, b2t, gscale=1.0, gscale_dev=None):
+    if not ps:
+        return
+    dt = _dt(*ps)
+    for p, g, m, v in zip(ps, gs, ms, vs):
+        _contig(p, m, v)
+        if g is not None:
+            _contig(g)
+            if g.dtype != p.dtype or g.size != p.size or m.size != p.size or v.size != p.size:
+                raise ValueError("adamw_multi: size/dtype mismatch")
+    n = len(ps)
+    _c("dtmi_adamw_multi", dt, n, _lib.ptr_array([p.ptr for p in ps]),
+       _lib.ptr_array([g.ptr if g is not None else 0 for g in gs]), _lib.ptr_array([m.ptr for m in ms]),
+       _lib.ptr_array([v.ptr for v in vs]), _lib.i64_array([p.size for p in ps]), float(lr), float(b1), float(b2),
+       float(eps), float(wd), float(1 - b1), float(1 - b2), float(b1t), float(b2t), float(gscale),
+       gscale_dev.ptr if gscale_dev is not None else None)
+
+
+def bucket_flatten(dst: DeviceArray, srcs, counts):
+    """srcs: DeviceArray or None (zeros) per slot; written back to back into dst."""
+    _contig(dst)
+    if sum(counts) > dst.size:
+        raise ValueError("bucket_flatten: sources exceed destination")
+    for s, n in zip(srcs, counts):
+        if s is not None:
+            _contig(s)
+            if s.size != n or s.dtype != dst.dtype:
+                raise ValueError("bucket_flatten: source size/dtype mismatch")
+    _c("dtmi_bucket_flatten", _lib.dtype_code(dst.dtype), dst.ptr,
+       _lib.ptr_array([s.ptr if s is not None else 0 for s in srcs]), _lib.i64_array(counts), len(counts))
+
+
+def average_blocks(n: int) -> int:
+    nb = C.c_int64()
+    _c("dtmi_bucket_average", 0, None, None, 1, int(n), int(n), 1.0, None, C.byref(nb))
+    return nb.value
+
+
+def bucket_average(out: DeviceArray, replicas: DeviceArray, world: int, inv_w: float,
+                   partials: DeviceArray | None = None):
+    """out[i] = fixed rank-order sum of replicas[r, i] times inv_w; replicas is [W, n]."""
+    _contig(out, replicas)
+    if replicas.ndim != 2 or replicas.shape[0] != world or replicas.shape[1] != out.size:
+        raise ValueError("bucket_average: replicas must be [world, n]")
+    if partials is not None and (partials.dtype != np.float64 or partials.size < average_blocks(out.size)):
+        raise ValueError("bucket_average: partials too small")
+    _c("dtmi_bucket_average", _dt(out, replicas), out.ptr, replicas.ptr, int(world), out.size, replicas.shape[1],
+       float(inv_w), partials.ptr if partials is not None else None, None)
+
+
+def sumsq(arrays, out: DeviceArray):
+    """f64 sum of squares of every array into the 1-element float64 `out`."""
+    arrays = [a for a in arrays if a is not None]
+    if out.dtype != np.float64 or out.size != 1:
+        raise TypeError("sumsq output must be a 1-element float64 array")
+    dt = _dt(*arrays) if arrays else 0
+    for a in arrays:
+        _contig(a)
+    _c("dtmi_sumsq", dt, _lib.ptr_array([a.ptr for a in arrays]), _lib.i64_array([a.size for a in arrays]),
+       len(arrays), out.ptr)
+
+
+def sumsq_finish(partials: DeviceArray, count: int, out: DeviceArray, accumulate=False):
+    _c("dtmi_sumsq_finish", partials.ptr, int(count), out.ptr, 1 if accumulate else 0)
+
+
+def clip_scale(sumsq_dev: DeviceArray, max_norm: float, scale_out: DeviceArray, norm_out: DeviceArray | None = None):
+    _c("dtmi_clip_scale", sumsq_dev.ptr, float(max_norm), scale_out.ptr,
+       norm_out.ptr if norm_out is not None else None)

@@ -1,0 +1,194 @@
+/*
+ * libdtmi — C ABI of the MI355X (gfx950) backward / gradient / optimizer path
+ * that stands in for dtrain's NumPy arithmetic.
+ *
+ * dtrain (siddhaantxsingh/DISTRIBUTED-TRAINING) is pure Python over NumPy and has
+ * no FFI of its own; every function below replaces the NumPy expression(s) cited
+ * next to it (paths relative to the dtrain source tree). The Python host package
+ * `dtmi` binds these with ctypes and keeps dtrain's Python API on top.
+ *
+ * Conventions
+ *   - Every function returns int status: 0 = ok, otherwise a DTMI_ERR_* code;
+ *     dtmi_last_error() returns the (thread-local) message of the last failure.
+ *   - dtype is DTMI_F32 or DTMI_F64. Pointers are device addresses (a buffer
+ *     base plus a byte offset, so views and shards are plain pointers); sizes
+ *     are int64_t element counts; arrays are row-major and contiguous unless a
+ *     stride argument says otherwise.
+ *   - Scalar hyper-parameters are passed as double, computed on the host the
+ *     way dtrain computes them; F32 kernels round them to float first (NumPy 2
+ *     treats Python floats as weak scalars of the array's dtype).
+ *   - All work is enqueued on one library HIP stream, asynchronously. Errors of
+ *     an asynchronous kernel surface at the next dtmi_sync / copy to host.
+ *   - Reductions are deterministic: fixed grids, fixed combination order, no
+ *     floating-point atomics. Same inputs give the same bits on every run.
+ */
+#ifndef DTMI_H
+#define DTMI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DTMI_F32 0
+#define DTMI_F64 1
+
+#define DTMI_OK 0
+#define DTMI_ERR_INVALID 1
+#define DTMI_ERR_HIP 2
+#define DTMI_ERR_OOM 3
+#define DTMI_ERR_NOT_INITIALIZED 4
+#define DTMI_ERR_INTERNAL 5
+
+/* ------------------------------------------------------------------ runtime
+ * Replaces: NumPy array allocation / np.zeros_like / .copy() behind
+ * dtrain/autograd.py:43 (Tensor.data) and dtrain/autograd.py:181 (leaf .grad).
+ */
+const char* dtmi_last_error(void);
+int dtmi_init(int device);                       /* select device, create the stream */
+int dtmi_device_info(int* num_cus, size_t* hbm_bytes, char* name, int name_len);
+int dtmi_malloc(void** ptr, size_t bytes);       /* pooled hipMalloc, 256-byte aligned */
+int dtmi_free(void* ptr);                        /* back to the pool (stream ordered) */
+int dtmi_empty_cache(void);                      /* release pooled blocks to HIP */
+int dtmi_memory_stats(size_t* in_use, size_t* cached, size_t* peak);
+int dtmi_memcpy_h2d(void* dst, const void* src, size_t bytes);   /* via pinned staging, async */
+int dtmi_memcpy_d2h(void* dst, const void* src, size_t bytes);   /* synchronous */
+int dtmi_memcpy_d2d(void* dst, const void* src, size_t bytes);
+int dtmi_fill(int dtype, void* x, double value, int64_t n);      /* fill kernel (no hipMemset) */
+int dtmi_zero_bytes(void* x, size_t bytes);
+int dtmi_sync(void);
+
+/* Timing: events on the library stream. */
+int dtmi_event_create(void** ev);
+int dtmi_event_record(void* ev);
+int dtmi_event_elapsed_ms(void* start, void* stop, float* ms);   /* waits for stop */
+int dtmi_event_destroy(void* ev);
+
+/* Per-kernel-family timing of every launch while enabled (HIP events around
+ * each launch on the library stream). Families are DTMI_FAM_*. */
+#define DTMI_FAM_GEMM 0
+#define DTMI_FAM_ATTN_FWD 1
+#define DTMI_FAM_ATTN_BWD 2
+#define DTMI_FAM_ADAMW 3
+#define DTMI_FAM_BUCKET_AVG 4
+#define DTMI_FAM_LN_BWD 5
+#define DTMI_FAM_GELU_BWD 6
+#define DTMI_FAM_XENT 7
+#define DTMI_FAM_SUMSQ 8
+#define DTMI_FAM_FLATTEN 9
+#define DTMI_FAM_OTHER 10
+#define DTMI_FAM_COUNT 11
+int dtmi_timing_enable(int enable);              /* enabling clears the counters */
+int dtmi_timing_read(int family, int64_t* launches, double* ms, double* work);
+
+/* ---------------------------------------------------- optimizer / gradient path */
+
+/* Fused AdamW over one flat buffer: one pass reads p, g, m, v and writes p, m, v.
+ * Replaces dtrain/optim.py:21-33 (AdamW.step) for one array, including the
+ * gradient pre-scale `p.grad * s` of dtrain/train.py:159 (gscale, 1.0 = none).
+ * The operation order is exactly optim.py:28-33 and the library is built with
+ * -ffp-contract=off, so F64 results are bit-identical to NumPy's.
+ * c1 = 1 - b1 and c2 = 1 - b2 as Python computes them; b1t = 1 - b1**t and
+ * b2t = 1 - b2**t with t already incremented (optim.py:22-24).
+ * gscale_dev, when not NULL, points at a device double that replaces gscale
+ * (the clip factor computed on the device by dtmi_clip_scale). */
+int dtmi_adamw(int dtype, void* p, const void* g, void* m, void* v, int64_t n,
+               double lr, double b1, double b2, double eps, double wd,
+               double c1, double c2, double b1t, double b2t,
+               double gscale, const double* gscale_dev);
+
+/* Multi-tensor AdamW: the same update over `ntensors` (p, g, m, v, n) tuples in
+ * one launch (dtrain/optim.py:25-33 iterates these in a Python loop). Tensors
+ * with g == NULL are skipped (optim.py:26-27). Pointer arrays live on the host. */
+int dtmi_adamw_multi(int dtype, int ntensors, void* const* p, const void* const* g,
+                     void* const* m, void* const* v, const int64_t* n,
+                     double lr, double b1, double b2, double eps, double wd,
+                     double c1, double c2, double b1t, double b2t,
+                     double gscale, const double* gscale_dev);
+
+/* Bucket flatten: copy `nsrc` contiguous gradients back to back into dst.
+ * Replaces the hook copy `b.buf[off:off+n] = p.grad.reshape(-1)` of
+ * dtrain/ddp.py:73-81 (one launch per completed bucket instead of one copy per
+ * parameter) and the ZeRO flatten of dtrain/zero.py:46-53. A NULL source
+ * writes zeros (ddp.py:88-94, zero.py:49-50). */
+int dtmi_bucket_flatten(int dtype, void* dst, const void* const* srcs, const int64_t* counts, int nsrc);
+
+/* Fixed-order average of W replica rows of one bucket:
+ *   out[i] = (((rep[0][i] + rep[1][i]) + rep[2][i]) + ...) * inv_w
+ * rep[r] = replicas + r * replica_stride (elements). Replaces the direct
+ * all-reduce order of dtrain/comm.py:374-391 (rank 0 first, then 1, 2, ...)
+ * followed by `b.buf *= 1.0 / world` of dtrain/ddp.py:104-106 (and `g *= 1/W`
+ * of dtrain/zero.py:55). Bit-exact to NumPy in F64 and F32.
+ * If sumsq_partials is not NULL the kernel also writes one double per block
+ * (the block's sum of out[i]^2, f64 accumulation) for dtmi_sumsq_finish; the
+ * number of blocks is returned in *nblocks (call with sumsq_partials == NULL
+ * and nblocks != NULL to query it first). */
+int dtmi_bucket_average(int dtype, void* out, const void* replicas, int world, int64_t n,
+                        int64_t replica_stride, double inv_w, double* sumsq_partials, int64_t* nblocks);
+
+/* Deterministic sum of squares in f64 over `nt` tensors, two-stage (per-block
+ * partials in a fixed grid, then one fixed-order pass). Replaces
+ * sum(float(np.dot(g64, g64)) for each grad) of dtrain/train.py:155-156 and
+ * dtrain/zero.py:56. The result is written to the device double *out_dev. */
+int dtmi_sumsq(int dtype, const void* const* ptrs, const int64_t* counts, int nt, double* out_dev);
+
+/* Final fixed-order pass over `count` per-block partials (from
+ * dtmi_bucket_average), accumulated onto *out_dev if accumulate != 0. */
+int dtmi_sumsq_finish(const double* partials, int64_t count, double* out_dev, int accumulate);
+
+/* Clip factor on the device from a device sum of squares, exactly
+ * dtrain/optim.py:49-52: n = sqrt(sq); 1.0 if n <= max_norm or n == 0 else
+ * max_norm / (n + 1e-6). Writes *scale_dev (double) and *norm_dev (may be NULL). */
+int dtmi_clip_scale(const double* sumsq_dev, double max_norm, double* scale_dev, double* norm_dev);
+
+/* ------------------------------------------------------- generic tensor ops
+ * Behind dtrain's Tensor operators (dtrain/autograd.py:76-148) and views.
+ */
+
+/* dst = src element by element over `shape` (ndim <= 8); element strides for
+ * either side, NULL = contiguous. Materialises reshape/transpose of strided
+ * views (dtrain/autograd.py:124-131 return NumPy views that later ops copy). */
+int dtmi_copy_strided(int dtype, void* dst, const int64_t* dst_strides, const void* src,
+                      const int64_t* src_strides, int ndim, const int64_t* shape);
+
+/* out (contiguous, `shape`) = a OP b, OP: 0 add, 1 sub, 2 mul; element strides
+ * of a and b over `shape` (0 on broadcast axes, NULL = contiguous).
+ * dtrain/autograd.py:76-98 (NumPy broadcasting of a + b, a - b, a * b). */
+#define DTMI_OP_ADD 0
+#define DTMI_OP_SUB 1
+#define DTMI_OP_MUL 2
+int dtmi_binary(int dtype, int op, void* out, const void* a, const int64_t* a_strides, const void* b,
+                const int64_t* b_strides, int ndim, const int64_t* shape);
+
+/* out = x * alpha (alpha_dev, when not NULL, points at a device scalar of
+ * dtype that replaces alpha). The loss scaling `loss * (1.0 / n_micro)` of
+ * dtrain/train.py:138 and its backward (autograd.py:96-97). */
+int dtmi_scale(int dtype, void* out, const void* x, int64_t n, double alpha, const void* alpha_dev);
+
+/* tanh-GELU forward and backward, dtrain/autograd.py:133-144 (same formula and
+ * operation order; tanh recomputed in the backward instead of saved). */
+int dtmi_gelu_fwd(int dtype, void* y, const void* x, int64_t n);
+int dtmi_gelu_bwd(int dtype, void* dx, const void* x, const void* dy, int64_t n);
+
+/* ReLU forward / backward, dtrain/autograd.py:146-148. */
+int dtmi_relu_fwd(int dtype, void* y, const void* x, int64_t n);
+int dtmi_relu_bwd(int dtype, void* dx, const void* x, const void* dy, int64_t n);
+
+/* Sum over the axes with reduce_mask[d] != 0 (kept axes in order into
+ * contiguous out): Tensor.sum and _unbroadcast, dtrain/autograd.py:29-36, 111-117. */
+int dtmi_reduce_sum(int dtype, void* out, const void* x, const int64_t* strides, int ndim,
+                    const int64_t* shape, const int* reduce_mask);
+
+/* Column sums of a row-major [rows, cols] matrix, deterministic two-stage
+ * (64-row partials, then a fixed-order pass). The bias gradient
+ * _unbroadcast(g, (N,)) of dtrain/autograd.py:29-36 for y = x @ w + b.
+ * accumulate != 0 adds onto out. */
+int dtmi_colsum(int dtype, void* out, const void* x, int64_t rows, int64_t cols, int accumulate);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DTMI_H */
