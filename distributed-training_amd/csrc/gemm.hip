@@ -1,0 +1,438 @@
+// Dense contractions on the MFMA matrix cores: C = sum_k A(m,k) B(k,n) (+ bias)
+// in float32 (v_mfma_f32_32x32x2_f32) and float64 (v_mfma_f64_16x16x4_f64).
+//
+// Behind dtrain's matmul node (dtrain/autograd.py:102-109) and Linear
+// (dtrain/nn.py:58-65): forward Y = X W (+ b), dX = dY W^T, dW = X^T dY.
+// Row-major operands in either orientation:
+//   A "KC": A(m,k) = A[m*lda + k]  (X, dY)      A "MC": A(m,k) = A[k*lda + m]  (X^T)
+//   B "NC": B(k,n) = B[k*ldb + n]  (W, dY)      B "KC": B(k,n) = B[n*ldb + k]  (W^T)
+//
+// Tiling. 256 threads = 4 waves in a 2x2 grid; block tile 128x128, k-tile 16
+// floats or 8 doubles, wave tile 64x64 (2x2 MFMA tiles of 32x32 in float32, 4x4 of 16x16 in
+// float64). Each operand tile is staged in LDS in its global orientation
+// (global -> LDS is a straight 16-byte vector copy, fully coalesced along the
+// contiguous dimension), double-buffered with one barrier per k-tile and the
+// next tile's global loads in flight during the MFMAs.
+//
+// MFMA k-slots. An MFMA takes k in lane groups g = lane / MT (2 groups of 32
+// lanes for 32x32x2, 4 groups of 16 for 16x16x4). Within each 8-wide k chunk,
+// step s of group g uses k = chunk + VEC*g + s (VEC = 4 floats or 2 doubles),
+// the same permutation for A and B (a permutation of the reduction index does
+// not change the sum's terms). With it a k-contiguous LDS tile gives a lane
+// its VEC k-values with one 16-byte ds_read, and an mn-contiguous LDS tile is
+// read with conflict-free 4/8-byte reads (row pads chosen so the lane groups
+// fall in different LDS banks).
+//
+// Grid. Tiles are enumerated group-of-8-rows first (L2 reuse of B panels) and
+// the linear block index is remapped so each of the 8 XCDs (blocks are dealt
+// to XCDs round-robin) works on a contiguous range of tiles and shares its L2.
+// Small tile counts with long K are split along K; the split partials are
+// summed in split order by a second kernel (deterministic, no atomics).
+#include "common.h"
+
+namespace dtmi {
+
+template <typename T>
+struct MF;
+
+template <>
+struct MF<float> {
+  static constexpr int MT = 32, G = 2, VEC = 4, NACC = 16;
+  typedef float acc_t __attribute__((ext_vector_type(16)));
+  typedef float vec_t __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ acc_t mma(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  // result register i of lane group g holds row (8*(i/4) + 4*g + i%4), column lane%32
+  static __device__ __forceinline__ int row(int i, int g) { return 8 * (i / 4) + 4 * g + (i % 4); }
+};
+
+template <>
+struct MF<double> {
+  static constexpr int MT = 16, G = 4, VEC = 2, NACC = 4;
+  typedef double acc_t __attribute__((ext_vector_type(4)));
+  typedef double vec_t __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ acc_t mma(double a, double b, acc_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  // result register i of lane group g holds row (g + 4*i), column lane%16
+  static __device__ __forceinline__ int row(int i, int g) { return g + 4 * i; }
+};
+
+struct GemmArgs {
+  const void* A;
+  const void* B;
+  void* C;
+  const void* bias;
+  void* ws;  // split-K partials [splits][batch][M][N] (NULL when not split)
+  int64_t M, N, K, lda, ldb, ldc;
+  int64_t sA, sB, sC;  // batch strides (elements)
+  int64_t k_per_split;
+  int tiles_m, tiles_n;
+  int accumulate;
+};
+
+constexpr int kBM = 128, kBN = 128, kKC = 8;
+// k-tile: 16 floats or 8 doubles (the float64 double-buffered tiles then fit 40 KB of LDS)
+template <typename T>
+constexpr int kBKT = sizeof(T) == 4 ? 16 : 8;
+
+template <typename T, bool KCONTIG>
+struct TileLayout {
+  static constexpr int VEC = MF<T>::VEC;
+  static constexpr int kBK = kBKT<T>;
+  // k-contiguous: [mn][kBK + VEC]; mn-contiguous: [kBK][128 + 8]
+  static constexpr int STRIDE = KCONTIG ? (kBK + VEC) : (128 + 8);
+  static constexpr int SIZE = KCONTIG ? 128 * STRIDE : kBK * STRIDE;
+  static constexpr int NVEC = 128 * kBK / VEC / 256;  // 16-byte vectors per thread per tile
+};
+
+template <typename T, bool KCONTIG>
+struct TileRegs {
+  typename MF<T>::vec_t v[TileLayout<T, KCONTIG>::NVEC];
+};
+
+// Global -> registers for one 128 x kBK operand tile (mn0 = first row/col of
+// the tile along M or N, k0 = first k). Out-of-range elements read as 0.
+template <typename T, bool KCONTIG, bool VECLD>
+__device__ __forceinline__ void load_tile(TileRegs<T, KCONTIG>& r, const T* __restrict__ P, int64_t ld, int64_t mn0, int64_t MN, int64_t k0,
+                                          int64_t kend) {
+  using L = TileLayout<T, KCONTIG>;
+  constexpr int VEC = L::VEC;
+  constexpr int kBK = L::kBK;
+#pragma unroll
+  for (int i = 0; i < L::NVEC; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    int64_t mn, k;
+    if (KCONTIG) {
+      mn = mn0 + f / (kBK / VEC);
+      k = k0 + (f % (kBK / VEC)) * VEC;
+    } else {
+      k = k0 + f / (128 / VEC);
+      mn = mn0 + (f % (128 / VEC)) * VEC;
+    }
+    if (VECLD) {
+      // every dimension that vectors run along is a multiple of VEC
+      if (mn < MN && k < kend) {
+        const T* src = KCONTIG ? P + mn * ld + k : P + k * ld + mn;
+        r.v[i] = *reinterpret_cast<const typename MF<T>::vec_t*>(src);
+      } else {
+        r.v[i] = typename MF<T>::vec_t(0);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        int64_t mm = KCONTIG ? mn : mn + e;
+        int64_t kk = KCONTIG ? k + e : k;
+        r.v[i][e] = (mm < MN && kk < kend) ? (KCONTIG ? P[mm * ld + kk] : P[kk * ld + mm]) : T(0);
+      }
+    }
+  }
+}
+
+template <typename T, bool KCONTIG>
+__device__ __forceinline__ void store_tile(T* __restrict__ lds, const TileRegs<T, KCONTIG>& r) {
+  using L = TileLayout<T, KCONTIG>;
+  constexpr int VEC = L::VEC;
+  constexpr int kBK = L::kBK;
+#pragma unroll
+  for (int i = 0; i < L::NVEC; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    int off;
+    if (KCONTIG)
+      off = (f / (kBK / VEC)) * L::STRIDE + (f % (kBK / VEC)) * VEC;
+    else
+      off = (f / (128 / VEC)) * L::STRIDE + (f % (128 / VEC)) * VEC;
+    *reinterpret_cast<typename MF<T>::vec_t*>(lds + off) = r.v[i];
+  }
+}
+
+// The VEC k-values lane (group g, position c) feeds for operand rows/cols
+// `base + c` at chunk `kk`.
+template <typename T, bool KCONTIG>
+__device__ __forceinline__ typename MF<T>::vec_t read_frag(const T* __restrict__ lds, int base, int kk, int g, int c) {
+  using L = TileLayout<T, KCONTIG>;
+  constexpr int VEC = L::VEC;
+  typename MF<T>::vec_t v;
+  if (KCONTIG) {
+    v = *reinterpret_cast<const typename MF<T>::vec_t*>(lds + (base + c) * L::STRIDE + kk + VEC * g);
+  } else {
+#pragma unroll
+    for (int s = 0; s < VEC; ++s) v[s] = lds[(kk + VEC * g + s) * L::STRIDE + base + c];
+  }
+  return v;
+}
+
+__device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn) {
+  const int nt = a.tiles_m * a.tiles_n;
+  int t = blockIdx.x;
+  if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);  // contiguous tile range per XCD
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * a.tiles_n;
+  const int group = t / per_group;
+  const int first_m = group * GROUP;
+  const int gsz = a.tiles_m - first_m < GROUP ? a.tiles_m - first_m : GROUP;
+  const int r = t - group * per_group;
+  tm = first_m + r % gsz;
+  tn = r / gsz;
+}
+
+template <typename T, bool AKC, bool BKC, bool VECA, bool VECB>
+__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
+  constexpr int kBK = kBKT<T>;
+  using MFT = MF<T>;
+  using LA = TileLayout<T, AKC>;
+  using LB = TileLayout<T, BKC>;
+  constexpr int MT = MFT::MT, VEC = MFT::VEC, NACC = MFT::NACC;
+  constexpr int TM = 64 / MT, TN = 64 / MT;
+  __shared__ __attribute__((aligned(16))) T lds[2 * (LA::SIZE + LB::SIZE)];
+
+  int tm, tn;
+  tile_coords(a, tm, tn);
+  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const int split = blockIdx.y;
+  const int64_t batch = blockIdx.z;
+  const int64_t kbeg = (int64_t)split * a.k_per_split;
+  const int64_t kend = kbeg + a.k_per_split < a.K ? kbeg + a.k_per_split : a.K;
+  const T* A = (const T*)a.A + batch * a.sA;
+  const T* B = (const T*)a.B + batch * a.sB;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / MT, c = lane % MT;
+  const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+
+  typename MFT::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = typename MFT::acc_t(0);
+
+  TileRegs<T, AKC> ra;
+  TileRegs<T, BKC> rb;
+  const int64_t ntiles = kend > kbeg ? (kend - kbeg + kBK - 1) / kBK : 0;
+  if (ntiles > 0) {
+    load_tile<T, AKC, VECA>(ra, A, a.lda, m0, a.M, kbeg, kend);
+    load_tile<T, BKC, VECB>(rb, B, a.ldb, n0, a.N, kbeg, kend);
+    store_tile<T, AKC>(lds, ra);
+    store_tile<T, BKC>(lds + 2 * LA::SIZE, rb);
+  }
+  __syncthreads();
+  for (int64_t kt = 0; kt < ntiles; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < ntiles;
+    if (more) {
+      const int64_t k0 = kbeg + (kt + 1) * kBK;
+      load_tile<T, AKC, VECA>(ra, A, a.lda, m0, a.M, k0, kend);
+      load_tile<T, BKC, VECB>(rb, B, a.ldb, n0, a.N, k0, kend);
+    }
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk += kKC) {
+      typename MFT::vec_t fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = read_frag<T, AKC>(lds + cur * LA::SIZE, wm0 + i * MT, kk, g, c);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = read_frag<T, BKC>(lds + 2 * LA::SIZE + cur * LB::SIZE, wn0 + j * MT, kk, g, c);
+#pragma unroll
+      for (int s = 0; s < VEC; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = MFT::mma(fa[i][s], fb[j][s], acc[i][j]);
+    }
+    if (more) {
+      store_tile<T, AKC>(lds + (cur ^ 1) * LA::SIZE, ra);
+      store_tile<T, BKC>(lds + 2 * LA::SIZE + (cur ^ 1) * LB::SIZE, rb);
+    }
+    __syncthreads();
+  }
+
+  // epilogue
+  const bool to_ws = a.ws != nullptr;
+  T* C = to_ws ? (T*)a.ws + ((int64_t)split * gridDim.z + batch) * a.M * a.N : (T*)a.C + batch * a.sC;
+  const int64_t ldc = to_ws ? a.N : a.ldc;
+  const T* bias = (const T*)a.bias;
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t n = n0 + wn0 + j * MT + c;
+      if (n >= a.N) continue;
+      const T bn = (!to_ws && bias) ? bias[n] : T(0);
+#pragma unroll
+      for (int r = 0; r < NACC; ++r) {
+        const int64_t m = m0 + wm0 + i * MT + MFT::row(r, g);
+        if (m >= a.M) continue;
+        T v = acc[i][j][r];
+        if (!to_ws) {
+          if (bias) v = v + bn;
+          if (a.accumulate) v = C[m * ldc + n] + v;
+        }
+        C[m * ldc + n] = v;
+      }
+    }
+}
+
+// C[b][m][n] = (sum over splits in order of ws[s][b][m][n]) (+ bias[n]) (+ C)
+template <typename T>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(T* __restrict__ C, const T* __restrict__ ws,
+                                                             const T* __restrict__ bias, int splits, int64_t batch,
+                                                             int64_t M, int64_t N, int64_t ldc, int64_t sC,
+                                                             int accumulate) {
+  const int64_t total = batch * M * N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+    const int64_t b = idx / (M * N);
+    const int64_t rem = idx - b * M * N;
+    const int64_t m = rem / N, n = rem - (rem / N) * N;
+    T v = ws[idx];
+    for (int s = 1; s < splits; ++s) v = v + ws[(int64_t)s * total + idx];
+    if (bias) v = v + bias[n];
+    T* dst = C + b * sC + m * ldc + n;
+    if (accumulate) v = *dst + v;
+    *dst = v;
+  }
+}
+
+template <typename T, bool AKC, bool BKC>
+static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb) {
+  if (veca && vecb)
+    gemm_kernel<T, AKC, BKC, true, true><<<grid, 256, 0, stream()>>>(a);
+  else if (veca)
+    gemm_kernel<T, AKC, BKC, true, false><<<grid, 256, 0, stream()>>>(a);
+  else if (vecb)
+    gemm_kernel<T, AKC, BKC, false, true><<<grid, 256, 0, stream()>>>(a);
+  else
+    gemm_kernel<T, AKC, BKC, false, false><<<grid, 256, 0, stream()>>>(a);
+}
+
+template <typename T>
+static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int64_t sA,
+                     const void* B, int64_t ldb, int64_t sB, void* C, int64_t ldc, int64_t sC, int64_t batch,
+                     const void* bias, int accumulate, int force_splits) {
+  constexpr int VEC = MF<T>::VEC;
+  GemmArgs a{};
+  a.A = A;
+  a.B = B;
+  a.C = C;
+  a.bias = bias;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = ldc;
+  a.sA = sA;
+  a.sB = sB;
+  a.sC = sC;
+  a.accumulate = accumulate;
+  a.tiles_m = (int)cdiv(M, kBM);
+  a.tiles_n = (int)cdiv(N, kBN);
+  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+  DTMI_CHECK(tiles < (1LL << 31) && batch < 65536, "dtmi_gemm: problem too large");
+  // split K when the tile grid alone cannot fill the GPU
+  int splits = 1;
+  if (force_splits > 0) {
+    splits = force_splits;
+  } else {
+    const int64_t want = 2LL * (num_cus() > 0 ? num_cus() : 256);
+    while (tiles * batch * splits * 2 <= want && K / (splits * 2) >= 512 && splits < 16) splits *= 2;
+  }
+  constexpr int kBK = kBKT<T>;
+  int64_t kps = cdiv(cdiv(K, splits), kBK) * kBK;
+  if (kps < kBK) kps = kBK;
+  splits = (int)cdiv(K > 0 ? K : 1, kps);
+  a.k_per_split = kps;
+  const size_t es = sizeof(T);
+  bool veca = aligned(A, 16) && lda % VEC == 0 && (batch == 1 || sA % VEC == 0) && (akc ? K % VEC == 0 : M % VEC == 0);
+  bool vecb = aligned(B, 16) && ldb % VEC == 0 && (batch == 1 || sB % VEC == 0) && (bkc ? K % VEC == 0 : N % VEC == 0);
+  void* ws = nullptr;
+  if (splits > 1) {
+    int rc = pool_alloc(&ws, (size_t)splits * batch * M * N * es);
+    if (rc) return rc;
+    a.ws = ws;
+  }
+  dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
+  {
+    TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
+    if (akc && bkc)
+      launch_variant<T, true, true>(a, grid, veca, vecb);
+    else if (akc)
+      launch_variant<T, true, false>(a, grid, veca, vecb);
+    else if (bkc)
+      launch_variant<T, false, true>(a, grid, veca, vecb);
+    else
+      launch_variant<T, false, false>(a, grid, veca, vecb);
+    if (splits > 1) {
+      int64_t total = batch * M * N;
+      int rg = (int)(cdiv(total, 256 * 4) < 8192 ? cdiv(total, 256 * 4) : 8192);
+      splitk_reduce_kernel<T><<<rg, 256, 0, stream()>>>((T*)C, (const T*)ws, (const T*)bias, splits, batch, M, N,
+                                                        ldc, sC, accumulate);
+    }
+  }
+  hipError_t le = hipGetLastError();
+  if (ws) pool_free(ws);
+  if (le != hipSuccess) return fail_hip(le, "gemm kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+}
+
+static int gemm_dispatch(int dtype, int akc, int bkc, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                         int64_t sA, const void* B, int64_t ldb, int64_t sB, void* C, int64_t ldc, int64_t sC,
+                         int64_t batch, const void* bias, int accumulate, int force_splits) {
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(M >= 0 && N >= 0 && K >= 0 && batch >= 1, "dtmi_gemm: bad sizes M=%lld N=%lld K=%lld batch=%lld",
+             (long long)M, (long long)N, (long long)K, (long long)batch);
+  if (M == 0 || N == 0) return DTMI_OK;
+  DTMI_CHECK(C != nullptr && (K == 0 || (A && B)), "dtmi_gemm: NULL pointer");
+  DTMI_CHECK(ldc >= N, "dtmi_gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
+  DTMI_CHECK(K == 0 || (akc ? lda >= K : lda >= M), "dtmi_gemm: lda too small");
+  DTMI_CHECK(K == 0 || (bkc ? ldb >= K : ldb >= N), "dtmi_gemm: ldb too small");
+  if (dtype == DTMI_F32)
+    return gemm_impl<float>(akc, bkc, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, batch, bias, accumulate,
+                            force_splits);
+  return gemm_impl<double>(akc, bkc, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, batch, bias, accumulate,
+                           force_splits);
+}
+
+}  // namespace dtmi
+
+using namespace dtmi;
+
+DTMI_EXPORT int dtmi_gemm(int dtype, int a_kcontig, int b_kcontig, int64_t M, int64_t N, int64_t K, const void* A,
+                          int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,
+                          int64_t ldc, int64_t strideC, int64_t batch, const void* bias, int accumulate,
+                          int splits) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  return gemm_dispatch(dtype, a_kcontig ? 1 : 0, b_kcontig ? 1 : 0, M, N, K, A, lda, strideA, B, ldb, strideB, C, ldc,
+                       strideC, batch, bias, accumulate, splits);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_fwd(int dtype, void* Y, const void* X, const void* W, const void* b, int64_t M,
+                                int64_t K, int64_t N) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  return gemm_dispatch(dtype, 1, 0, M, N, K, X, K, 0, W, N, 0, Y, N, 0, 1, b, 0, 0);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_bwd_dx(int dtype, void* dX, const void* dY, const void* W, int64_t M, int64_t K,
+                                   int64_t N, int accumulate) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  // dX[m, k] = sum_n dY[m, n] W[k, n]: A = dY (k-contiguous over n), B(n, k) = W[k, n] (k-contiguous)
+  return gemm_dispatch(dtype, 1, 1, M, K, N, dY, N, 0, W, N, 0, dX, K, 0, 1, nullptr, accumulate, 0);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_bwd_dw(int dtype, void* dW, void* db, const void* X, const void* dY, int64_t M,
+                                   int64_t K, int64_t N, int accumulate) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  // dW[k, n] = sum_m X[m, k] dY[m, n]: A(k, m) = X[m, k] (k-major storage), B(m, n) = dY[m, n]
+  int rc = gemm_dispatch(dtype, 0, 0, K, N, M, X, K, 0, dY, N, 0, dW, N, 0, 1, nullptr, accumulate, 0);
+  if (rc) return rc;
+  if (db) return dtmi_colsum(dtype, db, dY, M, N, accumulate);
+  return DTMI_OK;
+  DTMI_BODY_END
+}

@@ -1,0 +1,375 @@
+// LayerNorm forward and backward (dtrain/autograd.py:207-223).
+//
+// One 64-lane wave owns one row; the row lives in registers (each lane holds
+// NV 16-byte vectors, or NV scalars when the row is not vector-aligned), so x
+// and dy are read from HBM exactly once and the row reductions are wave
+// butterflies (no LDS, no barriers). Four waves per 256-thread block.
+//
+// Backward fuses dx with the column reductions dgamma = sum_rows(dy * xh) and
+// dbeta = sum_rows(dy): every wave accumulates its rows' contributions in
+// registers, the four waves of a block combine through LDS in wave order, and
+// each block writes one partial row; a second kernel sums the partial rows in
+// block order. The grid depends only on the row count, so results are
+// bit-reproducible.
+#include <cmath>
+
+#include "common.h"
+
+namespace dtmi {
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+// Lane `lane` owns elements  VW*lane + 64*VW*j + e  (j < NV, e < VW).
+template <typename T, int NV, int VW>
+struct RowRegs {
+  T v[NV][VW];
+};
+
+template <typename T, int VW>
+__device__ __forceinline__ void load_vec(T (&dst)[VW], const T* __restrict__ src) {
+  if constexpr (VW * sizeof(T) == 16) {
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VW; ++e) dst[e] = src[e];
+  }
+}
+
+template <typename T, int VW>
+__device__ __forceinline__ void store_vec(T* __restrict__ dst, const T (&src)[VW]) {
+  if constexpr (VW * sizeof(T) == 16) {
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  } else {
+#pragma unroll
+    for (int e = 0; e < VW; ++e) dst[e] = src[e];
+  }
+}
+
+template <typename T, int NV, int VW>
+__global__ void __launch_bounds__(256) ln_fwd_kernel(T* __restrict__ y, T* __restrict__ mean_out,
+                                                      T* __restrict__ rstd_out, const T* __restrict__ x,
+                                                      const T* __restrict__ w, const T* __restrict__ b, int64_t rows,
+                                                      int cols, T eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const T* xr = x + row * cols;
+  T xv[NV][VW];
+  T s = T(0);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = VW * lane + 64 * VW * j;
+    if (c < cols) {
+      load_vec<T, VW>(xv[j], xr + c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) xv[j][e] = T(0);
+    }
+#pragma unroll
+    for (int e = 0; e < VW; ++e) s += xv[j][e];
+  }
+  const T n = (T)cols;
+  const T mu = wave_sum(s) / n;
+  T q = T(0);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = VW * lane + 64 * VW * j;
+    if (c < cols) {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        T xc = xv[j][e] - mu;
+        q += xc * xc;
+      }
+    }
+  }
+  const T var = wave_sum(q) / n;
+  const T rstd = T(1) / sqrt(var + eps);
+  T* yr = y + row * cols;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = VW * lane + 64 * VW * j;
+    if (c < cols) {
+      T wv[VW], bv[VW], o[VW];
+      load_vec<T, VW>(wv, w + c);
+      load_vec<T, VW>(bv, b + c);
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        T xh = (xv[j][e] - mu) * rstd;
+        o[e] = xh * wv[e] + bv[e];
+      }
+      store_vec<T, VW>(yr + c, o);
+    }
+  }
+  if (lane == 0) {
+    mean_out[row] = mu;
+    rstd_out[row] = rstd;
+  }
+}
+
+// Blocks needed for the deterministic column partials: a function of rows only.
+static int ln_bwd_blocks(int64_t rows) {
+  int64_t b = cdiv(rows, 4 * 8);  // at least 8 rows per wave
+  if (b < 1) b = 1;
+  return (int)(b < 512 ? b : 512);
+}
+
+template <typename T, int NV, int VW>
+__global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __restrict__ part_dw,
+                                                      T* __restrict__ part_db, const T* __restrict__ dy,
+                                                      const T* __restrict__ x, const T* __restrict__ w,
+                                                      const T* __restrict__ mean, const T* __restrict__ rstd,
+                                                      int64_t rows, int cols, int accumulate_dx) {
+  extern __shared__ unsigned char lds_raw[];
+  T* lds = reinterpret_cast<T*>(lds_raw);  // [4 waves][2][NV*VW*64]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t wstride = (int64_t)gridDim.x * 4;
+  T wv[NV][VW], adw[NV][VW], adb[NV][VW];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = VW * lane + 64 * VW * j;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) adw[j][e] = adb[j][e] = T(0);
+    if (c < cols) {
+      load_vec<T, VW>(wv[j], w + c);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) wv[j][e] = T(0);
+    }
+  }
+  const T n = (T)cols;
+  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < rows; row += wstride) {
+    const T mu = mean[row], rs = rstd[row];
+    T gv[NV][VW], xh[NV][VW];
+    T s1 = T(0), s2 = T(0);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = VW * lane + 64 * VW * j;
+      if (c < cols) {
+        T xv[VW];
+        load_vec<T, VW>(gv[j], dy + row * cols + c);
+        load_vec<T, VW>(xv, x + row * cols + c);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          xh[j][e] = (xv[e] - mu) * rs;
+          T gxh = gv[j][e] * wv[j][e];
+          s1 += gxh;
+          s2 += gxh * xh[j][e];
+          adw[j][e] += gv[j][e] * xh[j][e];
+          adb[j][e] += gv[j][e];
+        }
+      }
+    }
+    const T m1 = wave_sum(s1) / n;
+    const T m2 = wave_sum(s2) / n;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = VW * lane + 64 * VW * j;
+      if (c < cols) {
+        T o[VW];
+        if (accumulate_dx) load_vec<T, VW>(o, dx + row * cols + c);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+          T gxh = gv[j][e] * wv[j][e];
+          T r = rs * ((gxh - m1) - xh[j][e] * m2);
+          o[e] = accumulate_dx ? o[e] + r : r;
+        }
+        store_vec<T, VW>(dx + row * cols + c, o);
+      }
+    }
+  }
+  // combine the four waves in wave order, write this block's partial rows
+  constexpr int PER = NV * VW;
+  T* mine = lds + (size_t)wave * 2 * PER * 64;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      mine[(j * VW + e) * 64 + lane] = adw[j][e];
+      mine[PER * 64 + (j * VW + e) * 64 + lane] = adb[j][e];
+    }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        const int k = (j * VW + e) * 64 + lane;
+        T sdw = lds[k], sdb = lds[PER * 64 + k];
+#pragma unroll
+        for (int wv2 = 1; wv2 < 4; ++wv2) {
+          sdw += lds[(size_t)wv2 * 2 * PER * 64 + k];
+          sdb += lds[(size_t)wv2 * 2 * PER * 64 + PER * 64 + k];
+        }
+        const int c = VW * lane + 64 * VW * j + e;
+        if (c < cols) {
+          part_dw[(int64_t)blockIdx.x * cols + c] = sdw;
+          part_db[(int64_t)blockIdx.x * cols + c] = sdb;
+        }
+      }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) ln_bwd_reduce_kernel(T* __restrict__ dw, T* __restrict__ db,
+                                                             const T* __restrict__ part_dw,
+                                                             const T* __restrict__ part_db, int nparts, int cols,
+                                                             int accumulate) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= cols) return;
+  T a = T(0), b = T(0);
+  for (int p = 0; p < nparts; ++p) {
+    a += part_dw[(int64_t)p * cols + c];
+    b += part_db[(int64_t)p * cols + c];
+  }
+  if (accumulate) {
+    a = dw[c] + a;
+    b = db[c] + b;
+  }
+  dw[c] = a;
+  db[c] = b;
+}
+
+// ---------------------------------------------------------------- dispatch
+template <typename T, int VW>
+struct LnDispatch {
+  template <int NV>
+  static void fwd(int grid, T* y, T* mu, T* rs, const T* x, const T* w, const T* b, int64_t rows, int cols, T eps) {
+    ln_fwd_kernel<T, NV, VW><<<grid, 256, 0, stream()>>>(y, mu, rs, x, w, b, rows, cols, eps);
+  }
+  template <int NV>
+  static void bwd(int grid, T* dx, T* pdw, T* pdb, const T* dy, const T* x, const T* w, const T* mu, const T* rs,
+                  int64_t rows, int cols, int acc) {
+    size_t lds = (size_t)4 * 2 * NV * VW * 64 * sizeof(T);
+    ln_bwd_kernel<T, NV, VW><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, rows, cols, acc);
+  }
+};
+
+#define LN_NV_SWITCH(nv, CALL) \
+  switch (nv) {                \
+    case 1: CALL(1); break;    \
+    case 2: CALL(2); break;    \
+    case 3: CALL(3); break;    \
+    case 4: CALL(4); break;    \
+    case 6: CALL(6); break;    \
+    case 8: CALL(8); break;    \
+    case 12: CALL(12); break;  \
+    default: CALL(16); break;  \
+  }
+
+static int pick_nv(int64_t per_lane) {
+  static const int opts[] = {1, 2, 3, 4, 6, 8, 12, 16};
+  for (int o : opts)
+    if (per_lane <= o) return o;
+  return -1;
+}
+
+template <typename T>
+static int ln_fwd(void* y, void* mean, void* rstd, const void* x, const void* w, const void* b, int64_t rows,
+                  int64_t cols, double eps) {
+  constexpr int VWV = 16 / sizeof(T);
+  bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(y, 16) && aligned(w, 16) && aligned(b, 16);
+  int vw = vec ? VWV : 1;
+  int nv = pick_nv(cdiv(cols, 64LL * vw));
+  DTMI_CHECK(nv > 0, "dtmi_layernorm_fwd: rows of %lld elements exceed the supported %d", (long long)cols, 64 * 16 * vw);
+  int grid = (int)cdiv(rows, 4);
+  TimedLaunch tl(DTMI_FAM_OTHER, (double)rows * cols * 2 * sizeof(T));
+  T* Y = (T*)y;
+  T* MU = (T*)mean;
+  T* RS = (T*)rstd;
+  const T *X = (const T*)x, *W = (const T*)w, *B = (const T*)b;
+  int c = (int)cols;
+  T e = (T)eps;
+  if (vec) {
+#define CALLV(NV) LnDispatch<T, VWV>::template fwd<NV>(grid, Y, MU, RS, X, W, B, rows, c, e)
+    LN_NV_SWITCH(nv, CALLV)
+#undef CALLV
+  } else {
+#define CALLS(NV) LnDispatch<T, 1>::template fwd<NV>(grid, Y, MU, RS, X, W, B, rows, c, e)
+    LN_NV_SWITCH(nv, CALLS)
+#undef CALLS
+  }
+  LAUNCH_CHECK("ln_fwd_kernel");
+  return DTMI_OK;
+}
+
+template <typename T>
+static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, const void* w, const void* mean,
+                  const void* rstd, int64_t rows, int64_t cols, int accumulate) {
+  constexpr int VWV = 16 / sizeof(T);
+  bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(dy, 16) && aligned(dx, 16) && aligned(w, 16);
+  int vw = vec ? VWV : 1;
+  int nv = pick_nv(cdiv(cols, 64LL * vw));
+  DTMI_CHECK(nv > 0, "dtmi_layernorm_bwd: rows of %lld elements exceed the supported %d", (long long)cols, 64 * 16 * vw);
+  const int grid = ln_bwd_blocks(rows);
+  void* parts = nullptr;
+  int rc = pool_alloc(&parts, (size_t)2 * grid * cols * sizeof(T));
+  if (rc) return rc;
+  T* pdw = (T*)parts;
+  T* pdb = pdw + (size_t)grid * cols;
+  {
+    TimedLaunch tl(DTMI_FAM_LN_BWD, (double)rows * cols * 3 * sizeof(T));
+    T* DX = (T*)dx;
+    const T *DY = (const T*)dy, *X = (const T*)x, *W = (const T*)w, *MU = (const T*)mean, *RS = (const T*)rstd;
+    int c = (int)cols;
+    int acc = (accumulate & 1) ? 1 : 0;
+    if (vec) {
+#define CALLV(NV) LnDispatch<T, VWV>::template bwd<NV>(grid, DX, pdw, pdb, DY, X, W, MU, RS, rows, c, acc)
+      LN_NV_SWITCH(nv, CALLV)
+#undef CALLV
+    } else {
+#define CALLS(NV) LnDispatch<T, 1>::template bwd<NV>(grid, DX, pdw, pdb, DY, X, W, MU, RS, rows, c, acc)
+      LN_NV_SWITCH(nv, CALLS)
+#undef CALLS
+    }
+    ln_bwd_reduce_kernel<T><<<(unsigned)cdiv(cols, 256), 256, 0, stream()>>>(
+        (T*)dw, (T*)db, pdw, pdb, grid, (int)cols, (accumulate & 2) ? 1 : 0);
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(parts);
+  if (le != hipSuccess) return fail_hip(le, "ln_bwd kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+}
+
+}  // namespace dtmi
+
+using namespace dtmi;
+
+DTMI_EXPORT int dtmi_layernorm_fwd(int dtype, void* y, void* mean, void* rstd, const void* x, const void* w,
+                                   const void* b, int64_t rows, int64_t cols, double eps) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(rows >= 0 && cols > 0 && cols < (1 << 30), "dtmi_layernorm_fwd: bad shape [%lld, %lld]", (long long)rows,
+             (long long)cols);
+  if (rows == 0) return DTMI_OK;
+  DTMI_CHECK(y && mean && rstd && x && w && b, "dtmi_layernorm_fwd: NULL pointer");
+  if (dtype == DTMI_F32) return ln_fwd<float>(y, mean, rstd, x, w, b, rows, cols, eps);
+  return ln_fwd<double>(y, mean, rstd, x, w, b, rows, cols, eps);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_layernorm_bwd(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x,
+                                   const void* w, const void* mean, const void* rstd, int64_t rows, int64_t cols,
+                                   int accumulate) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(rows >= 0 && cols > 0 && cols < (1 << 30), "dtmi_layernorm_bwd: bad shape [%lld, %lld]", (long long)rows,
+             (long long)cols);
+  DTMI_CHECK(dw && db, "dtmi_layernorm_bwd: NULL dgamma/dbeta");
+  if (rows == 0) {
+    if (accumulate & 2) return DTMI_OK;
+    int rc = dtmi_fill(dtype, dw, 0.0, cols);
+    return rc ? rc : dtmi_fill(dtype, db, 0.0, cols);
+  }
+  DTMI_CHECK(dx && dy && x && w && mean && rstd, "dtmi_layernorm_bwd: NULL pointer");
+  if (dtype == DTMI_F32) return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, rows, cols, accumulate);
+  return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, rows, cols, accumulate);
+  DTMI_BODY_END
+}

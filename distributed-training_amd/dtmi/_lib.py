@@ -59,6 +59,17 @@ SIGNATURES: dict[str, list] = {
     "dtmi_relu_bwd": [i32, vp, vp, vp, i64],
     "dtmi_reduce_sum": [i32, vp, vp, pi64, i32, pi64, C.POINTER(C.c_int)],
     "dtmi_colsum": [i32, vp, vp, i64, i64, i32],
+    "dtmi_layernorm_fwd": [i32, vp, vp, vp, vp, vp, vp, i64, i64, f64],
+    "dtmi_layernorm_bwd": [i32, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
+    "dtmi_xent_fwd": [i32, vp, vp, vp, vp, vp, i64, i64],
+    "dtmi_xent_bwd": [i32, vp, vp, vp, vp, vp, vp, f64, i64, i64],
+    "dtmi_softmax_bwd": [i32, vp, vp, vp, i64, i64],
+    "dtmi_embedding_fwd": [i32, vp, vp, vp, i64, i64, i64],
+    "dtmi_embedding_bwd": [i32, vp, vp, vp, vp, vp, i32, i64, i64, i32],
+    "dtmi_gemm": [i32, i32, i32, i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, i64, vp, i32, i32],
+    "dtmi_linear_fwd": [i32, vp, vp, vp, vp, i64, i64, i64],
+    "dtmi_linear_bwd_dx": [i32, vp, vp, vp, i64, i64, i64, i32],
+    "dtmi_linear_bwd_dw": [i32, vp, vp, vp, vp, i64, i64, i64, i32],
 }
 
 _lib = None

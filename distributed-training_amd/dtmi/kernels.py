@@ -251,3 +251,175 @@ def sumsq_finish(partials: DeviceArray, count: int, out: DeviceArray, accumulate
 def clip_scale(sumsq_dev: DeviceArray, max_norm: float, scale_out: DeviceArray, norm_out: DeviceArray | None = None):
     _c("dtmi_clip_scale", sumsq_dev.ptr, float(max_norm), scale_out.ptr,
        norm_out.ptr if norm_out is not None else None)
+
+
+# -------------------------------------------------------------- layer norm
+def layernorm_fwd(x: DeviceArray, w: DeviceArray, b: DeviceArray, eps: float = 1e-5):
+    """Returns (y, mean, rstd); x is [..., C] (rows = product of leading dims)."""
+    _contig(x, w, b)
+    C_ = x.shape[-1]
+    if w.shape != (C_,) or b.shape != (C_,):
+        raise ValueError("layernorm: gamma/beta must be [C]")
+    rows = x.size // C_ if C_ else 0
+    y = empty(x.shape, x.dtype)
+    mean = empty((rows,), x.dtype)
+    rstd = empty((rows,), x.dtype)
+    _c("dtmi_layernorm_fwd", _dt(x, w, b), y.ptr, mean.ptr, rstd.ptr, x.ptr, w.ptr, b.ptr, rows, C_, float(eps))
+    return y, mean, rstd
+
+
+def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceArray, rstd: DeviceArray):
+    """Returns (dx, dw, db)."""
+    _contig(dy, x, w, mean, rstd)
+    if dy.shape != x.shape:
+        raise ValueError("layernorm_bwd: dy/x shape mismatch")
+    C_ = x.shape[-1]
+    rows = x.size // C_
+    if mean.size != rows or rstd.size != rows:
+        raise ValueError("layernorm_bwd: bad row statistics")
+    dx = empty(x.shape, x.dtype)
+    dw = empty((C_,), x.dtype)
+    db = empty((C_,), x.dtype)
+    _c("dtmi_layernorm_bwd", _dt(dy, x, w, mean, rstd), dx.ptr, dw.ptr, db.ptr, dy.ptr, x.ptr, w.ptr, mean.ptr,
+       rstd.ptr, rows, C_, 0)
+    return dx, dw, db
+
+
+# ----------------------------------------------------------- cross entropy
+def xent_fwd(logits: DeviceArray, targets: DeviceArray):
+    """logits [..., V], targets int64 [...]. Returns (loss 0-d, rowmax, rowsum)."""
+    _contig(logits, targets)
+    V = logits.shape[-1]
+    rows = logits.size // V
+    if targets.dtype != np.int64 or targets.size != rows:
+        raise ValueError("xent: targets must be int64 with one entry per row")
+    loss = empty((), logits.dtype)
+    rmax = empty((rows,), logits.dtype)
+    rsum = empty((rows,), logits.dtype)
+    _c("dtmi_xent_fwd", _dt(logits), loss.ptr, rmax.ptr, rsum.ptr, logits.ptr, targets.ptr, rows, V)
+    return loss, rmax, rsum
+
+
+def xent_bwd(logits: DeviceArray, targets: DeviceArray, rmax: DeviceArray, rsum: DeviceArray,
+             g: DeviceArray | None = None, g_host: float = 1.0) -> DeviceArray:
+    _contig(logits, targets, rmax, rsum)
+    V = logits.shape[-1]
+    rows = logits.size // V
+    if g is not None and (g.size != 1 or g.dtype != logits.dtype):
+        raise TypeError("xent_bwd: upstream gradient must be a 1-element array of the logits dtype")
+    dz = empty(logits.shape, logits.dtype)
+    _c("dtmi_xent_bwd", _dt(logits, rmax, rsum), dz.ptr, logits.ptr, rmax.ptr, rsum.ptr, targets.ptr,
+       g.ptr if g is not None else None, float(g_host), rows, V)
+    return dz
+
+
+def softmax_bwd(p: DeviceArray, dp: DeviceArray) -> DeviceArray:
+    _contig(p, dp)
+    if p.shape != dp.shape:
+        raise ValueError("softmax_bwd shape mismatch")
+    cols = p.shape[-1]
+    ds = empty(p.shape, p.dtype)
+    _c("dtmi_softmax_bwd", _dt(p, dp), ds.ptr, p.ptr, dp.ptr, p.size // cols, cols)
+    return ds
+
+
+# --------------------------------------------------------------- embedding
+def embedding_fwd(weight: DeviceArray, idx_dev: DeviceArray, out_shape) -> DeviceArray:
+    _contig(weight, idx_dev)
+    V, C_ = weight.shape
+    out = empty(tuple(out_shape) + (C_,), weight.dtype)
+    _c("dtmi_embedding_fwd", _dt(weight), out.ptr, weight.ptr, idx_dev.ptr, idx_dev.size, V, C_)
+    return out
+
+
+def embedding_segments(idx: np.ndarray):
+    """Stable sort of the host index array: (perm, seg_start, seg_row) int32 arrays
+    such that segment s lists, in increasing order, the positions holding row
+    seg_row[s] -- np.add.at's order of additions."""
+    flat = np.asarray(idx).reshape(-1).astype(np.int64)
+    perm = np.argsort(flat, kind="stable").astype(np.int32)
+    sv = flat[perm]
+    if sv.size:
+        starts = np.flatnonzero(np.r_[True, sv[1:] != sv[:-1]]).astype(np.int32)
+    else:
+        starts = np.zeros(0, np.int32)
+    seg_row = sv[starts].astype(np.int32) if sv.size else np.zeros(0, np.int32)
+    seg_start = np.r_[starts, np.int32(flat.size)].astype(np.int32)
+    return perm, seg_start, seg_row
+
+
+def embedding_bwd(dout: DeviceArray, V: int, segs) -> DeviceArray:
+    """segs: device int32 arrays (perm, seg_start, seg_row)."""
+    _contig(dout)
+    C_ = dout.shape[-1]
+    perm, seg_start, seg_row = segs
+    dw = empty((V, C_), dout.dtype)
+    _c("dtmi_embedding_bwd", _dt(dout), dw.ptr, dout.ptr, perm.ptr, seg_start.ptr, seg_row.ptr, seg_row.size, V,
+       C_, 1)
+    return dw
+
+
+# -------------------------------------------------------------------- GEMM
+def gemm(A: DeviceArray, B: DeviceArray, a_kcontig=True, b_kcontig=False, bias=None, out=None, splits=0):
+    """C = op(A) op(B) for 2-D or batched 3-D contiguous operands.
+    A is [M, K] (a_kcontig) or [K, M]; B is [K, N] (not b_kcontig) or [N, K]."""
+    _contig(A, B)
+    batched = A.ndim == 3
+    if batched:
+        if B.ndim != 3 or B.shape[0] != A.shape[0]:
+            raise ValueError("gemm: batched operands must share the batch dimension")
+        nb = A.shape[0]
+        a2, b2 = A.shape[1:], B.shape[1:]
+    else:
+        if A.ndim != 2 or B.ndim != 2:
+            raise ValueError("gemm: operands must be 2-D (or 3-D batched)")
+        nb = 1
+        a2, b2 = A.shape, B.shape
+    M, K = (a2[0], a2[1]) if a_kcontig else (a2[1], a2[0])
+    K2, N = (b2[1], b2[0]) if b_kcontig else (b2[0], b2[1])
+    if K != K2:
+        raise ValueError(f"gemm: inner dimensions differ ({K} vs {K2})")
+    shape = (nb, M, N) if batched else (M, N)
+    if out is None:
+        out = empty(shape, A.dtype)
+    elif out.shape != shape or not out.is_contiguous:
+        raise ValueError("gemm: bad output")
+    if bias is not None:
+        _contig(bias)
+        if bias.shape != (N,):
+            raise ValueError("gemm: bias must be [N]")
+    lda = a2[1]
+    ldb = b2[1]
+    _c("dtmi_gemm", _dt(A, B, out), 1 if a_kcontig else 0, 1 if b_kcontig else 0, M, N, K, A.ptr, lda,
+       a2[0] * a2[1], B.ptr, ldb, b2[0] * b2[1], out.ptr, N, M * N, nb, bias.ptr if bias is not None else None, 0,
+       int(splits))
+    return out
+
+
+def linear_fwd(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None) -> DeviceArray:
+    _contig(x2, w)
+    M, K = x2.shape
+    K2, N = w.shape
+    if K != K2:
+        raise ValueError("linear: shape mismatch")
+    y = empty((M, N), x2.dtype)
+    _c("dtmi_linear_fwd", _dt(x2, w), y.ptr, x2.ptr, w.ptr, b.ptr if b is not None else None, M, K, N)
+    return y
+
+
+def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, need_db=True):
+    """Returns (dx, dw, db) for y = x @ w + b with x [M, K], w [K, N]."""
+    _contig(x2, w, dy2)
+    M, K = x2.shape
+    N = w.shape[1]
+    if dy2.shape != (M, N):
+        raise ValueError("linear_bwd: dy shape mismatch")
+    dt = _dt(x2, w, dy2)
+    dx = None
+    if need_dx:
+        dx = empty((M, K), x2.dtype)
+        _c("dtmi_linear_bwd_dx", dt, dx.ptr, dy2.ptr, w.ptr, M, K, N, 0)
+    dw = empty((K, N), x2.dtype)
+    db = empty((N,), x2.dtype) if need_db else None
+    _c("dtmi_linear_bwd_dw", dt, dw.ptr, db.ptr if db is not None else None, x2.ptr, dy2.ptr, M, K, N, 0)
+    return dx, dw, db

@@ -187,6 +187,67 @@ int dtmi_reduce_sum(int dtype, void* out, const void* x, const int64_t* strides,
  * accumulate != 0 adds onto out. */
 int dtmi_colsum(int dtype, void* out, const void* x, int64_t rows, int64_t cols, int accumulate);
 
+/* ------------------------------------------------------------ LayerNorm
+ * dtrain/autograd.py:207-223. Row-major [rows, cols]; one wave per row.
+ * Forward saves the row mean and 1/sqrt(var + eps) for the backward (dtrain
+ * keeps xh and rstd; xh is recomputed from x, mean and rstd).
+ * Backward: dx = rstd * (gxh - mean(gxh) - xh * mean(gxh * xh)), gxh = dy * w;
+ * dw = sum_rows(dy * xh); db = sum_rows(dy) (deterministic block partials).
+ * accumulate: bit 0 adds dx onto the existing dx, bit 1 adds dw/db onto theirs. */
+int dtmi_layernorm_fwd(int dtype, void* y, void* mean, void* rstd, const void* x, const void* w, const void* b,
+                       int64_t rows, int64_t cols, double eps);
+int dtmi_layernorm_bwd(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x, const void* w,
+                       const void* mean, const void* rstd, int64_t rows, int64_t cols, int accumulate);
+
+/* --------------------------------------------------------- cross entropy
+ * dtrain/autograd.py:250-266 over logits [rows, vocab] and int64 targets.
+ * Forward writes the mean loss -(sum_r log p[r, t_r]) / rows to *loss and the
+ * per-row max and sum of exp for the backward. Backward writes
+ * dlogits = (exp(z - max) / sum - onehot(t)) * (g / rows) where g is *g_dev
+ * (a device scalar of dtype) or g_host when g_dev is NULL. */
+int dtmi_xent_fwd(int dtype, void* loss, void* rowmax, void* rowsum, const void* logits, const int64_t* targets,
+                  int64_t rows, int64_t vocab);
+int dtmi_xent_bwd(int dtype, void* dlogits, const void* logits, const void* rowmax, const void* rowsum,
+                  const int64_t* targets, const void* g_dev, double g_host, int64_t rows, int64_t vocab);
+
+/* Row-wise softmax backward dS = P * (dP - rowsum(dP * P)), the core of
+ * dtrain/autograd.py:242 (without the 1/sqrt(d) factor). */
+int dtmi_softmax_bwd(int dtype, void* ds, const void* p, const void* dp, int64_t rows, int64_t cols);
+
+/* ------------------------------------------------------------- embedding
+ * dtrain/autograd.py:199-204. Forward gathers weight rows by int64 index.
+ * Backward reproduces np.add.at(zeros, idx, g) bit for bit: perm lists the
+ * positions of idx stably sorted by value, segment s covers
+ * perm[seg_start[s] .. seg_start[s+1]) and belongs to row seg_row[s]; each row
+ * is the in-order sum of its positions' gradient rows. zero_fill != 0 clears
+ * dweight first (rows nobody indexes stay zero). */
+int dtmi_embedding_fwd(int dtype, void* out, const void* weight, const int64_t* idx, int64_t n_idx, int64_t vocab,
+                       int64_t cols);
+int dtmi_embedding_bwd(int dtype, void* dweight, const void* dout, const int32_t* perm, const int32_t* seg_start,
+                       const int32_t* seg_row, int nseg, int64_t vocab, int64_t cols, int zero_fill);
+
+/* ------------------------------------------------------------ MFMA GEMM
+ * C[b] = sum_k A(m,k) B(k,n) (+ bias[n]) (+ C[b] if accumulate), batched.
+ * a_kcontig: A(m,k) = A[m*lda + k], else A[k*lda + m].
+ * b_kcontig: B(k,n) = B[n*ldb + k], else B[k*ldb + n].
+ * splits > 0 forces that many K splits (0 = chosen from the tile count).
+ * dtrain/autograd.py:102-109: a @ b and its backward g @ b^T, a^T @ g
+ * (batched over leading dimensions). */
+int dtmi_gemm(int dtype, int a_kcontig, int b_kcontig, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+              int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C, int64_t ldc, int64_t strideC,
+              int64_t batch, const void* bias, int accumulate, int splits);
+
+/* Linear layer y = x @ w + b (dtrain/nn.py:63-65) with X [M,K], W [K,N]:
+ * forward Y = X W + b (bias fused in the epilogue, may be NULL);
+ * dX = dY W^T (autograd.py:106); dW = X^T dY (autograd.py:107, the batch sum
+ * of _unbroadcast folded into the reduction over M) and db = column sums of
+ * dY (autograd.py:29-36 via the add node, may be NULL). */
+int dtmi_linear_fwd(int dtype, void* Y, const void* X, const void* W, const void* b, int64_t M, int64_t K, int64_t N);
+int dtmi_linear_bwd_dx(int dtype, void* dX, const void* dY, const void* W, int64_t M, int64_t K, int64_t N,
+                       int accumulate);
+int dtmi_linear_bwd_dw(int dtype, void* dW, void* db, const void* X, const void* dY, int64_t M, int64_t K, int64_t N,
+                       int accumulate);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,168 @@
+"""Bandwidth kernels (LayerNorm, cross entropy, softmax backward, embedding) and
+the MFMA GEMM on the GPU against the oracle.
+
+Bar: float64 normwise relative error <= 1e-12, float32 <= 1e-5; the embedding
+backward is bit-exact (same additions in the same order as np.add.at);
+reductions are deterministic (two runs, same bits).
+"""
+import numpy as np
+import pytest
+
+from helpers import bits_equal, rel_err
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float64: 1e-12, np.float32: 1e-5}
+
+
+def _dev():
+    from dtmi import device as D, kernels as K
+    return D, K
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("shape", [(2, 3, 6), (256, 64), (4096, 768), (5, 1000), (3, 17)])
+def test_layernorm_forward_backward(dev, dt, shape):
+    D, K = _dev()
+    rng = np.random.default_rng(sum(shape))
+    C = shape[-1]
+    x = rng.standard_normal(shape).astype(dt)
+    w = (1 + 0.01 * rng.standard_normal(C)).astype(dt)
+    b = (0.01 * rng.standard_normal(C)).astype(dt)
+    g = rng.standard_normal(shape).astype(dt)
+    y, cache = ops.layer_norm_fwd(x, w, b)
+    gx, gw, gb = ops.layer_norm_bwd(g, cache, w)
+    dy, mean, rstd = K.layernorm_fwd(D.from_numpy(x), D.from_numpy(w), D.from_numpy(b))
+    assert rel_err(dy.numpy(), y) <= TOL[dt]
+    assert rel_err(rstd.numpy(), cache[1].reshape(-1)) <= TOL[dt]
+    dx, dw, db = K.layernorm_bwd(D.from_numpy(g), D.from_numpy(x), D.from_numpy(w), mean, rstd)
+    assert rel_err(dx.numpy(), gx) <= TOL[dt]
+    assert rel_err(dw.numpy(), gw) <= TOL[dt]
+    assert rel_err(db.numpy(), gb) <= TOL[dt]
+    dx2, dw2, _ = K.layernorm_bwd(D.from_numpy(g), D.from_numpy(x), D.from_numpy(w), mean, rstd)
+    assert bits_equal(dx2.numpy(), dx.numpy()) and bits_equal(dw2.numpy(), dw.numpy())
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("rows,V", [(6, 5), (256, 65), (64, 50304), (33, 1003)])
+def test_cross_entropy_forward_backward(dev, dt, rows, V):
+    D, K = _dev()
+    rng = np.random.default_rng(rows + V)
+    z = (rng.standard_normal((rows, V)) * 3).astype(dt)
+    t = rng.integers(0, V, rows)
+    loss, cache = ops.cross_entropy_fwd(z, t)
+    gscale = np.asarray(0.25, dtype=dt)  # the `loss * (1/n_micro)` upstream gradient
+    gz = ops.cross_entropy_bwd(gscale, z, t, cache)
+    dz = D.from_numpy(z)
+    dtgt = D.from_numpy(t.astype(np.int64))
+    dloss, rmax, rsum = K.xent_fwd(dz, dtgt)
+    assert rel_err(dloss.numpy(), loss) <= TOL[dt]
+    ggrad = K.xent_bwd(dz, dtgt, rmax, rsum, g=D.from_numpy(gscale.reshape(1)))
+    assert rel_err(ggrad.numpy(), gz) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+def test_softmax_backward(dev, dt):
+    D, K = _dev()
+    rng = np.random.default_rng(7)
+    s = rng.standard_normal((16 * 12 * 4, 256))
+    p = (np.exp(s) / np.exp(s).sum(-1, keepdims=True)).astype(dt)
+    dp = rng.standard_normal(p.shape).astype(dt)
+    ref = ops.softmax_bwd(p, dp)
+    assert rel_err(K.softmax_bwd(D.from_numpy(p), D.from_numpy(dp)).numpy(), ref) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("V,C,shape", [(3, 4, (2, 3)), (65, 64, (8, 32)), (50304, 768, (8, 1024)), (32, 16, (8, 32))])
+def test_embedding_forward_and_bit_exact_scatter_add(dev, dt, V, C, shape):
+    D, K = _dev()
+    rng = np.random.default_rng(V)
+    w = rng.standard_normal((V, C)).astype(dt)
+    idx = rng.integers(0, V, shape)
+    if V == 3:
+        idx = np.array([[0, 2, 2], [1, 0, 2]])  # dtrain tests/test_autograd.py:61-63
+    g = rng.standard_normal(shape + (C,)).astype(dt)
+    didx = D.from_numpy(idx.astype(np.int64).reshape(-1))
+    out = K.embedding_fwd(D.from_numpy(w), didx, shape)
+    assert bits_equal(out.numpy(), w[idx])
+    perm, start, row = K.embedding_segments(idx)
+    segs = tuple(D.from_numpy(a) for a in (perm, start, row))
+    dw = K.embedding_bwd(D.from_numpy(g), V, segs)
+    assert bits_equal(dw.numpy(), ops.embedding_bwd(g, (V, C), dt, idx))
+
+
+def _gemm_ref(a, b, akc, bkc):
+    A = a if akc else np.swapaxes(a, -1, -2)
+    B = b if not bkc else np.swapaxes(b, -1, -2)
+    return A @ B
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("akc,bkc", [(True, False), (True, True), (False, False), (False, True)])
+@pytest.mark.parametrize("M,N,K", [(256, 192, 64), (300, 65, 64), (1, 1, 1), (129, 257, 33), (8, 5, 7),
+                                   (512, 2304, 768)])
+def test_gemm_layouts_and_ragged_shapes(dev, dt, akc, bkc, M, N, K):
+    D, K_ = _dev()
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    a = rng.standard_normal((M, K) if akc else (K, M)).astype(dt)
+    b = rng.standard_normal((N, K) if bkc else (K, N)).astype(dt)
+    bias = rng.standard_normal(N).astype(dt)
+    ref = _gemm_ref(a.astype(np.float64), b.astype(np.float64), akc, bkc) + bias
+    got = K_.gemm(D.from_numpy(a), D.from_numpy(b), a_kcontig=akc, b_kcontig=bkc, bias=D.from_numpy(bias)).numpy()
+    assert rel_err(got, ref) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+def test_gemm_split_k_is_deterministic_and_correct(dev, dt):
+    D, K_ = _dev()
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((4096, 256)).astype(dt)  # X: [M=4096, K=256] -> dW = X^T dY
+    g = rng.standard_normal((4096, 384)).astype(dt)
+    ref = a.astype(np.float64).T @ g.astype(np.float64)
+    outs = [K_.gemm(D.from_numpy(a), D.from_numpy(g), a_kcontig=False, b_kcontig=False, splits=s).numpy()
+            for s in (1, 4, 4, 0)]
+    for o in outs:
+        assert rel_err(o, ref) <= TOL[dt]
+    assert bits_equal(outs[1], outs[2])
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+def test_batched_gemm(dev, dt):
+    D, K_ = _dev()
+    rng = np.random.default_rng(12)
+    a = rng.standard_normal((3, 40, 24)).astype(dt)
+    b = rng.standard_normal((3, 24, 56)).astype(dt)
+    got = K_.gemm(D.from_numpy(a), D.from_numpy(b)).numpy()
+    assert rel_err(got, a @ b) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+def test_linear_forward_backward_at_layernorm_linear_workload(dev, dt):
+    """The LayerNorm + Linear backward workload: x [16384, 768], W [768, 3072],
+    y = LN(x) W + b; dX, dW, db, dgamma, dbeta against the oracle."""
+    D, K = _dev()
+    rng = np.random.default_rng(2)
+    M, Cin, N = 16384, 768, 3072
+    x = rng.standard_normal((M, Cin)).astype(dt)
+    W = (rng.standard_normal((Cin, N)) * 0.02).astype(dt)
+    b = np.zeros(N, dt)
+    gamma = (1 + rng.standard_normal(Cin) * 0.01).astype(dt)
+    beta = (rng.standard_normal(Cin) * 0.01).astype(dt)
+    dY = rng.standard_normal((M, N)).astype(dt)
+    h, cache = ops.layer_norm_fwd(x, gamma, beta)
+    gh, gW = ops.matmul_bwd(dY, h, W)
+    gb = ops.unbroadcast(dY, (N,))
+    gx, ggam, gbet = ops.layer_norm_bwd(gh, cache, gamma)
+    dx_, dW_, db_ = D.from_numpy(x), D.from_numpy(W), D.from_numpy(b)
+    hd, mean, rstd = K.layernorm_fwd(dx_, D.from_numpy(gamma), D.from_numpy(beta))
+    y = K.linear_fwd(hd, dW_, db_)
+    assert rel_err(y.numpy(), h @ W + b) <= TOL[dt]
+    dh, dW, db = K.linear_bwd(hd, dW_, D.from_numpy(dY))
+    assert rel_err(dh.numpy(), gh) <= TOL[dt]
+    assert rel_err(dW.numpy(), gW) <= TOL[dt]
+    assert rel_err(db.numpy(), gb) <= TOL[dt]
+    dx, dgam, dbet = K.layernorm_bwd(dh, dx_, D.from_numpy(gamma), mean, rstd)
+    assert rel_err(dx.numpy(), gx) <= TOL[dt]
+    assert rel_err(dgam.numpy(), ggam) <= TOL[dt]
+    assert rel_err(dbet.numpy(), gbet) <= TOL[dt]
