@@ -1,0 +1,589 @@
+// Causal self-attention on the MFMA cores: flash-style forward that keeps the
+// per-row max and sum of the softmax, and a backward that recomputes the
+// probabilities from them (dtrain/autograd.py:226-247 computes and keeps the
+// full (B, H, T, T) probability tensor instead).
+//
+// Shapes (B, H, T, D) with D contiguous and arbitrary element strides for the
+// b, h and t axes, so q/k/v are read straight out of the fused qkv projection
+// ([B, T, 3, H, D] row-major) and o / dq / dk / dv are written straight into
+// [B, T, H, D] / [B, T, 3, H, D] layouts: the reshape/transpose/split of
+// dtrain/nn.py:100-103 costs no copies.
+//
+// Transposed formulation. With MT x MT MFMA tiles (32 in float32, 16 in
+// float64) an MFMA result gives each lane one column and NACC rows. Each wave
+// owns MT queries (forward, dQ) or MT keys (dK/dV) as the COLUMNS of its tiles
+// (S^T = K Q^T in the forward), so per-query softmax statistics are per-lane
+// values combined across the G lane groups with one or two xor-shuffles, and
+// the probabilities computed in registers feed the next MFMA directly as its
+// B operand: result register i of lane group g is exactly the value that lane
+// supplies as k-slot g of an MFMA step, with the A operand (V, dO, K or Q
+// rows) read from LDS at the matching row. The k-permutation is the same on
+// both operands, so every product is a plain sum over the reduction index.
+//
+// Backward without atomics: kernel A owns a key block and loops over the query
+// blocks that see it (dK, dV accumulate in registers); kernel B owns a query
+// block and loops over its key blocks (dQ in registers). Both recompute
+// P = exp(s - max) / sum. Results are deterministic.
+#include <cmath>
+
+#include "common.h"
+
+namespace dtmi {
+
+template <typename T>
+struct AM;
+template <>
+struct AM<float> {
+  static constexpr int MT = 32, G = 2, VEC = 4, NACC = 16, PAD = 4;
+  typedef float acc_t __attribute__((ext_vector_type(16)));
+  typedef float vec_t __attribute__((ext_vector_type(4)));
+  static __device__ __forceinline__ acc_t mma(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int i, int g) { return 8 * (i / 4) + 4 * g + (i % 4); }
+};
+template <>
+struct AM<double> {
+  static constexpr int MT = 16, G = 4, VEC = 2, NACC = 4, PAD = 2;
+  typedef double acc_t __attribute__((ext_vector_type(4)));
+  typedef double vec_t __attribute__((ext_vector_type(2)));
+  static __device__ __forceinline__ acc_t mma(double a, double b, acc_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int i, int g) { return g + 4 * i; }
+};
+
+template <typename T>
+__device__ __forceinline__ T group_max(T x) {
+  constexpr int G = AM<T>::G;
+  x = fmax(x, __shfl_xor(x, 32, 64));
+  if (G == 4) x = fmax(x, __shfl_xor(x, 16, 64));
+  return x;
+}
+template <typename T>
+__device__ __forceinline__ T group_sum(T x) {
+  constexpr int G = AM<T>::G;
+  x += __shfl_xor(x, 32, 64);
+  if (G == 4) x += __shfl_xor(x, 16, 64);
+  return x;
+}
+
+struct Strides3 {
+  int64_t b, h, t;
+};
+
+struct AttnArgs {
+  const void *q, *k, *v, *o, *dO;
+  void *out, *dq, *dk, *dv;
+  void *rowmax, *rowsum;  // [B, H, T]
+  const void* drow;       // [B, H, T] rowsum(dO * O)
+  Strides3 sq, sk, sv, so, sdo, sdq, sdk, sdv;
+  int64_t B, H, T, D;
+  double scale;
+  int vec;  // 16-byte global access allowed for every operand
+};
+
+// Load NR rows [r0, r0 + NR) of a (T x D) matrix with row stride `rs` into LDS
+// [NR][DP + PAD]; rows >= T and columns >= D read as 0.
+template <typename T, int NR, int DP>
+__device__ __forceinline__ void load_rows(T* __restrict__ lds, const T* __restrict__ base, int64_t rs, int64_t r0,
+                                          int64_t Tn, int64_t D, bool vec) {
+  constexpr int VEC = AM<T>::VEC, LD = DP + AM<T>::PAD;
+  if (vec) {
+    constexpr int NV = NR * DP / VEC;
+    for (int f = threadIdx.x; f < NV; f += 256) {
+      const int r = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
+      typename AM<T>::vec_t x = typename AM<T>::vec_t(0);
+      if (r0 + r < Tn && d < D) x = *reinterpret_cast<const typename AM<T>::vec_t*>(base + (r0 + r) * rs + d);
+      *reinterpret_cast<typename AM<T>::vec_t*>(lds + r * LD + d) = x;
+    }
+  } else {
+    for (int f = threadIdx.x; f < NR * DP; f += 256) {
+      const int r = f / DP, d = f % DP;
+      lds[r * LD + d] = (r0 + r < Tn && d < D) ? base[(r0 + r) * rs + d] : T(0);
+    }
+  }
+}
+
+// A lane's VEC-vectors of one row (its column c of the wave tile), d-chunked:
+// element s of vector ch is d = 8*ch + VEC*g + s.
+template <typename T, int DP>
+__device__ __forceinline__ void load_frag_rows(typename AM<T>::vec_t (&f)[DP / 8], const T* __restrict__ base,
+                                               int64_t rs, int64_t r, int64_t Tn, int64_t D, int g, bool vec) {
+  constexpr int VEC = AM<T>::VEC;
+#pragma unroll
+  for (int ch = 0; ch < DP / 8; ++ch) {
+    const int d = 8 * ch + VEC * g;
+    typename AM<T>::vec_t x = typename AM<T>::vec_t(0);
+    if (r < Tn) {
+      if (vec) {
+        if (d < D) x = *reinterpret_cast<const typename AM<T>::vec_t*>(base + r * rs + d);
+      } else {
+#pragma unroll
+        for (int s = 0; s < VEC; ++s)
+          if (d + s < D) x[s] = base[r * rs + d + s];
+      }
+    }
+    f[ch] = x;
+  }
+}
+
+// acc (MT x MT, rows = LDS rows rbase.., cols = lane's fragment rows) +=
+// sum_d lds[rbase + row][d] * frag[col][d]
+template <typename T, int DP>
+__device__ __forceinline__ typename AM<T>::acc_t mma_rows_frag(typename AM<T>::acc_t acc, const T* __restrict__ lds,
+                                                                int rbase, const typename AM<T>::vec_t (&f)[DP / 8],
+                                                                int g, int c) {
+  constexpr int VEC = AM<T>::VEC, LD = DP + AM<T>::PAD;
+#pragma unroll
+  for (int ch = 0; ch < DP / 8; ++ch) {
+    const typename AM<T>::vec_t a =
+        *reinterpret_cast<const typename AM<T>::vec_t*>(lds + (rbase + c) * LD + 8 * ch + VEC * g);
+#pragma unroll
+    for (int s = 0; s < VEC; ++s) acc = AM<T>::mma(a[s], f[ch][s], acc);
+  }
+  return acc;
+}
+
+// out^T (DP x MT, DP/MT tiles over d) += sum_j lds[jbase + j][d] * P(col, j),
+// where P for k-slot g at step i is register i of pacc (rows j = row(i, g)).
+template <typename T, int DP>
+__device__ __forceinline__ void mma_lds_t_regs(typename AM<T>::acc_t (&out)[DP / AM<T>::MT],
+                                               const T* __restrict__ lds, int jbase,
+                                               const typename AM<T>::acc_t& pacc, int g, int c) {
+  constexpr int MT = AM<T>::MT, NACC = AM<T>::NACC, LD = DP + AM<T>::PAD;
+#pragma unroll
+  for (int i = 0; i < NACC; ++i) {
+    const T* rowp = lds + (jbase + AM<T>::row(i, g)) * LD + c;
+#pragma unroll
+    for (int dt = 0; dt < DP / MT; ++dt) out[dt] = AM<T>::mma(rowp[dt * MT], pacc[i], out[dt]);
+  }
+}
+
+// ----------------------------------------------------------------- forward
+template <typename T, int DP>
+__global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
+  using M = AM<T>;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  constexpr int KB = 2 * MT;  // keys per LDS block
+  constexpr int QB = 4 * MT;  // queries per block (MT per wave)
+  constexpr int STAGE = (2 * KB * LD > QB * LD) ? 2 * KB * LD : QB * LD;
+  __shared__ __attribute__((aligned(16))) T lds[STAGE];
+  T* Ks = lds;
+  T* Vs = lds + KB * LD;
+
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int64_t q0 = (int64_t)blockIdx.x * QB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / MT, c = lane % MT;
+  const int64_t qr = q0 + wave * MT + c;  // this lane's query (column)
+  const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+  const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+  const T* V = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+  const T scale = (T)a.scale;
+  const T ninf = -INFINITY;
+  const bool vec = a.vec != 0;
+
+  typename M::vec_t qf[DP / 8];
+  load_frag_rows<T, DP>(qf, Q, a.sq.t, qr, a.T, a.D, g, vec);
+
+  typename M::acc_t oacc[DP / MT];
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] = typename M::acc_t(0);
+  T mrow = ninf, lrow = T(0);
+
+  const int64_t qmax = (q0 + QB < a.T ? q0 + QB : a.T) - 1;
+  const int64_t nkb = qmax / KB + 1;
+  for (int64_t kb = 0; kb < nkb; ++kb) {
+    const int64_t k0 = kb * KB;
+    __syncthreads();
+    load_rows<T, KB, DP>(Ks, K, a.sk.t, k0, a.T, a.D, vec);
+    load_rows<T, KB, DP>(Vs, V, a.sv.t, k0, a.T, a.D, vec);
+    __syncthreads();
+    typename M::acc_t sacc[KB / MT];
+#pragma unroll
+    for (int jt = 0; jt < KB / MT; ++jt) {
+      sacc[jt] = mma_rows_frag<T, DP>(typename M::acc_t(0), Ks, jt * MT, qf, g, c);
+    }
+    // scale, causal mask (key j > query r), block max
+    T bmax = ninf;
+#pragma unroll
+    for (int jt = 0; jt < KB / MT; ++jt)
+#pragma unroll
+      for (int i = 0; i < NACC; ++i) {
+        const int64_t j = k0 + jt * MT + M::row(i, g);
+        T s = sacc[jt][i] * scale;
+        s = (j <= qr && j < a.T) ? s : ninf;
+        sacc[jt][i] = s;
+        bmax = fmax(bmax, s);
+      }
+    bmax = group_max(bmax);
+    const T mnew = fmax(mrow, bmax);
+    const T alpha = (mnew == ninf) ? T(1) : exp(mrow - mnew);
+    T psum = T(0);
+#pragma unroll
+    for (int jt = 0; jt < KB / MT; ++jt)
+#pragma unroll
+      for (int i = 0; i < NACC; ++i) {
+        const T p = (mnew == ninf) ? T(0) : exp(sacc[jt][i] - mnew);
+        sacc[jt][i] = p;
+        psum += p;
+      }
+    psum = group_sum(psum);
+    lrow = lrow * alpha + psum;
+    mrow = mnew;
+#pragma unroll
+    for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
+#pragma unroll
+    for (int jt = 0; jt < KB / MT; ++jt) mma_lds_t_regs<T, DP>(oacc, Vs, jt * MT, sacc[jt], g, c);
+  }
+  // normalise and write through LDS: lane holds O^T(d = dt*MT + row(i, g), query c)
+  __syncthreads();
+  T* Os = lds + wave * MT * LD;
+  const T inv = lrow > T(0) ? T(1) / lrow : T(0);
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt)
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) Os[c * LD + dt * MT + M::row(i, g)] = oacc[dt][i] * inv;
+  __syncthreads();
+  T* O = (T*)a.out + b * a.so.b + h * a.so.h;
+  for (int f = threadIdx.x; f < QB * DP; f += 256) {
+    const int r = f / DP, d = f % DP;
+    const int64_t qq = q0 + r;
+    if (qq < a.T && d < a.D) O[qq * a.so.t + d] = lds[r * LD + d];
+  }
+  if (g == 0 && qr < a.T) {
+    ((T*)a.rowmax)[bh * a.T + qr] = mrow;
+    ((T*)a.rowsum)[bh * a.T + qr] = lrow;
+  }
+}
+
+// D_r = sum_d dO[r, d] * O[r, d]  (= rowsum(dP * P), the softmax-backward term)
+template <typename T>
+__global__ void __launch_bounds__(256) attn_drow_kernel(AttnArgs a) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int64_t total = a.B * a.H * a.T;
+  if (row >= total) return;
+  const int64_t t = row % a.T, bh = row / a.T, b = bh / a.H, h = bh % a.H;
+  const T* O = (const T*)a.o + b * a.so.b + h * a.so.h + t * a.so.t;
+  const T* G = (const T*)a.dO + b * a.sdo.b + h * a.sdo.h + t * a.sdo.t;
+  T s = T(0);
+  for (int64_t d = lane; d < a.D; d += 64) s += O[d] * G[d];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (lane == 0) ((T*)a.drow)[row] = s;
+}
+
+// ------------------------------------------------- backward A: dK and dV
+template <typename T, int DP>
+__global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnArgs a) {
+  using M = AM<T>;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  constexpr int QB = 2 * MT;  // queries per LDS block
+  constexpr int KBB = 4 * MT;  // keys per block (MT per wave)
+  constexpr int STAGE = (2 * QB * LD > KBB * LD) ? 2 * QB * LD : KBB * LD;
+  __shared__ __attribute__((aligned(16))) T lds[STAGE];
+  __shared__ T stat_m[QB], stat_l[QB], stat_d[QB];
+  T* Qs = lds;
+  T* Gs = lds + QB * LD;
+
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int64_t k0 = (int64_t)blockIdx.x * KBB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / MT, c = lane % MT;
+  const int64_t kj = k0 + wave * MT + c;  // this lane's key (column)
+  const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+  const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+  const T* V = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+  const T* G = (const T*)a.dO + b * a.sdo.b + h * a.sdo.h;
+  const T* RM = (const T*)a.rowmax + bh * a.T;
+  const T* RS = (const T*)a.rowsum + bh * a.T;
+  const T* DR = (const T*)a.drow + bh * a.T;
+  const T scale = (T)a.scale;
+  const bool vec = a.vec != 0;
+
+  typename M::vec_t kf[DP / 8], vf[DP / 8];
+  load_frag_rows<T, DP>(kf, K, a.sk.t, kj, a.T, a.D, g, vec);
+  load_frag_rows<T, DP>(vf, V, a.sv.t, kj, a.T, a.D, g, vec);
+  typename M::acc_t dk[DP / MT], dv[DP / MT];
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt) dk[dt] = dv[dt] = typename M::acc_t(0);
+
+  if (k0 < a.T) {
+    for (int64_t qs = (k0 / QB) * QB; qs < a.T; qs += QB) {
+      __syncthreads();
+      load_rows<T, QB, DP>(Qs, Q, a.sq.t, qs, a.T, a.D, vec);
+      load_rows<T, QB, DP>(Gs, G, a.sdo.t, qs, a.T, a.D, vec);
+      for (int r = threadIdx.x; r < QB; r += 256) {
+        const bool ok = qs + r < a.T;
+        stat_m[r] = ok ? RM[qs + r] : T(0);
+        stat_l[r] = ok ? RS[qs + r] : T(1);
+        stat_d[r] = ok ? DR[qs + r] : T(0);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int rt = 0; rt < QB / MT; ++rt) {
+        // S(r, j) and dP(r, j): rows r = queries (LDS), columns j = this wave's keys
+        typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Qs, rt * MT, kf, g, c);
+        typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Gs, rt * MT, vf, g, c);
+#pragma unroll
+        for (int i = 0; i < NACC; ++i) {
+          const int rl = rt * MT + M::row(i, g);
+          const int64_t r = qs + rl;
+          const bool live = kj <= r && r < a.T && kj < a.T;
+          const T p = live ? exp(s[i] * scale - stat_m[rl]) / stat_l[rl] : T(0);
+          s[i] = p;
+          dp[i] = p * (dp[i] - stat_d[rl]);
+        }
+        // dV^T += dO^T P ; dK^T += Q^T dS
+        mma_lds_t_regs<T, DP>(dv, Gs, rt * MT, s, g, c);
+        mma_lds_t_regs<T, DP>(dk, Qs, rt * MT, dp, g, c);
+      }
+    }
+  }
+  // write dK (scaled) and dV through LDS
+  T* DK = (T*)a.dk + b * a.sdk.b + h * a.sdk.h;
+  T* DV = (T*)a.dv + b * a.sdv.b + h * a.sdv.h;
+  for (int which = 0; which < 2; ++which) {
+    __syncthreads();
+    T* Ws = lds + wave * MT * LD;
+#pragma unroll
+    for (int dt = 0; dt < DP / MT; ++dt)
+#pragma unroll
+      for (int i = 0; i < NACC; ++i)
+        Ws[c * LD + dt * MT + M::row(i, g)] = which == 0 ? dk[dt][i] * scale : dv[dt][i];
+    __syncthreads();
+    T* dst = which == 0 ? DK : DV;
+    const int64_t st = which == 0 ? a.sdk.t : a.sdv.t;
+    for (int f = threadIdx.x; f < KBB * DP; f += 256) {
+      const int r = f / DP, d = f % DP;
+      const int64_t kk = k0 + r;
+      if (kk < a.T && d < a.D) dst[kk * st + d] = lds[r * LD + d];
+    }
+  }
+}
+
+// ------------------------------------------------------- backward B: dQ
+template <typename T, int DP>
+__global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnArgs a) {
+  using M = AM<T>;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  constexpr int KB = 2 * MT;
+  constexpr int QB = 4 * MT;
+  constexpr int STAGE = (2 * KB * LD > QB * LD) ? 2 * KB * LD : QB * LD;
+  __shared__ __attribute__((aligned(16))) T lds[STAGE];
+  T* Ks = lds;
+  T* Vs = lds + KB * LD;
+
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int64_t q0 = (int64_t)blockIdx.x * QB;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / MT, c = lane % MT;
+  const int64_t qr = q0 + wave * MT + c;
+  const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+  const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+  const T* V = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+  const T* G = (const T*)a.dO + b * a.sdo.b + h * a.sdo.h;
+  const T scale = (T)a.scale;
+  const bool vec = a.vec != 0;
+  const bool qok = qr < a.T;
+  const T mq = qok ? ((const T*)a.rowmax)[bh * a.T + qr] : T(0);
+  const T lq = qok ? ((const T*)a.rowsum)[bh * a.T + qr] : T(1);
+  const T dq_r = qok ? ((const T*)a.drow)[bh * a.T + qr] : T(0);
+
+  typename M::vec_t qf[DP / 8], gf[DP / 8];
+  load_frag_rows<T, DP>(qf, Q, a.sq.t, qr, a.T, a.D, g, vec);
+  load_frag_rows<T, DP>(gf, G, a.sdo.t, qr, a.T, a.D, g, vec);
+  typename M::acc_t dq[DP / MT];
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt) dq[dt] = typename M::acc_t(0);
+
+  const int64_t qmax = (q0 + QB < a.T ? q0 + QB : a.T) - 1;
+  const int64_t nkb = q0 < a.T ? qmax / KB + 1 : 0;
+  for (int64_t kb = 0; kb < nkb; ++kb) {
+    const int64_t k0 = kb * KB;
+    __syncthreads();
+    load_rows<T, KB, DP>(Ks, K, a.sk.t, k0, a.T, a.D, vec);
+    load_rows<T, KB, DP>(Vs, V, a.sv.t, k0, a.T, a.D, vec);
+    __syncthreads();
+#pragma unroll
+    for (int jt = 0; jt < KB / MT; ++jt) {
+      // S^T(j, r), dP^T(j, r): rows j = keys (LDS), columns r = this wave's queries
+      typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Ks, jt * MT, qf, g, c);
+      typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Vs, jt * MT, gf, g, c);
+#pragma unroll
+      for (int i = 0; i < NACC; ++i) {
+        const int64_t j = k0 + jt * MT + M::row(i, g);
+        const bool live = j <= qr && qok && j < a.T;
+        const T p = live ? exp(s[i] * scale - mq) / lq : T(0);
+        dp[i] = p * (dp[i] - dq_r);
+      }
+      // dQ^T += K^T dS^T
+      mma_lds_t_regs<T, DP>(dq, Ks, jt * MT, dp, g, c);
+    }
+  }
+  __syncthreads();
+  T* Ws = lds + wave * MT * LD;
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt)
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) Ws[c * LD + dt * MT + M::row(i, g)] = dq[dt][i] * scale;
+  __syncthreads();
+  T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h;
+  for (int f = threadIdx.x; f < QB * DP; f += 256) {
+    const int r = f / DP, d = f % DP;
+    const int64_t qq = q0 + r;
+    if (qq < a.T && d < a.D) DQ[qq * a.sdq.t + d] = lds[r * LD + d];
+  }
+}
+
+// ----------------------------------------------------------------- host
+static bool strides_vec(const Strides3& s, int64_t vec) { return s.b % vec == 0 && s.h % vec == 0 && s.t % vec == 0; }
+
+template <typename T>
+static int pick_dp(int64_t D) {
+  constexpr int MT = AM<T>::MT;
+  for (int dp : {16, 32, 64})
+    if (dp >= MT && D <= dp) return dp;
+  return -1;
+}
+
+#define DP_SWITCH(dp, KERNEL, T, grid)                                     \
+  switch (dp) {                                                            \
+    case 16: KERNEL<T, (sizeof(T) == 8 ? 16 : 32)><<<grid, 256, 0, stream()>>>(a); break; \
+    case 32: KERNEL<T, 32><<<grid, 256, 0, stream()>>>(a); break;          \
+    default: KERNEL<T, 64><<<grid, 256, 0, stream()>>>(a); break;         \
+  }
+
+template <typename T>
+static int attn_fwd_impl(AttnArgs& a) {
+  constexpr int MT = AM<T>::MT;
+  const int dp = pick_dp<T>(a.D);
+  DTMI_CHECK(dp > 0, "dtmi_attn_fwd: head dimension %lld > 64 is not supported", (long long)a.D);
+  dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
+  // causal-exact FLOP: 2 GEMMs of 2*D*T(T+1)/2 per (b, h)
+  TimedLaunch tl(DTMI_FAM_ATTN_FWD, 2.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
+  DP_SWITCH(dp, attn_fwd_kernel, T, grid)
+  LAUNCH_CHECK("attn_fwd_kernel");
+  return DTMI_OK;
+}
+
+template <typename T>
+static int attn_bwd_impl(AttnArgs& a) {
+  constexpr int MT = AM<T>::MT;
+  const int dp = pick_dp<T>(a.D);
+  DTMI_CHECK(dp > 0, "dtmi_attn_bwd: head dimension %lld > 64 is not supported", (long long)a.D);
+  const int64_t rows = a.B * a.H * a.T;
+  void* drow = nullptr;
+  int rc = pool_alloc(&drow, (size_t)rows * sizeof(T));
+  if (rc) return rc;
+  a.drow = drow;
+  {
+    // causal-exact FLOP of the 5 backward GEMMs (S recompute, dV, dP, dQ, dK)
+    TimedLaunch tl(DTMI_FAM_ATTN_BWD, 5.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
+    attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
+    dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
+    DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
+    DP_SWITCH(dp, attn_bwd_q_kernel, T, grid)
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(drow);
+  if (le != hipSuccess) return fail_hip(le, "attention backward kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+}
+
+static Strides3 s3(const int64_t* s) { return Strides3{s[0], s[1], s[2]}; }
+
+}  // namespace dtmi
+
+using namespace dtmi;
+
+DTMI_EXPORT int dtmi_attn_fwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
+                              const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                              const int64_t* v_strides, void* o, const int64_t* o_strides, void* rowmax,
+                              void* rowsum) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(B >= 0 && H >= 0 && T >= 0 && D > 0 && B * H < 65536, "dtmi_attn_fwd: bad shape (B*H must be < 65536)");
+  if (B * H * T == 0) return DTMI_OK;
+  DTMI_CHECK(q && k && v && o && rowmax && rowsum && q_strides && k_strides && v_strides && o_strides,
+             "dtmi_attn_fwd: NULL pointer");
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = o;
+  a.rowmax = rowmax;
+  a.rowsum = rowsum;
+  a.sq = s3(q_strides);
+  a.sk = s3(k_strides);
+  a.sv = s3(v_strides);
+  a.so = s3(o_strides);
+  a.B = B;
+  a.H = H;
+  a.T = T;
+  a.D = D;
+  a.scale = scale;
+  const int64_t vecn = dtype == DTMI_F32 ? 4 : 2;
+  a.vec = (D % vecn == 0 && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && strides_vec(a.sq, vecn) &&
+           strides_vec(a.sk, vecn) && strides_vec(a.sv, vecn))
+              ? 1
+              : 0;
+  if (dtype == DTMI_F32) return attn_fwd_impl<float>(a);
+  return attn_fwd_impl<double>(a);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
+                              const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                              const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dO,
+                              const int64_t* dO_strides, const void* rowmax, const void* rowsum, void* dq,
+                              const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                              const int64_t* dv_strides) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(B >= 0 && H >= 0 && T >= 0 && D > 0 && B * H < 65536, "dtmi_attn_bwd: bad shape (B*H must be < 65536)");
+  if (B * H * T == 0) return DTMI_OK;
+  DTMI_CHECK(q && k && v && o && dO && rowmax && rowsum && dq && dk && dv, "dtmi_attn_bwd: NULL pointer");
+  DTMI_CHECK(q_strides && k_strides && v_strides && o_strides && dO_strides && dq_strides && dk_strides && dv_strides,
+             "dtmi_attn_bwd: NULL strides");
+  AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.dO = dO;
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.rowmax = (void*)rowmax;
+  a.rowsum = (void*)rowsum;
+  a.sq = s3(q_strides);
+  a.sk = s3(k_strides);
+  a.sv = s3(v_strides);
+  a.so = s3(o_strides);
+  a.sdo = s3(dO_strides);
+  a.sdq = s3(dq_strides);
+  a.sdk = s3(dk_strides);
+  a.sdv = s3(dv_strides);
+  a.B = B;
+  a.H = H;
+  a.T = T;
+  a.D = D;
+  a.scale = scale;
+  const int64_t vecn = dtype == DTMI_F32 ? 4 : 2;
+  a.vec = (D % vecn == 0 && aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(dO, 16) &&
+           strides_vec(a.sq, vecn) && strides_vec(a.sk, vecn) && strides_vec(a.sv, vecn) &&
+           strides_vec(a.sdo, vecn))
+              ? 1
+              : 0;
+  if (dtype == DTMI_F32) return attn_bwd_impl<float>(a);
+  return attn_bwd_impl<double>(a);
+  DTMI_BODY_END
+}

@@ -423,3 +423,48 @@ def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, 
     db = empty((N,), x2.dtype) if need_db else None
     _c("dtmi_linear_bwd_dw", dt, dw.ptr, db.ptr if db is not None else None, x2.ptr, dy2.ptr, M, K, N, 0)
     return dx, dw, db
+
+
+# --------------------------------------------------------------- attention
+def _bht_strides(x: DeviceArray):
+    """(b, h, t) element strides of a (B, H, T, D) view whose last axis is contiguous."""
+    if x.ndim != 4 or (x.shape[3] > 1 and x.strides[3] != 1):
+        raise ValueError("attention operands must be (B, H, T, D) views with contiguous D")
+    return _lib.i64_array(x.strides[:3])
+
+
+def attn_fwd(q: DeviceArray, k: DeviceArray, v: DeviceArray, out: DeviceArray | None = None, scale=None):
+    """Causal attention over (B, H, T, D) views. Returns (o, rowmax, rowsum);
+    `out` may be a strided (B, H, T, D) view to write into."""
+    if not (q.shape == k.shape == v.shape):
+        raise ValueError("q, k, v shapes differ")
+    B, H, T, D = q.shape
+    dt = _dt(q, k, v)
+    if out is None:
+        out = empty(q.shape, q.dtype)
+    if out.shape != q.shape:
+        raise ValueError("attn_fwd: bad output")
+    rowmax = empty((B, H, T), q.dtype)
+    rowsum = empty((B, H, T), q.dtype)
+    s = float(1.0 / np.sqrt(D)) if scale is None else float(scale)
+    _c("dtmi_attn_fwd", dt, B, H, T, D, s, q.ptr, _bht_strides(q), k.ptr, _bht_strides(k), v.ptr, _bht_strides(v),
+       out.ptr, _bht_strides(out), rowmax.ptr, rowsum.ptr)
+    return out, rowmax, rowsum
+
+
+def attn_bwd(q, k, v, o, dO, rowmax, rowsum, dq=None, dk=None, dv=None, scale=None):
+    """Returns (dq, dk, dv); each may be passed as a (B, H, T, D) view to fill."""
+    B, H, T, D = q.shape
+    for x in (k, v, o, dO):
+        if x.shape != q.shape:
+            raise ValueError("attn_bwd: operand shapes differ")
+    dt = _dt(q, k, v, o, dO, rowmax, rowsum)
+    _contig(rowmax, rowsum)
+    dq = dq if dq is not None else empty(q.shape, q.dtype)
+    dk = dk if dk is not None else empty(q.shape, q.dtype)
+    dv = dv if dv is not None else empty(q.shape, q.dtype)
+    s = float(1.0 / np.sqrt(D)) if scale is None else float(scale)
+    _c("dtmi_attn_bwd", dt, B, H, T, D, s, q.ptr, _bht_strides(q), k.ptr, _bht_strides(k), v.ptr, _bht_strides(v),
+       o.ptr, _bht_strides(o), dO.ptr, _bht_strides(dO), rowmax.ptr, rowsum.ptr, dq.ptr, _bht_strides(dq), dk.ptr,
+       _bht_strides(dk), dv.ptr, _bht_strides(dv))
+    return dq, dk, dv

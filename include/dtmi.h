@@ -248,6 +248,24 @@ int dtmi_linear_bwd_dx(int dtype, void* dX, const void* dY, const void* W, int64
 int dtmi_linear_bwd_dw(int dtype, void* dW, void* db, const void* X, const void* dY, int64_t M, int64_t K, int64_t N,
                        int accumulate);
 
+/* ------------------------------------------------------- causal attention
+ * dtrain/autograd.py:226-247: o = softmax(q k^T * scale + causal mask) v over
+ * (B, H, T, D), D <= 64 contiguous; each *_strides argument points at three
+ * element strides (b, h, t) of that operand, so q/k/v/o/dq/dk/dv may be views
+ * into fused [B, T, 3, H, D] / [B, T, H, D] buffers. The forward writes o and
+ * the per-row max and sum of exp (rowmax/rowsum, contiguous [B, H, T]); the
+ * backward recomputes the probabilities from them and writes dq, dk, dv
+ * (dtrain keeps the full probability tensor instead). */
+int dtmi_attn_fwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
+                  const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                  const int64_t* v_strides, void* o, const int64_t* o_strides, void* rowmax, void* rowsum);
+int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
+                  const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                  const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dO,
+                  const int64_t* dO_strides, const void* rowmax, const void* rowsum, void* dq,
+                  const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                  const int64_t* dv_strides);
+
 #ifdef __cplusplus
 }
 #endif

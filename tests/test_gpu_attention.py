@@ -1,0 +1,92 @@
+"""Causal attention (flash-style forward + recompute backward, MFMA) on the GPU
+against the oracle restatement of dtrain's causal_attention.
+
+Bar: float64 normwise relative error <= 1e-12; float32 <= 1e-5 (dtrain itself
+computes the float32 case in float64 under NumPy 2; the oracle reproduces that).
+"""
+import numpy as np
+import pytest
+
+from helpers import rel_err
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+TOL = {np.float64: 1e-12, np.float32: 1e-5}
+
+
+def _dev():
+    from dtmi import device as D, kernels as K
+    return D, K
+
+
+def _check(D, K, q, k, v, g, dt):
+    o_ref, p, scale = ops.attention_fwd(q, k, v)
+    gq, gk, gv = ops.attention_bwd(g, q, k, v, p, scale)
+    m_ref, l_ref = ops.row_stats(q, k)
+    dq_, dk_, dv_ = D.from_numpy(q), D.from_numpy(k), D.from_numpy(v)
+    o, rmax, rsum = K.attn_fwd(dq_, dk_, dv_)
+    assert rel_err(o.numpy(), o_ref) <= TOL[dt]
+    assert rel_err(rmax.numpy(), m_ref) <= TOL[dt]
+    assert rel_err(rsum.numpy(), l_ref) <= TOL[dt]
+    gq_d, gk_d, gv_d = K.attn_bwd(dq_, dk_, dv_, o, D.from_numpy(g), rmax, rsum)
+    assert rel_err(gq_d.numpy(), gq) <= TOL[dt]
+    assert rel_err(gk_d.numpy(), gk) <= TOL[dt]
+    assert rel_err(gv_d.numpy(), gv) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("shape", [(1, 2, 4, 3), (1, 2, 8, 4), (2, 2, 5, 4), (8, 4, 32, 16), (2, 3, 100, 64),
+                                   (1, 1, 257, 33), (16, 12, 256, 64)])
+def test_attention_forward_backward(dev, dt, shape):
+    D, K = _dev()
+    rng = np.random.default_rng(sum(shape))
+    q, k, v, g = (rng.standard_normal(shape).astype(dt) for _ in range(4))
+    _check(D, K, q, k, v, g, dt)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_attention_golden_from_dtrain(dev, golden, dt):
+    D, K = _dev()
+    G = golden("dtrain_attention.npz")
+    key = np.dtype(dt).name
+    q, k, v, g = (G[f"{key}/{s}"] for s in "qkvg")
+    o, rmax, rsum = K.attn_fwd(D.from_numpy(q), D.from_numpy(k), D.from_numpy(v))
+    assert rel_err(o.numpy(), G[f"{key}/o"]) <= TOL[dt]
+    gq, gk, gv = K.attn_bwd(D.from_numpy(q), D.from_numpy(k), D.from_numpy(v), o, D.from_numpy(g), rmax, rsum)
+    assert rel_err(gq.numpy(), G[f"{key}/gq"]) <= TOL[dt]
+    assert rel_err(gk.numpy(), G[f"{key}/gk"]) <= TOL[dt]
+    assert rel_err(gv.numpy(), G[f"{key}/gv"]) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_attention_on_fused_qkv_layout(dev, dt):
+    """q, k, v as strided views of a [B, T, 3, H, D] projection output (the
+    reshape/transpose/split of dtrain/nn.py:100-103), outputs written into
+    [B, T, H, D] and [B, T, 3, H, D] buffers."""
+    D, K = _dev()
+    B, T, H, Dh = 2, 96, 3, 16
+    rng = np.random.default_rng(4)
+    qkv = rng.standard_normal((B, T, 3, H, Dh)).astype(dt)
+    g = rng.standard_normal((B, T, H, Dh)).astype(dt)
+    q, k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
+    gh = np.ascontiguousarray(g.transpose(0, 2, 1, 3))
+    o_ref, p, scale = ops.attention_fwd(q, k, v)
+    gq, gk, gv = ops.attention_bwd(gh, q, k, v, p, scale)
+
+    dqkv = D.from_numpy(qkv)
+    t5 = dqkv.transpose(2, 0, 3, 1, 4)  # [3, B, H, T, D] view
+    qd, kd, vd = t5[0], t5[1], t5[2]
+    assert not qd.is_contiguous
+    obuf = D.empty((B, T, H, Dh), dt)
+    o, rmax, rsum = K.attn_fwd(qd, kd, vd, out=obuf.transpose(0, 2, 1, 3))
+    assert rel_err(obuf.numpy().transpose(0, 2, 1, 3), o_ref) <= TOL[dt]
+    gbuf = D.from_numpy(g)
+    dbuf = D.full((B, T, 3, H, Dh), 7.0, dt)
+    d5 = dbuf.transpose(2, 0, 3, 1, 4)
+    K.attn_bwd(qd, kd, vd, obuf.transpose(0, 2, 1, 3), gbuf.transpose(0, 2, 1, 3), rmax, rsum,
+               dq=d5[0], dk=d5[1], dv=d5[2])
+    got = dbuf.numpy()
+    assert rel_err(got[:, :, 0].transpose(0, 2, 1, 3), gq) <= TOL[dt]
+    assert rel_err(got[:, :, 1].transpose(0, 2, 1, 3), gk) <= TOL[dt]
+    assert rel_err(got[:, :, 2].transpose(0, 2, 1, 3), gv) <= TOL[dt]
