@@ -1,0 +1,300 @@
+"""Reverse-mode autograd over device arrays, with dtrain's Tensor API.
+
+Mirrors dtrain/autograd.py: `Tensor(data, requires_grad, name)`, `.grad`,
+`.backward(grad=None)`, `.register_grad_ready_hook(fn)`, the operators
+`+ - * @`, `.sum .mean .reshape .transpose .gelu .relu`, and the functional ops
+`embedding`, `layer_norm`, `causal_attention`, `cross_entropy`, `no_grad`.
+
+Differences from dtrain are in where the numbers live, not in semantics:
+`.data` and `.grad` are DeviceArrays (HBM buffers owned by libdtmi; `.numpy()`
+and `np.asarray` copy to the host), and every op's forward and backward is a
+libdtmi kernel launch. `backward()` is dtrain's algorithm (autograd.py:151-195):
+a topological order, a reverse walk, leaf accumulation `grad = g` or
+`grad + g`, and grad-ready hooks called once per leaf with its final gradient.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import device as dev
+from . import kernels as K
+from .device import DeviceArray
+
+_grad_enabled = True
+
+
+class no_grad:
+    """dtrain/autograd.py:19-26."""
+
+    def __enter__(self):
+        global _grad_enabled
+        self.prev, _grad_enabled = _grad_enabled, False
+
+    def __exit__(self, *a):
+        global _grad_enabled
+        _grad_enabled = self.prev
+
+
+def _contig(x: DeviceArray) -> DeviceArray:
+    return x if x.is_contiguous else x.contiguous()
+
+
+def _unbroadcast(g: DeviceArray, shape: tuple) -> DeviceArray:
+    """dtrain/autograd.py:29-36: sum g over the axes broadcast from `shape`."""
+    shape = tuple(shape)
+    if g.shape == shape:
+        return g
+    lead = g.ndim - len(shape)
+    if lead > 0:
+        g = _contig(g)
+        rest = g.shape[lead:]
+        if len(rest) == 1:  # [.., N] -> [N]: deterministic two-stage column sum
+            g = K.colsum(g.reshape(-1, rest[0]))
+        else:
+            g = K.reduce_sum(g, list(range(lead)))
+    axes = [i for i, s in enumerate(shape) if s == 1 and g.shape[i] != 1]
+    if axes:
+        g = K.reduce_sum(g, axes, keepdims=True)
+    return g
+
+
+def _broadcast_to(g: DeviceArray, shape) -> DeviceArray:
+    """np.broadcast_to(g, shape).copy() on the device."""
+    shape = tuple(shape)
+    out = dev.empty(shape, g.dtype)
+    if out.size == 0:
+        return out
+    nd = len(shape)
+    pad = nd - g.ndim
+    st = [0] * pad + [0 if (s == 1 and shape[pad + i] != 1) else g.strides[i] for i, s in enumerate(g.shape)]
+    view = DeviceArray(g.block, shape, g.dtype, g.offset, st)
+    K.copy_into(out, view)
+    return out
+
+
+class Tensor:
+    __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "_hooks", "name", "__weakref__")
+
+    def __init__(self, data, requires_grad=False, _parents=(), _backward=None, name=None):
+        self.data = data if isinstance(data, DeviceArray) else dev.asarray(np.asarray(data))
+        self.grad = None
+        self.requires_grad = requires_grad
+        self._parents = _parents
+        self._backward = _backward
+        self._hooks = []
+        self.name = name
+
+    # ------------------------------------------------------------ utilities
+    @property
+    def shape(self):
+        return self.data.shape
+
+    @property
+    def dtype(self):
+        return self.data.dtype
+
+    def numpy(self):
+        return self.data.numpy()
+
+    def register_grad_ready_hook(self, fn):
+        """fn(tensor) is called once this leaf's gradient is complete."""
+        self._hooks.append(fn)
+
+    def __repr__(self):
+        return f"Tensor(shape={self.shape}, dtype={self.dtype}, requires_grad={self.requires_grad})"
+
+    @staticmethod
+    def _make(data, parents, backward):
+        rg = _grad_enabled and any(p.requires_grad for p in parents)
+        return Tensor(data, rg, parents if rg else (), backward if rg else None)
+
+    def _wrap(self, o):
+        return o if isinstance(o, Tensor) else Tensor(np.asarray(o, dtype=self.dtype))
+
+    # ---------------------------------------------------------------- ops
+    def __add__(self, o):
+        a, b = self, self._wrap(o)
+
+        def bw(g):
+            return _unbroadcast(g, a.shape), _unbroadcast(g, b.shape)
+        return Tensor._make(K.binary("add", a.data, b.data), (a, b), bw)
+
+    __radd__ = __add__
+
+    def __neg__(self):
+        return Tensor._make(K.neg(self.data), (self,), lambda g: (K.neg(g),))
+
+    def __sub__(self, o):
+        return self + (-self._wrap(o))
+
+    def __mul__(self, o):
+        a, b = self, self._wrap(o)
+
+        def bw(g):
+            return (_unbroadcast(K.binary("mul", g, b.data), a.shape),
+                    _unbroadcast(K.binary("mul", g, a.data), b.shape))
+        return Tensor._make(K.binary("mul", a.data, b.data), (a, b), bw)
+
+    __rmul__ = __mul__
+
+    def __matmul__(self, o):
+        a, b = self, o
+        A, B = _contig(a.data), _contig(b.data)
+        if A.ndim >= 2 and B.ndim == 2:
+            lead = A.shape[:-1]
+            y = K.gemm(A.reshape(-1, A.shape[-1]), B).reshape(*lead, B.shape[1])
+
+            def bw(g):
+                g2 = _contig(g).reshape(-1, B.shape[1])
+                A2 = A.reshape(-1, A.shape[-1])
+                ga = K.gemm(g2, B, a_kcontig=True, b_kcontig=True).reshape(A.shape)  # g @ b^T
+                gb = K.gemm(A2, g2, a_kcontig=False, b_kcontig=False)               # sum_batch a^T @ g
+                return ga, gb
+        elif A.ndim == 3 and B.ndim == 3 and A.shape[0] == B.shape[0]:
+            y = K.gemm(A, B)
+
+            def bw(g):
+                gc = _contig(g)
+                return K.gemm(gc, B, a_kcontig=True, b_kcontig=True), K.gemm(A, gc, a_kcontig=False, b_kcontig=False)
+        else:
+            raise NotImplementedError(f"matmul of shapes {A.shape} @ {B.shape}")
+        return Tensor._make(y, (a, b), bw)
+
+    def sum(self, axis=None, keepdims=False):
+        a = self
+        nd = a.data.ndim
+        axes = list(range(nd)) if axis is None else [axis] if isinstance(axis, int) else list(axis)
+        axes = [x % nd for x in axes] if nd else []
+        out = K.reduce_sum(_contig(a.data), axes, keepdims=keepdims)
+
+        def bw(g):
+            if axis is not None and not keepdims:
+                g = _contig(g).reshape(tuple(1 if d in axes else s for d, s in enumerate(a.shape)))
+            return (_broadcast_to(g, a.shape),)
+        return Tensor._make(out, (a,), bw)
+
+    def mean(self, axis=None, keepdims=False):
+        n = self.data.size if axis is None else self.data.shape[axis]
+        return self.sum(axis, keepdims) * (1.0 / n)
+
+    def reshape(self, *shape):
+        a = self
+        return Tensor._make(a.data.reshape(*shape), (a,), lambda g: (g.reshape(a.shape),))
+
+    def transpose(self, *axes):
+        a = self
+        inv = tuple(np.argsort(axes))
+        return Tensor._make(a.data.transpose(*axes), (a,), lambda g: (g.transpose(*inv),))
+
+    def gelu(self):
+        x = _contig(self.data)
+
+        def bw(g):
+            return (K.gelu_bwd(x, _contig(g)),)
+        return Tensor._make(K.gelu_fwd(x), (self,), bw)
+
+    def relu(self):
+        x = _contig(self.data)
+        return Tensor._make(K.relu_fwd(x), (self,), lambda g: (K.relu_bwd(x, _contig(g)),))
+
+    # ------------------------------------------------------------ backward
+    def backward(self, grad=None):
+        """dtrain/autograd.py:151-195 over device gradients."""
+        if grad is None:
+            if self.data.size != 1:
+                raise ValueError("backward() without a gradient needs a scalar output")
+            grad = dev.full(self.data.shape, 1.0, self.data.dtype)
+        elif not isinstance(grad, DeviceArray):
+            grad = dev.asarray(np.asarray(grad, dtype=self.dtype))
+        order, seen, users = [], set(), {}
+        stack = [(self, False)]
+        while stack:
+            node, done = stack.pop()
+            if done:
+                order.append(node)
+                continue
+            if id(node) in seen:
+                continue
+            seen.add(id(node))
+            stack.append((node, True))
+            for p in node._parents:
+                users[id(p)] = users.get(id(p), 0) + 1
+                if id(p) not in seen:
+                    stack.append((p, False))
+        grads = {id(self): grad}
+        for node in reversed(order):
+            g = grads.pop(id(node), None)
+            if g is None:
+                continue
+            if node._backward is None:
+                if node.requires_grad:
+                    node.grad = g if node.grad is None else K.binary("add", node.grad, g)
+                    for h in node._hooks:
+                        h(node)
+                continue
+            for p, pg in zip(node._parents, node._backward(g)):
+                if not p.requires_grad or pg is None:
+                    continue
+                if tuple(pg.shape) != tuple(p.shape):
+                    raise RuntimeError(f"gradient shape {pg.shape} != {p.shape}")
+                k = id(p)
+                grads[k] = pg if k not in grads else K.binary("add", grads[k], pg)
+        return None
+
+
+# ------------------------------------------------------------ functional ops
+def embedding(weight: Tensor, idx: np.ndarray) -> Tensor:
+    """dtrain/autograd.py:199-204. `idx` is a host integer array."""
+    idx = np.asarray(idx)
+    V = weight.shape[0]
+    if idx.size and (idx.min() < -V or idx.max() >= V):
+        raise IndexError(f"index out of bounds for axis 0 with size {V}")
+    flat = np.where(idx < 0, idx + V, idx).astype(np.int64).reshape(-1)
+    didx = dev.from_numpy(flat)
+    w = weight.data if weight.data.is_contiguous else weight.data.contiguous()
+    out = K.embedding_fwd(w, didx, idx.shape)
+
+    def bw(g):
+        perm, start, row = K.embedding_segments(flat)
+        segs = (dev.from_numpy(perm), dev.from_numpy(start), dev.from_numpy(row))
+        return (K.embedding_bwd(_contig(g).reshape(-1, weight.shape[1]), V, segs),)
+    return Tensor._make(out, (weight,), bw)
+
+
+def layer_norm(x: Tensor, w: Tensor, b: Tensor, eps=1e-5) -> Tensor:
+    """dtrain/autograd.py:207-223."""
+    xd = _contig(x.data)
+    y, mean, rstd = K.layernorm_fwd(xd, _contig(w.data), _contig(b.data), eps)
+
+    def bw(g):
+        return K.layernorm_bwd(_contig(g), xd, _contig(w.data), mean, rstd)
+    return Tensor._make(y, (x, w, b), bw)
+
+
+def causal_attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
+    """dtrain/autograd.py:226-247 for (B, H, T, D) inputs (any strides with a
+    contiguous last axis). Keeps row max/sum instead of the probabilities."""
+    o, rmax, rsum = K.attn_fwd(q.data, k.data, v.data)
+
+    def bw(g):
+        gq = dev.empty(q.shape, q.dtype)
+        gk = dev.empty(q.shape, q.dtype)
+        gv = dev.empty(q.shape, q.dtype)
+        K.attn_bwd(q.data, k.data, v.data, o, _contig(g), rmax, rsum, dq=gq, dk=gk, dv=gv)
+        return gq, gk, gv
+    return Tensor._make(o, (q, k, v), bw)
+
+
+def cross_entropy(logits: Tensor, targets: np.ndarray) -> Tensor:
+    """dtrain/autograd.py:250-266: mean cross-entropy; `targets` is a host array."""
+    z = _contig(logits.data)
+    V = z.shape[-1]
+    t = np.asarray(targets).reshape(-1)
+    if t.size and (t.min() < 0 or t.max() >= V):
+        raise IndexError(f"target out of bounds for {V} classes")
+    dt = dev.from_numpy(t.astype(np.int64))
+    loss, rmax, rsum = K.xent_fwd(z, dt)
+
+    def bw(g):
+        return (K.xent_bwd(z, dt, rmax, rsum, g=_contig(g).reshape(1)),)
+    return Tensor._make(loss, (logits,), bw)

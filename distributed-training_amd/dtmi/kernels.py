@@ -222,13 +222,17 @@ def average_blocks(n: int) -> int:
 
 def bucket_average(out: DeviceArray, replicas: DeviceArray, world: int, inv_w: float,
                    partials: DeviceArray | None = None):
-    """out[i] = fixed rank-order sum of replicas[r, i] times inv_w; replicas is [W, n]."""
-    _contig(out, replicas)
+    """out[i] = fixed rank-order sum of replicas[r, i] times inv_w; replicas is a
+    [W, n] array or a column slice of one (row stride >= n, unit column stride)."""
+    _contig(out)
     if replicas.ndim != 2 or replicas.shape[0] != world or replicas.shape[1] != out.size:
         raise ValueError("bucket_average: replicas must be [world, n]")
+    if replicas.shape[1] > 1 and replicas.strides[1] != 1:
+        raise ValueError("bucket_average: replica rows must be contiguous")
+    stride = replicas.strides[0] if world > 1 else replicas.shape[1]
     if partials is not None and (partials.dtype != np.float64 or partials.size < average_blocks(out.size)):
         raise ValueError("bucket_average: partials too small")
-    _c("dtmi_bucket_average", _dt(out, replicas), out.ptr, replicas.ptr, int(world), out.size, replicas.shape[1],
+    _c("dtmi_bucket_average", _dt(out, replicas), out.ptr, replicas.ptr, int(world), out.size, int(stride),
        float(inv_w), partials.ptr if partials is not None else None, None)
 
 

@@ -1,0 +1,204 @@
+"""Modules with dtrain's API (dtrain/nn.py): Module, Linear, LayerNorm, GPTConfig,
+Block, GPT.
+
+Same parameter order (attribute definition order, depth first), same names,
+same initialisation (one NumPy default_rng(seed), same draw order and std per
+tensor, float64 draws cast to the model dtype), so a dtmi GPT starts from the
+very values a dtrain GPT of the same config and seed holds. After construction
+GPT packs every parameter into one contiguous device buffer in that order
+(`GPT.flat`); each parameter's `.data` is a view into it.
+
+Two ops are fused relative to dtrain's graph without changing the arithmetic:
+Linear runs x @ w + b as one GEMM with the bias added in its epilogue (the add
+node's backward becomes the GEMM's column-sum), and the attention block reads
+q, k, v straight out of the qkv projection and writes its output in [B, T, C]
+order, so the reshape / transpose / split of Block.forward (nn.py:100-103)
+cost no copies and the backward writes d(qkv) in place.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import device as dev
+from . import kernels as K
+from .autograd import Tensor, _contig, cross_entropy, embedding, layer_norm
+
+
+class Module:
+    def parameters(self):
+        """All parameters in a deterministic order (attribute definition order, depth-first)."""
+        out, seen = [], set()
+
+        def walk(m):
+            for v in m.__dict__.values():
+                if isinstance(v, Tensor) and v.requires_grad and id(v) not in seen:
+                    seen.add(id(v))
+                    out.append(v)
+                elif isinstance(v, Module):
+                    walk(v)
+                elif isinstance(v, (list, tuple)):
+                    for x in v:
+                        if isinstance(x, Module):
+                            walk(x)
+        walk(self)
+        return out
+
+    def named_parameters(self):
+        names = {}
+
+        def walk(m, prefix):
+            for k, v in m.__dict__.items():
+                if isinstance(v, Tensor) and v.requires_grad:
+                    names.setdefault(id(v), prefix + k)
+                elif isinstance(v, Module):
+                    walk(v, prefix + k + ".")
+                elif isinstance(v, (list, tuple)):
+                    for i, x in enumerate(v):
+                        if isinstance(x, Module):
+                            walk(x, f"{prefix}{k}.{i}.")
+        walk(self, "")
+        return [(names[id(p)], p) for p in self.parameters()]
+
+    def zero_grad(self):
+        for p in self.parameters():
+            p.grad = None
+
+    def __call__(self, *a, **k):
+        return self.forward(*a, **k)
+
+
+def param(arr, name=None):
+    return Tensor(arr, requires_grad=True, name=name)
+
+
+def linear(x: Tensor, w: Tensor, b: Tensor | None) -> Tensor:
+    """y = x @ w (+ b) for x [..., K], w [K, N], b [N]: one GEMM, bias fused."""
+    X = _contig(x.data)
+    lead = X.shape[:-1]
+    X2 = X.reshape(-1, X.shape[-1])
+    W = w.data
+    y = K.linear_fwd(X2, W, b.data if b is not None else None).reshape(*lead, W.shape[1])
+
+    def bw(g):
+        g2 = _contig(g).reshape(-1, W.shape[1])
+        dx, dw, db = K.linear_bwd(X2, W, g2, need_dx=x.requires_grad, need_db=b is not None)
+        dx = dx.reshape(X.shape) if dx is not None else None
+        return (dx, dw, db) if b is not None else (dx, dw)
+    parents = (x, w, b) if b is not None else (x, w)
+    return Tensor._make(y, parents, bw)
+
+
+def qkv_attention(qkv: Tensor, heads: int) -> Tensor:
+    """Causal self-attention of dtrain's Block (nn.py:100-103) on the fused
+    projection qkv [B, T, 3C]: returns the merged heads [B, T, C]."""
+    B, T, C3 = qkv.shape
+    C = C3 // 3
+    D = C // heads
+    src = _contig(qkv.data)
+    t5 = src.reshape(B, T, 3, heads, D).transpose(2, 0, 3, 1, 4)  # [3, B, H, T, D] view
+    out = dev.empty((B, T, C), qkv.dtype)
+    _, rmax, rsum = K.attn_fwd(t5[0], t5[1], t5[2], out=out.reshape(B, T, heads, D).transpose(0, 2, 1, 3))
+
+    def bw(g):
+        gq = dev.empty((B, T, C3), qkv.dtype)
+        d5 = gq.reshape(B, T, 3, heads, D).transpose(2, 0, 3, 1, 4)
+        gv = _contig(g).reshape(B, T, heads, D).transpose(0, 2, 1, 3)
+        o = out.reshape(B, T, heads, D).transpose(0, 2, 1, 3)
+        K.attn_bwd(t5[0], t5[1], t5[2], o, gv, rmax, rsum, dq=d5[0], dk=d5[1], dv=d5[2])
+        return (gq,)
+    return Tensor._make(out, (qkv,), bw)
+
+
+class Linear(Module):
+    def __init__(self, nin, nout, rng, dtype=np.float32, bias=True, std=0.02):
+        self.w = param((rng.standard_normal((nin, nout)) * std).astype(dtype))
+        self.b = param(np.zeros(nout, dtype)) if bias else None
+
+    def forward(self, x):
+        return linear(x, self.w, self.b)
+
+
+class LayerNorm(Module):
+    def __init__(self, n, dtype=np.float32):
+        self.w = param(np.ones(n, dtype))
+        self.b = param(np.zeros(n, dtype))
+
+    def forward(self, x):
+        return layer_norm(x, self.w, self.b)
+
+
+@dataclass
+class GPTConfig:
+    vocab: int = 65
+    ctx: int = 64
+    dim: int = 128
+    heads: int = 4
+    layers: int = 4
+    dtype: str = "float32"
+
+
+class Block(Module):
+    def __init__(self, c: GPTConfig, rng):
+        dt = np.dtype(c.dtype)
+        self.c = c
+        self.ln1 = LayerNorm(c.dim, dt)
+        self.qkv = Linear(c.dim, 3 * c.dim, rng, dt)
+        self.proj = Linear(c.dim, c.dim, rng, dt, std=0.02 / np.sqrt(2 * c.layers))
+        self.ln2 = LayerNorm(c.dim, dt)
+        self.fc = Linear(c.dim, 4 * c.dim, rng, dt)
+        self.out = Linear(4 * c.dim, c.dim, rng, dt, std=0.02 / np.sqrt(2 * c.layers))
+
+    def forward(self, x):
+        a = qkv_attention(self.qkv(self.ln1(x)), self.c.heads)
+        x = x + self.proj(a)
+        return x + self.out(self.fc(self.ln2(x)).gelu())
+
+
+class GPT(Module):
+    def __init__(self, c: GPTConfig, seed=0):
+        rng = np.random.default_rng(seed)
+        dt = np.dtype(c.dtype)
+        self.c = c
+        self.tok = param((rng.standard_normal((c.vocab, c.dim)) * 0.02).astype(dt))
+        self.pos = param((rng.standard_normal((c.ctx, c.dim)) * 0.01).astype(dt))
+        self.blocks = [Block(c, rng) for _ in range(c.layers)]
+        self.ln = LayerNorm(c.dim, dt)
+        self.head = Linear(c.dim, c.vocab, rng, dt, bias=False)
+        self._pack()
+
+    def _pack(self):
+        """Move every parameter into one contiguous device buffer (forward order)."""
+        params = self.parameters()
+        n = sum(p.data.size for p in params)
+        flat = dev.empty((n,), params[0].dtype)
+        off = 0
+        for p in params:
+            k = p.data.size
+            view = flat[off:off + k].reshape(p.data.shape)
+            K.copy_into(view, p.data)
+            p.data = view
+            off += k
+        self.flat = flat
+
+    def load_numpy(self, arrays: dict):
+        """Set parameters from host arrays keyed by name (e.g. a dtrain state)."""
+        for name, p in self.named_parameters():
+            a = np.asarray(arrays[name], dtype=p.dtype)
+            if a.shape != p.shape:
+                raise ValueError(f"{name}: shape {a.shape} != {p.shape}")
+            p.data.assign(a)
+
+    def state_numpy(self) -> dict:
+        return {name: p.numpy() for name, p in self.named_parameters()}
+
+    def forward(self, idx: np.ndarray, targets: np.ndarray | None = None):
+        B, T = idx.shape
+        x = embedding(self.tok, idx) + embedding(self.pos, np.arange(T))
+        for b in self.blocks:
+            x = b(x)
+        logits = self.head(self.ln(x))
+        if targets is None:
+            return logits
+        return logits, cross_entropy(logits, targets)
