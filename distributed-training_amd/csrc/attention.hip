@@ -162,7 +162,7 @@ __device__ __forceinline__ void mma_lds_t_regs(typename AM<T>::acc_t (&out)[DP /
 
 // ----------------------------------------------------------------- forward
 template <typename T, int DP>
-__global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
   constexpr int KB = 2 * MT;  // keys per LDS block
@@ -174,7 +174,7 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(AttnArgs a) {
 
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh % a.H;
-  const int64_t q0 = (int64_t)blockIdx.x * QB;
+  const int64_t q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
   const int64_t qr = q0 + wave * MT + c;  // this lane's query (column)
@@ -278,7 +278,7 @@ __global__ void __launch_bounds__(256) attn_drow_kernel(AttnArgs a) {
 
 // ------------------------------------------------- backward A: dK and dV
 template <typename T, int DP>
-__global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
   constexpr int QB = 2 * MT;  // queries per LDS block
@@ -324,7 +324,7 @@ __global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnArgs a) {
         stat_d[r] = ok ? DR[qs + r] : T(0);
       }
       __syncthreads();
-#pragma unroll
+#pragma unroll 1
       for (int rt = 0; rt < QB / MT; ++rt) {
         // S(r, j) and dP(r, j): rows r = queries (LDS), columns j = this wave's keys
         typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Qs, rt * MT, kf, g, c);
@@ -368,7 +368,7 @@ __global__ void __launch_bounds__(256) attn_bwd_kv_kernel(AttnArgs a) {
 
 // ------------------------------------------------------- backward B: dQ
 template <typename T, int DP>
-__global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
   constexpr int KB = 2 * MT;
@@ -380,7 +380,7 @@ __global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnArgs a) {
 
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh % a.H;
-  const int64_t q0 = (int64_t)blockIdx.x * QB;
+  const int64_t q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
   const int64_t qr = q0 + wave * MT + c;
@@ -410,7 +410,7 @@ __global__ void __launch_bounds__(256) attn_bwd_q_kernel(AttnArgs a) {
     load_rows<T, KB, DP>(Ks, K, a.sk.t, k0, a.T, a.D, vec);
     load_rows<T, KB, DP>(Vs, V, a.sv.t, k0, a.T, a.D, vec);
     __syncthreads();
-#pragma unroll
+#pragma unroll 1
     for (int jt = 0; jt < KB / MT; ++jt) {
       // S^T(j, r), dP^T(j, r): rows j = keys (LDS), columns r = this wave's queries
       typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Ks, jt * MT, qf, g, c);

@@ -9,6 +9,7 @@
 // 16-byte vector access when aligned, grid-stride loops, no atomics.
 #include <cmath>
 
+#include "colreduce.h"
 #include "common.h"
 
 namespace dtmi {
@@ -234,7 +235,7 @@ __global__ void reduce_axes_kernel(T* __restrict__ out, const T* __restrict__ x,
 // stage 1 block (bx, by) sums rows [by*RB, (by+1)*RB) of columns
 // [bx*256*V, ...) into part[by][col]; stage 2 sums the parts of each column in
 // increasing `by` order. Coalesced: consecutive threads read consecutive columns.
-constexpr int kColRows = 64;
+constexpr int kColRows = 128;
 
 template <typename T>
 __global__ void __launch_bounds__(256) colsum_stage1_kernel(T* __restrict__ part, const T* __restrict__ x,
@@ -244,18 +245,16 @@ __global__ void __launch_bounds__(256) colsum_stage1_kernel(T* __restrict__ part
   const int64_t r0 = (int64_t)blockIdx.y * kColRows;
   const int64_t r1 = r0 + kColRows < rows ? r0 + kColRows : rows;
   T acc = T(0);
-  for (int64_t r = r0; r < r1; ++r) acc = acc + x[r * cols + c];
+  int64_t r = r0;
+  for (; r + 8 <= r1; r += 8) {
+    T v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = x[(r + u) * cols + c];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = acc + v[u];
+  }
+  for (; r < r1; ++r) acc = acc + x[r * cols + c];
   part[(int64_t)blockIdx.y * cols + c] = acc;
-}
-
-template <typename T>
-__global__ void __launch_bounds__(256) colsum_stage2_kernel(T* __restrict__ out, const T* __restrict__ part,
-                                                             int64_t nparts, int64_t cols, int accumulate) {
-  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  T acc = T(0);
-  for (int64_t p = 0; p < nparts; ++p) acc = acc + part[p * cols + c];
-  out[c] = accumulate ? out[c] + acc : acc;
 }
 
 template <typename T>
@@ -524,14 +523,12 @@ DTMI_EXPORT int dtmi_colsum(int dtype, void* out, const void* x, int64_t rows, i
   {
     TimedLaunch tl(DTMI_FAM_OTHER, (double)(rows * cols + cols) * es);
     dim3 g1((unsigned)cdiv(cols, 256), (unsigned)nparts);
-    dim3 g2((unsigned)cdiv(cols, 256));
     if (dtype == DTMI_F32) {
       colsum_stage1_kernel<float><<<g1, 256, 0, stream()>>>((float*)part, (const float*)x, rows, cols);
-      colsum_stage2_kernel<float><<<g2, 256, 0, stream()>>>((float*)out, (const float*)part, nparts, cols, accumulate);
+      launch_colreduce<float>((float*)out, (const float*)part, (int)nparts, cols, accumulate);
     } else {
       colsum_stage1_kernel<double><<<g1, 256, 0, stream()>>>((double*)part, (const double*)x, rows, cols);
-      colsum_stage2_kernel<double><<<g2, 256, 0, stream()>>>((double*)out, (const double*)part, nparts, cols,
-                                                             accumulate);
+      launch_colreduce<double>((double*)out, (const double*)part, (int)nparts, cols, accumulate);
     }
   }
   hipError_t le = hipGetLastError();

@@ -329,13 +329,26 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   a.tiles_n = (int)cdiv(N, kBN);
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
   DTMI_CHECK(tiles < (1LL << 31) && batch < 65536, "dtmi_gemm: problem too large");
-  // split K when the tile grid alone cannot fill the GPU
+  // Split K so that the blocks fill whole waves of the CUs: a grid of b
+  // blocks on C CUs runs ceil(b / C) rounds, so its useful fraction is
+  // b / (C * ceil(b / C)). Take the fewest splits (each split keeps >= 256 of
+  // K) that reach 90 %, else the best one found.
   int splits = 1;
   if (force_splits > 0) {
     splits = force_splits;
   } else {
-    const int64_t want = 2LL * (num_cus() > 0 ? num_cus() : 256);
-    while (tiles * batch * splits * 2 <= want && K / (splits * 2) >= 512 && splits < 16) splits *= 2;
+    const int64_t cus = num_cus() > 0 ? num_cus() : 256;
+    double best = 0.0;
+    for (int s = 1; s <= 16; ++s) {
+      if (s > 1 && K / s < 256) break;
+      const int64_t blocks = tiles * batch * s;
+      const double eff = (double)blocks / (double)(cus * cdiv(blocks, cus));
+      if (eff > best + 1e-9) {
+        best = eff;
+        splits = s;
+      }
+      if (eff >= 0.9) break;
+    }
   }
   constexpr int kBK = kBKT<T>;
   int64_t kps = cdiv(cdiv(K, splits), kBK) * kBK;

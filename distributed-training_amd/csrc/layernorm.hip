@@ -13,6 +13,7 @@
 // bit-reproducible.
 #include <cmath>
 
+#include "colreduce.h"
 #include "common.h"
 
 namespace dtmi {
@@ -113,9 +114,9 @@ __global__ void __launch_bounds__(256) ln_fwd_kernel(T* __restrict__ y, T* __res
 
 // Blocks needed for the deterministic column partials: a function of rows only.
 static int ln_bwd_blocks(int64_t rows) {
-  int64_t b = cdiv(rows, 4 * 8);  // at least 8 rows per wave
+  int64_t b = cdiv(rows, 4 * 2);  // two rows per wave
   if (b < 1) b = 1;
-  return (int)(b < 512 ? b : 512);
+  return (int)(b < 1024 ? b : 1024);
 }
 
 template <typename T, int NV, int VW>
@@ -215,26 +216,6 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
   }
 }
 
-template <typename T>
-__global__ void __launch_bounds__(256) ln_bwd_reduce_kernel(T* __restrict__ dw, T* __restrict__ db,
-                                                             const T* __restrict__ part_dw,
-                                                             const T* __restrict__ part_db, int nparts, int cols,
-                                                             int accumulate) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= cols) return;
-  T a = T(0), b = T(0);
-  for (int p = 0; p < nparts; ++p) {
-    a += part_dw[(int64_t)p * cols + c];
-    b += part_db[(int64_t)p * cols + c];
-  }
-  if (accumulate) {
-    a = dw[c] + a;
-    b = db[c] + b;
-  }
-  dw[c] = a;
-  db[c] = b;
-}
-
 // ---------------------------------------------------------------- dispatch
 template <typename T, int VW>
 struct LnDispatch {
@@ -327,8 +308,8 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
       LN_NV_SWITCH(nv, CALLS)
 #undef CALLS
     }
-    ln_bwd_reduce_kernel<T><<<(unsigned)cdiv(cols, 256), 256, 0, stream()>>>(
-        (T*)dw, (T*)db, pdw, pdb, grid, (int)cols, (accumulate & 2) ? 1 : 0);
+    launch_colreduce<T>((T*)dw, pdw, grid, cols, (accumulate & 2) ? 1 : 0);
+    launch_colreduce<T>((T*)db, pdb, grid, cols, (accumulate & 2) ? 1 : 0);
   }
   hipError_t le = hipGetLastError();
   pool_free(parts);
