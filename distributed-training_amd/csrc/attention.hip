@@ -160,73 +160,154 @@ __device__ __forceinline__ void mma_lds_t_regs(typename AM<T>::acc_t (&out)[DP /
   }
 }
 
+// Base-2 exponential: one v_exp_f32 for float (softmax probabilities need
+// about 1 ulp, which it gives); the accurate library exp2 for double.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ double ex2(double x) { return exp2(x); }
+
+// Registers for one NR x DP tile in flight from global memory (16-byte
+// vectors, 256 threads), stored to LDS [NR][DP + PAD] after the current tile's
+// MFMAs. Rows >= Tn and columns >= D are zero.
+template <typename T, int NR, int DP>
+struct TileFetch {
+  typedef typename AM<T>::vec_t V;
+  static constexpr int VEC = AM<T>::VEC, LD = DP + AM<T>::PAD;
+  static constexpr int TOTAL = NR * DP / VEC;
+  static constexpr int NV = (TOTAL + 255) / 256;
+  V r[NV];
+
+  __device__ __forceinline__ void fetch(const T* __restrict__ base, int64_t rs, int r0, int Tn, int D, bool vec) {
+    const bool full = vec && (r0 + NR <= Tn) && (D == DP);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      if (TOTAL % 256 != 0 && f >= TOTAL) continue;
+      const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
+      const T* src = base + (int64_t)(r0 + rr) * rs + d;
+      if (full) {
+        r[i] = *reinterpret_cast<const V*>(src);
+      } else if (vec) {
+        r[i] = (r0 + rr < Tn && d < D) ? *reinterpret_cast<const V*>(src) : V(0);
+      } else {
+        V x = V(0);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+          if (r0 + rr < Tn && d + e < D) x[e] = src[e];
+        r[i] = x;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(T* __restrict__ lds) const {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      if (TOTAL % 256 != 0 && f >= TOTAL) continue;
+      const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
+      *reinterpret_cast<V*>(lds + rr * LD + d) = r[i];
+    }
+  }
+};
+
+// Write a wave's MT x DP result (held transposed: lane column c = row of the
+// result, register rows = d) through LDS to global rows r0 + (0 .. NROWS).
+template <typename T, int DP, int NROWS>
+__device__ __forceinline__ void store_result(T* __restrict__ lds, const typename AM<T>::acc_t (&acc)[DP / AM<T>::MT],
+                                             T mul, T* __restrict__ dst, int64_t rs, int r0, int Tn, int D, int wave,
+                                             int g, int c) {
+  using M = AM<T>;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  T* Ws = lds + wave * MT * LD;
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt)
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) Ws[c * LD + dt * MT + M::row(i, g)] = acc[dt][i] * mul;
+  __syncthreads();
+  for (int f = threadIdx.x; f < NROWS * DP; f += 256) {
+    const int r = f / DP, d = f % DP;
+    if (r0 + r < Tn && d < D) dst[(int64_t)(r0 + r) * rs + d] = lds[r * LD + d];
+  }
+}
+
 // ----------------------------------------------------------------- forward
+// rowmax is kept in base-2 units: m = log2(e) * max_j (q . k_j * scale).
 template <typename T, int DP>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
-  constexpr int KB = 2 * MT;  // keys per LDS block
+  constexpr int KB = 2 * MT;  // keys per tile
   constexpr int QB = 4 * MT;  // queries per block (MT per wave)
-  constexpr int STAGE = (2 * KB * LD > QB * LD) ? 2 * KB * LD : QB * LD;
-  __shared__ __attribute__((aligned(16))) T lds[STAGE];
-  T* Ks = lds;
-  T* Vs = lds + KB * LD;
+  constexpr int TILE = KB * LD, STAGE = 2 * TILE;
+  constexpr int LDS_N = 2 * STAGE > QB * LD ? 2 * STAGE : QB * LD;
+  __shared__ __attribute__((aligned(16))) T lds[LDS_N];
 
-  const int64_t bh = blockIdx.y;
+  const int bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh % a.H;
-  const int64_t q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
+  const int Tn = (int)a.T, D = (int)a.D;
+  const int q0 = (int)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
-  const int64_t qr = q0 + wave * MT + c;  // this lane's query (column)
+  const int wq0 = q0 + wave * MT;
+  const int qr = wq0 + c;  // this lane's query (column)
   const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
   const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
   const T* V = (const T*)a.v + b * a.sv.b + h * a.sv.h;
-  const T scale = (T)a.scale;
+  const T sl2 = (T)(a.scale * 1.4426950408889634);  // scale * log2(e)
   const T ninf = -INFINITY;
   const bool vec = a.vec != 0;
 
   typename M::vec_t qf[DP / 8];
-  load_frag_rows<T, DP>(qf, Q, a.sq.t, qr, a.T, a.D, g, vec);
-
+  load_frag_rows<T, DP>(qf, Q, a.sq.t, qr, Tn, D, g, vec);
   typename M::acc_t oacc[DP / MT];
 #pragma unroll
   for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] = typename M::acc_t(0);
   T mrow = ninf, lrow = T(0);
 
-  const int64_t qmax = (q0 + QB < a.T ? q0 + QB : a.T) - 1;
-  const int64_t nkb = qmax / KB + 1;
-  for (int64_t kb = 0; kb < nkb; ++kb) {
-    const int64_t k0 = kb * KB;
-    __syncthreads();
-    load_rows<T, KB, DP>(Ks, K, a.sk.t, k0, a.T, a.D, vec);
-    load_rows<T, KB, DP>(Vs, V, a.sv.t, k0, a.T, a.D, vec);
-    __syncthreads();
+  const int qlast = (q0 + QB < Tn ? q0 + QB : Tn) - 1;
+  const int nkb = qlast / KB + 1;
+  TileFetch<T, KB, DP> fk, fv;
+  fk.fetch(K, a.sk.t, 0, Tn, D, vec);
+  fv.fetch(V, a.sv.t, 0, Tn, D, vec);
+  fk.store(lds);
+  fv.store(lds + TILE);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * KB;
+    const T* Ks = lds + (kb & 1) * STAGE;
+    const T* Vs = Ks + TILE;
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      fk.fetch(K, a.sk.t, k0 + KB, Tn, D, vec);
+      fv.fetch(V, a.sv.t, k0 + KB, Tn, D, vec);
+    }
     typename M::acc_t sacc[KB / MT];
 #pragma unroll
-    for (int jt = 0; jt < KB / MT; ++jt) {
-      sacc[jt] = mma_rows_frag<T, DP>(typename M::acc_t(0), Ks, jt * MT, qf, g, c);
-    }
-    // scale, causal mask (key j > query r), block max
+    for (int jt = 0; jt < KB / MT; ++jt) sacc[jt] = mma_rows_frag<T, DP>(typename M::acc_t(0), Ks, jt * MT, qf, g, c);
+    // causal mask only where a key of the tile can exceed a query of the wave
+    const bool mask = (k0 + KB - 1 > wq0) || (k0 + KB > Tn);
     T bmax = ninf;
 #pragma unroll
     for (int jt = 0; jt < KB / MT; ++jt)
 #pragma unroll
       for (int i = 0; i < NACC; ++i) {
-        const int64_t j = k0 + jt * MT + M::row(i, g);
-        T s = sacc[jt][i] * scale;
-        s = (j <= qr && j < a.T) ? s : ninf;
+        T s = sacc[jt][i] * sl2;
+        if (mask) {
+          const int j = k0 + jt * MT + M::row(i, g);
+          s = (j <= qr && j < Tn) ? s : ninf;
+        }
         sacc[jt][i] = s;
         bmax = fmax(bmax, s);
       }
     bmax = group_max(bmax);
     const T mnew = fmax(mrow, bmax);
-    const T alpha = (mnew == ninf) ? T(1) : exp(mrow - mnew);
+    const bool live = mnew != ninf;
+    const T alpha = live ? ex2(mrow - mnew) : T(1);
     T psum = T(0);
 #pragma unroll
     for (int jt = 0; jt < KB / MT; ++jt)
 #pragma unroll
       for (int i = 0; i < NACC; ++i) {
-        const T p = (mnew == ninf) ? T(0) : exp(sacc[jt][i] - mnew);
+        const T p = live ? ex2(sacc[jt][i] - mnew) : T(0);
         sacc[jt][i] = p;
         psum += p;
       }
@@ -237,25 +318,18 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
     for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
 #pragma unroll
     for (int jt = 0; jt < KB / MT; ++jt) mma_lds_t_regs<T, DP>(oacc, Vs, jt * MT, sacc[jt], g, c);
+    if (more) {
+      T* nxt = lds + ((kb + 1) & 1) * STAGE;
+      fk.store(nxt);
+      fv.store(nxt + TILE);
+    }
+    __syncthreads();
   }
-  // normalise and write through LDS: lane holds O^T(d = dt*MT + row(i, g), query c)
-  __syncthreads();
-  T* Os = lds + wave * MT * LD;
-  const T inv = lrow > T(0) ? T(1) / lrow : T(0);
-#pragma unroll
-  for (int dt = 0; dt < DP / MT; ++dt)
-#pragma unroll
-    for (int i = 0; i < NACC; ++i) Os[c * LD + dt * MT + M::row(i, g)] = oacc[dt][i] * inv;
-  __syncthreads();
   T* O = (T*)a.out + b * a.so.b + h * a.so.h;
-  for (int f = threadIdx.x; f < QB * DP; f += 256) {
-    const int r = f / DP, d = f % DP;
-    const int64_t qq = q0 + r;
-    if (qq < a.T && d < a.D) O[qq * a.so.t + d] = lds[r * LD + d];
-  }
-  if (g == 0 && qr < a.T) {
-    ((T*)a.rowmax)[bh * a.T + qr] = mrow;
-    ((T*)a.rowsum)[bh * a.T + qr] = lrow;
+  store_result<T, DP, QB>(lds, oacc, lrow > T(0) ? T(1) / lrow : T(0), O, a.so.t, q0, Tn, D, wave, g, c);
+  if (g == 0 && qr < Tn) {
+    ((T*)a.rowmax)[(int64_t)bh * Tn + qr] = mrow;
+    ((T*)a.rowsum)[(int64_t)bh * Tn + qr] = lrow;
   }
 }
 
@@ -277,93 +351,115 @@ __global__ void __launch_bounds__(256) attn_drow_kernel(AttnArgs a) {
 }
 
 // ------------------------------------------------- backward A: dK and dV
+// One block owns 4*MT keys (MT per wave, as the columns of its tiles) and walks
+// the query tiles of MT rows that can see them, double-buffered.
 template <typename T, int DP>
 __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
-  constexpr int QB = 2 * MT;  // queries per LDS block
-  constexpr int KBB = 4 * MT;  // keys per block (MT per wave)
-  constexpr int STAGE = (2 * QB * LD > KBB * LD) ? 2 * QB * LD : KBB * LD;
-  __shared__ __attribute__((aligned(16))) T lds[STAGE];
-  __shared__ T stat_m[QB], stat_l[QB], stat_d[QB];
-  T* Qs = lds;
-  T* Gs = lds + QB * LD;
+  constexpr int QT = MT;      // queries per tile
+  constexpr int KBB = 4 * MT;  // keys per block
+  constexpr int TILE = QT * LD, STAGE = 2 * TILE;
+  constexpr int LDS_N = 2 * STAGE > KBB * LD ? 2 * STAGE : KBB * LD;
+  __shared__ __attribute__((aligned(16))) T lds[LDS_N];
+  __shared__ T stats[2][3][QT];
 
-  const int64_t bh = blockIdx.y;
+  const int bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh % a.H;
-  const int64_t k0 = (int64_t)blockIdx.x * KBB;
+  const int Tn = (int)a.T, D = (int)a.D;
+  const int k0 = (int)blockIdx.x * KBB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
-  const int64_t kj = k0 + wave * MT + c;  // this lane's key (column)
+  const int wk0 = k0 + wave * MT;
+  const int kj = wk0 + c;  // this lane's key (column)
   const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
   const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
   const T* V = (const T*)a.v + b * a.sv.b + h * a.sv.h;
   const T* G = (const T*)a.dO + b * a.sdo.b + h * a.sdo.h;
-  const T* RM = (const T*)a.rowmax + bh * a.T;
-  const T* RS = (const T*)a.rowsum + bh * a.T;
-  const T* DR = (const T*)a.drow + bh * a.T;
-  const T scale = (T)a.scale;
+  const T* RM = (const T*)a.rowmax + (int64_t)bh * Tn;
+  const T* RS = (const T*)a.rowsum + (int64_t)bh * Tn;
+  const T* DR = (const T*)a.drow + (int64_t)bh * Tn;
+  const T sl2 = (T)(a.scale * 1.4426950408889634);
   const bool vec = a.vec != 0;
 
   typename M::vec_t kf[DP / 8], vf[DP / 8];
-  load_frag_rows<T, DP>(kf, K, a.sk.t, kj, a.T, a.D, g, vec);
-  load_frag_rows<T, DP>(vf, V, a.sv.t, kj, a.T, a.D, g, vec);
+  load_frag_rows<T, DP>(kf, K, a.sk.t, kj, Tn, D, g, vec);
+  load_frag_rows<T, DP>(vf, V, a.sv.t, kj, Tn, D, g, vec);
   typename M::acc_t dk[DP / MT], dv[DP / MT];
 #pragma unroll
   for (int dt = 0; dt < DP / MT; ++dt) dk[dt] = dv[dt] = typename M::acc_t(0);
 
-  if (k0 < a.T) {
-    for (int64_t qs = (k0 / QB) * QB; qs < a.T; qs += QB) {
-      __syncthreads();
-      load_rows<T, QB, DP>(Qs, Q, a.sq.t, qs, a.T, a.D, vec);
-      load_rows<T, QB, DP>(Gs, G, a.sdo.t, qs, a.T, a.D, vec);
-      for (int r = threadIdx.x; r < QB; r += 256) {
-        const bool ok = qs + r < a.T;
-        stat_m[r] = ok ? RM[qs + r] : T(0);
-        stat_l[r] = ok ? RS[qs + r] : T(1);
-        stat_d[r] = ok ? DR[qs + r] : T(0);
-      }
-      __syncthreads();
-#pragma unroll 1
-      for (int rt = 0; rt < QB / MT; ++rt) {
-        // S(r, j) and dP(r, j): rows r = queries (LDS), columns j = this wave's keys
-        typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Qs, rt * MT, kf, g, c);
-        typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Gs, rt * MT, vf, g, c);
-#pragma unroll
-        for (int i = 0; i < NACC; ++i) {
-          const int rl = rt * MT + M::row(i, g);
-          const int64_t r = qs + rl;
-          const bool live = kj <= r && r < a.T && kj < a.T;
-          const T p = live ? exp(s[i] * scale - stat_m[rl]) / stat_l[rl] : T(0);
-          s[i] = p;
-          dp[i] = p * (dp[i] - stat_d[rl]);
-        }
-        // dV^T += dO^T P ; dK^T += Q^T dS
-        mma_lds_t_regs<T, DP>(dv, Gs, rt * MT, s, g, c);
-        mma_lds_t_regs<T, DP>(dk, Qs, rt * MT, dp, g, c);
-      }
+  const int qs0 = (k0 / QT) * QT;
+  const int nqt = k0 < Tn ? (Tn - qs0 + QT - 1) / QT : 0;
+  TileFetch<T, QT, DP> fq, fg;
+  T st0 = T(0), st1 = T(1), st2 = T(0);
+  auto fetch_stats = [&](int qs) {
+    if (threadIdx.x < QT) {
+      const int r = qs + threadIdx.x;
+      const bool ok = r < Tn;
+      st0 = ok ? RM[r] : T(0);
+      st1 = ok ? RS[r] : T(1);
+      st2 = ok ? DR[r] : T(0);
     }
+  };
+  auto store_stats = [&](int stage) {
+    if (threadIdx.x < QT) {
+      stats[stage][0][threadIdx.x] = st0;
+      stats[stage][1][threadIdx.x] = st1;
+      stats[stage][2][threadIdx.x] = st2;
+    }
+  };
+  if (nqt > 0) {
+    fq.fetch(Q, a.sq.t, qs0, Tn, D, vec);
+    fg.fetch(G, a.sdo.t, qs0, Tn, D, vec);
+    fetch_stats(qs0);
+    fq.store(lds);
+    fg.store(lds + TILE);
+    store_stats(0);
   }
-  // write dK (scaled) and dV through LDS
+  __syncthreads();
+  for (int it = 0; it < nqt; ++it) {
+    const int qs = qs0 + it * QT;
+    const int cur = it & 1;
+    const T* Qs = lds + cur * STAGE;
+    const T* Gs = Qs + TILE;
+    const bool more = it + 1 < nqt;
+    if (more) {
+      fq.fetch(Q, a.sq.t, qs + QT, Tn, D, vec);
+      fg.fetch(G, a.sdo.t, qs + QT, Tn, D, vec);
+      fetch_stats(qs + QT);
+    }
+    // S(r, j) and dP(r, j): rows r = the tile's queries (LDS), columns j = this wave's keys
+    typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Qs, 0, kf, g, c);
+    typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Gs, 0, vf, g, c);
+    const bool mask = (qs < wk0 + MT - 1) || (qs + QT > Tn) || (wk0 + MT > Tn);
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) {
+      const int rl = M::row(i, g);
+      T p = ex2(s[i] * sl2 - stats[cur][0][rl]) / stats[cur][1][rl];
+      if (mask) {
+        const int r = qs + rl;
+        p = (kj <= r && r < Tn && kj < Tn) ? p : T(0);
+      }
+      s[i] = p;
+      dp[i] = p * (dp[i] - stats[cur][2][rl]);
+    }
+    // dV^T += dO^T P ; dK^T += Q^T dS
+    mma_lds_t_regs<T, DP>(dv, Gs, 0, s, g, c);
+    mma_lds_t_regs<T, DP>(dk, Qs, 0, dp, g, c);
+    if (more) {
+      T* nxt = lds + (cur ^ 1) * STAGE;
+      fq.store(nxt);
+      fg.store(nxt + TILE);
+      store_stats(cur ^ 1);
+    }
+    __syncthreads();
+  }
   T* DK = (T*)a.dk + b * a.sdk.b + h * a.sdk.h;
   T* DV = (T*)a.dv + b * a.sdv.b + h * a.sdv.h;
-  for (int which = 0; which < 2; ++which) {
-    __syncthreads();
-    T* Ws = lds + wave * MT * LD;
-#pragma unroll
-    for (int dt = 0; dt < DP / MT; ++dt)
-#pragma unroll
-      for (int i = 0; i < NACC; ++i)
-        Ws[c * LD + dt * MT + M::row(i, g)] = which == 0 ? dk[dt][i] * scale : dv[dt][i];
-    __syncthreads();
-    T* dst = which == 0 ? DK : DV;
-    const int64_t st = which == 0 ? a.sdk.t : a.sdv.t;
-    for (int f = threadIdx.x; f < KBB * DP; f += 256) {
-      const int r = f / DP, d = f % DP;
-      const int64_t kk = k0 + r;
-      if (kk < a.T && d < a.D) dst[kk * st + d] = lds[r * LD + d];
-    }
-  }
+  store_result<T, DP, KBB>(lds, dk, (T)a.scale, DK, a.sdk.t, k0, Tn, D, wave, g, c);
+  __syncthreads();
+  store_result<T, DP, KBB>(lds, dv, T(1), DV, a.sdv.t, k0, Tn, D, wave, g, c);
 }
 
 // ------------------------------------------------------- backward B: dQ
@@ -373,43 +469,56 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
   constexpr int KB = 2 * MT;
   constexpr int QB = 4 * MT;
-  constexpr int STAGE = (2 * KB * LD > QB * LD) ? 2 * KB * LD : QB * LD;
-  __shared__ __attribute__((aligned(16))) T lds[STAGE];
-  T* Ks = lds;
-  T* Vs = lds + KB * LD;
+  constexpr int TILE = KB * LD, STAGE = 2 * TILE;
+  constexpr int LDS_N = 2 * STAGE > QB * LD ? 2 * STAGE : QB * LD;
+  __shared__ __attribute__((aligned(16))) T lds[LDS_N];
 
-  const int64_t bh = blockIdx.y;
+  const int bh = blockIdx.y;
   const int64_t b = bh / a.H, h = bh % a.H;
-  const int64_t q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
+  const int Tn = (int)a.T, D = (int)a.D;
+  const int q0 = (int)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
-  const int64_t qr = q0 + wave * MT + c;
+  const int wq0 = q0 + wave * MT;
+  const int qr = wq0 + c;
   const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
   const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
   const T* V = (const T*)a.v + b * a.sv.b + h * a.sv.h;
   const T* G = (const T*)a.dO + b * a.sdo.b + h * a.sdo.h;
-  const T scale = (T)a.scale;
+  const T sl2 = (T)(a.scale * 1.4426950408889634);
   const bool vec = a.vec != 0;
-  const bool qok = qr < a.T;
-  const T mq = qok ? ((const T*)a.rowmax)[bh * a.T + qr] : T(0);
-  const T lq = qok ? ((const T*)a.rowsum)[bh * a.T + qr] : T(1);
-  const T dq_r = qok ? ((const T*)a.drow)[bh * a.T + qr] : T(0);
+  const bool qok = qr < Tn;
+  const T mq = qok ? ((const T*)a.rowmax)[(int64_t)bh * Tn + qr] : T(0);
+  const T linv = qok ? T(1) / ((const T*)a.rowsum)[(int64_t)bh * Tn + qr] : T(0);
+  const T dq_r = qok ? ((const T*)a.drow)[(int64_t)bh * Tn + qr] : T(0);
 
   typename M::vec_t qf[DP / 8], gf[DP / 8];
-  load_frag_rows<T, DP>(qf, Q, a.sq.t, qr, a.T, a.D, g, vec);
-  load_frag_rows<T, DP>(gf, G, a.sdo.t, qr, a.T, a.D, g, vec);
+  load_frag_rows<T, DP>(qf, Q, a.sq.t, qr, Tn, D, g, vec);
+  load_frag_rows<T, DP>(gf, G, a.sdo.t, qr, Tn, D, g, vec);
   typename M::acc_t dq[DP / MT];
 #pragma unroll
   for (int dt = 0; dt < DP / MT; ++dt) dq[dt] = typename M::acc_t(0);
 
-  const int64_t qmax = (q0 + QB < a.T ? q0 + QB : a.T) - 1;
-  const int64_t nkb = q0 < a.T ? qmax / KB + 1 : 0;
-  for (int64_t kb = 0; kb < nkb; ++kb) {
-    const int64_t k0 = kb * KB;
-    __syncthreads();
-    load_rows<T, KB, DP>(Ks, K, a.sk.t, k0, a.T, a.D, vec);
-    load_rows<T, KB, DP>(Vs, V, a.sv.t, k0, a.T, a.D, vec);
-    __syncthreads();
+  const int qlast = (q0 + QB < Tn ? q0 + QB : Tn) - 1;
+  const int nkb = q0 < Tn ? qlast / KB + 1 : 0;
+  TileFetch<T, KB, DP> fk, fv;
+  if (nkb > 0) {
+    fk.fetch(K, a.sk.t, 0, Tn, D, vec);
+    fv.fetch(V, a.sv.t, 0, Tn, D, vec);
+    fk.store(lds);
+    fv.store(lds + TILE);
+  }
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int k0 = kb * KB;
+    const T* Ks = lds + (kb & 1) * STAGE;
+    const T* Vs = Ks + TILE;
+    const bool more = kb + 1 < nkb;
+    if (more) {
+      fk.fetch(K, a.sk.t, k0 + KB, Tn, D, vec);
+      fv.fetch(V, a.sv.t, k0 + KB, Tn, D, vec);
+    }
+    const bool mask = (k0 + KB - 1 > wq0) || (k0 + KB > Tn) || !qok;
 #pragma unroll 1
     for (int jt = 0; jt < KB / MT; ++jt) {
       // S^T(j, r), dP^T(j, r): rows j = keys (LDS), columns r = this wave's queries
@@ -417,28 +526,25 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
       typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Vs, jt * MT, gf, g, c);
 #pragma unroll
       for (int i = 0; i < NACC; ++i) {
-        const int64_t j = k0 + jt * MT + M::row(i, g);
-        const bool live = j <= qr && qok && j < a.T;
-        const T p = live ? exp(s[i] * scale - mq) / lq : T(0);
+        T p = ex2(s[i] * sl2 - mq) * linv;
+        if (mask) {
+          const int j = k0 + jt * MT + M::row(i, g);
+          p = (j <= qr && qok && j < Tn) ? p : T(0);
+        }
         dp[i] = p * (dp[i] - dq_r);
       }
       // dQ^T += K^T dS^T
       mma_lds_t_regs<T, DP>(dq, Ks, jt * MT, dp, g, c);
     }
+    if (more) {
+      T* nxt = lds + ((kb + 1) & 1) * STAGE;
+      fk.store(nxt);
+      fv.store(nxt + TILE);
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  T* Ws = lds + wave * MT * LD;
-#pragma unroll
-  for (int dt = 0; dt < DP / MT; ++dt)
-#pragma unroll
-    for (int i = 0; i < NACC; ++i) Ws[c * LD + dt * MT + M::row(i, g)] = dq[dt][i] * scale;
-  __syncthreads();
   T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h;
-  for (int f = threadIdx.x; f < QB * DP; f += 256) {
-    const int r = f / DP, d = f % DP;
-    const int64_t qq = q0 + r;
-    if (qq < a.T && d < a.D) DQ[qq * a.sdq.t + d] = lds[r * LD + d];
-  }
+  store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c);
 }
 
 // ----------------------------------------------------------------- host

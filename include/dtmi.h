@@ -253,9 +253,10 @@ int dtmi_linear_bwd_dw(int dtype, void* dW, void* db, const void* X, const void*
  * (B, H, T, D), D <= 64 contiguous; each *_strides argument points at three
  * element strides (b, h, t) of that operand, so q/k/v/o/dq/dk/dv may be views
  * into fused [B, T, 3, H, D] / [B, T, H, D] buffers. The forward writes o and
- * the per-row max and sum of exp (rowmax/rowsum, contiguous [B, H, T]); the
- * backward recomputes the probabilities from them and writes dq, dk, dv
- * (dtrain keeps the full probability tensor instead). */
+ * the per-row softmax statistics (contiguous [B, H, T]): rowmax = log2(e) *
+ * max_j(q . k_j * scale) (base-2 units, the kernels use exp2) and rowsum =
+ * sum_j exp(q . k_j * scale - max); the backward recomputes the probabilities
+ * from them and writes dq, dk, dv (dtrain keeps the full probability tensor). */
 int dtmi_attn_fwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
                   const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
                   const int64_t* v_strides, void* o, const int64_t* o_strides, void* rowmax, void* rowsum);
