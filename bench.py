@@ -130,11 +130,20 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seq", type=int, default=2, help="sequences in the CPU baseline sample")
     ap.add_argument("--seed", type=int, default=5)
+    ap.add_argument("--workload", default="gpt2",
+                    choices=["gpt2", "ln_linear", "attention", "bucket_adamw", "chargpt", "copy"],
+                    help="gpt2: the headline training step; the others are the per-path microbenchmarks")
+    ap.add_argument("--dtype", default="float32", choices=["float32", "float64"],
+                    help="compute dtype of the microbenchmarks (the gpt2 step is float32)")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the data-parallel exchange is simulated on-device over {WORLD} replicas "
               f"and no multi-GPU path is built; --gpus {a.gpus} is not supported.", file=sys.stderr)
         return 2
+    if a.workload != "gpt2":
+        out = MICRO[a.workload](a)
+        print(json.dumps(out), flush=True)
+        return 0
 
     from dtmi import _lib
     from dtmi import ddp as P, nn as N, optim as O, replicas as R, train as S
@@ -205,6 +214,245 @@ def main(argv=None):
     print(json.dumps(out), flush=True)
     return 0
 
+
+
+# --------------------------------------------------------------- microbenchmarks
+# Per-path workloads with their own roofline line; the headline line above is
+# the gpt2 step. Each times `--steps` launches after `--warmup` with the
+# library's per-family HIP-event timing, so `achieved` is algorithmic work per
+# launch over the average launch time of the dominant family.
+
+def _threads():
+    try:
+        from threadpoolctl import threadpool_info
+        return max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:  # noqa: BLE001
+        return int(os.environ.get("OMP_NUM_THREADS", "1"))
+
+
+def _timed(a, fn, families):
+    from dtmi import _lib
+    for _ in range(a.warmup):
+        fn()
+    _lib.sync()
+    _lib.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        fn()
+    _lib.sync()
+    dt = time.perf_counter() - t0
+    fams = {f: _lib.timing_read(f) for f in families}
+    _lib.timing_enable(False)
+    return dt, fams
+
+
+def _line(metric, value, unit, a, ms, config, roofline, cpu, extra=None):
+    out = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
+           "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": {"float32": "f32", "float64": "f64"}[a.dtype], "data": "synthetic", "config": config,
+           "roofline": roofline, "cpu_baseline": cpu}
+    if extra:
+        out.update(extra)
+    return out
+
+
+def _mfma_peak(dtype):
+    return 157.3e12 if dtype == "float32" else 78.6e12
+
+
+def micro_ln_linear(a):
+    """LayerNorm + Linear backward, x [16384, 768], W [768, 3072]: dX, dW, db, dgamma, dbeta."""
+    from dtmi import device as D, kernels as K
+    M, Cin, N = 16384, 768, 3072
+    dt = np.dtype(a.dtype)
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((M, Cin)).astype(dt)
+    W = (rng.standard_normal((Cin, N)) * 0.02).astype(dt)
+    gamma = (1 + rng.standard_normal(Cin) * 0.01).astype(dt)
+    beta = (rng.standard_normal(Cin) * 0.01).astype(dt)
+    dY = rng.standard_normal((M, N)).astype(dt)
+    dx_, dW_, dg_, db_, dY_ = D.from_numpy(x), D.from_numpy(W), D.from_numpy(gamma), D.from_numpy(beta), \
+        D.from_numpy(dY)
+    h, mean, rstd = K.layernorm_fwd(dx_, dg_, db_)
+
+    def step():
+        dh, dw, db = K.linear_bwd(h, dW_, dY_)
+        K.layernorm_bwd(dh, dx_, dg_, mean, rstd)
+    dtm, fams = _timed(a, step, ["gemm", "ln_bwd", "other"])
+    n, ms, work = fams["gemm"]
+    flop = 2 * 2 * M * Cin * N
+    ach = work / (ms * 1e-3)
+    ln_n, ln_ms, ln_work = fams["ln_bwd"]
+    cpu = None
+    if not a.no_cpu_baseline:
+        from oracle import ops as OP
+        rows = 2048
+        t0 = time.perf_counter()
+        hh, cache = OP.layer_norm_fwd(x[:rows], gamma, beta)
+        gh, gW = OP.matmul_bwd(dY[:rows], hh, W)
+        OP.unbroadcast(dY[:rows], (N,))
+        OP.layer_norm_bwd(gh, cache, gamma)
+        t = time.perf_counter() - t0
+        cpu = {"value": round(2 * 2 * rows * Cin * N / t / 1e9, 2), "unit": "GFLOP/s", "cores": _threads(),
+               "kind": "port", "sample": f"oracle LN+Linear backward on {rows} of the {M} rows ({t:.1f} s)"}
+    return _line("LN + Linear backward GEMM throughput (dX, dW) at x[16384,768] W[768,3072]",
+                 round(flop / (1e-3 * ms / n) / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
+                 {"workload": f"LayerNorm + Linear backward, x [16384,768], W [768,3072], dY [16384,3072], {a.dtype}"},
+                 {"bound": "mfma", "kernel": "gemm_kernel", "achieved": round(ach / 1e12, 2),
+                  "peak": _mfma_peak(a.dtype) / 1e12, "unit": "TFLOP/s",
+                  "frac": round(ach / _mfma_peak(a.dtype), 4), "traffic": None},
+                 cpu, {"ln_bwd": {"GB/s": round(ln_work / (ln_ms * 1e-3) / 1e9, 1),
+                                  "ms": round(ln_ms / max(ln_n, 1), 4)}})
+
+
+def micro_attention(a):
+    """Causal attention backward, B 16, H 12, T 256, D 64 (forward untimed)."""
+    from dtmi import device as D, kernels as K
+    B, H, T, Dh = 16, 12, 256, 64
+    dt = np.dtype(a.dtype)
+    rng = np.random.default_rng(3)
+    q, k, v, g = (rng.standard_normal((B, H, T, Dh)).astype(dt) for _ in range(4))
+    dq_, dk_, dv_, dg_ = (D.from_numpy(t) for t in (q, k, v, g))
+    o, rmax, rsum = K.attn_fwd(dq_, dk_, dv_)
+    outs = [D.empty(q.shape, dt) for _ in range(3)]
+
+    def step():
+        K.attn_bwd(dq_, dk_, dv_, o, dg_, rmax, rsum, dq=outs[0], dk=outs[1], dv=outs[2])
+    dtm, fams = _timed(a, step, ["attn_bwd"])
+    n, ms, work = fams["attn_bwd"]
+    ach = work / (ms * 1e-3)
+    cpu = None
+    if not a.no_cpu_baseline:
+        from oracle import ops as OP
+        bs = 2
+        t0 = time.perf_counter()
+        _, p, sc = OP.attention_fwd(q[:bs], k[:bs], v[:bs])
+        t1 = time.perf_counter()
+        OP.attention_bwd(g[:bs], q[:bs], k[:bs], v[:bs], p, sc)
+        t = time.perf_counter() - t1
+        fl = 5 * 2 * bs * H * Dh * T * (T + 1) / 2
+        cpu = {"value": round(fl / t / 1e9, 2), "unit": "GFLOP/s", "cores": _threads(), "kind": "port",
+               "sample": f"oracle causal_attention backward on {bs} of {B} batches ({t:.2f} s), causal-exact FLOP"}
+    return _line("causal attention backward throughput (5 GEMMs, causal-exact FLOP) at B16 H12 T256 D64",
+                 round(ach / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
+                 {"workload": f"causal self-attention backward B=16 H=12 T=256 D=64 {a.dtype}"},
+                 {"bound": "mfma", "kernel": "attn_bwd_kv_kernel + attn_bwd_q_kernel", "achieved": round(ach / 1e12, 2),
+                  "peak": _mfma_peak(a.dtype) / 1e12, "unit": "TFLOP/s",
+                  "frac": round(ach / _mfma_peak(a.dtype), 4), "traffic": None}, cpu)
+
+
+def micro_bucket_adamw(a):
+    """124,439,808-element fixed-order 4-replica average (+ fused sum of squares),
+    clip and AdamW over the full buffer, then AdamW on the 1/4 shard."""
+    from dtmi import device as D, kernels as K
+    n, W = 124_439_808, 4
+    dt = np.dtype(a.dtype)
+    rng = np.random.default_rng(4)
+    p = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)).astype(dt)
+    reps = (rng.standard_normal((W, n), dtype=np.float32) * np.float32(1e-3)).astype(dt)
+    m = np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-4)).astype(dt)
+    v = np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-4)).astype(dt)
+    dp_, dm_, dv_, dr_ = D.from_numpy(p), D.from_numpy(m), D.from_numpy(v), D.from_numpy(reps)
+    del reps
+    g_ = D.empty((n,), dt)
+    nb = K.average_blocks(n)
+    parts = D.empty((nb,), np.float64)
+    sq, s_dev = D.empty((1,), np.float64), D.empty((1,), np.float64)
+    b1t, b2t = 1 - 0.9 ** 101, 1 - 0.95 ** 101
+    sh = n // 4
+
+    def step():
+        K.bucket_average(g_, dr_, W, 1.0 / W, partials=parts)
+        K.sumsq_finish(parts, nb, sq)
+        K.clip_scale(sq, 1.0, s_dev)
+        K.adamw(dp_, g_, dm_, dv_, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t, gscale_dev=s_dev)
+        K.adamw(dp_[:sh], g_[:sh], dm_[:sh], dv_[:sh], 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t, gscale_dev=s_dev)
+    dtm, fams = _timed(a, step, ["bucket_avg", "adamw", "sumsq"])
+    an, ams, awork = fams["adamw"]
+    bn, bms, bwork = fams["bucket_avg"]
+    total_bytes = awork + bwork
+    total_ms = ams + bms
+    ach = awork / (ams * 1e-3)
+    cpu = None
+    if not a.no_cpu_baseline:
+        from oracle import optim as OO
+        from oracle.ddp import fixed_order_sum
+        k = n // 16
+        rr = rng.standard_normal((W, k)).astype(dt)
+        t0 = time.perf_counter()
+        gg = fixed_order_sum(list(rr))
+        gg *= 1.0 / W
+        s = OO.clip_scale(float(np.dot(gg.astype(np.float64), gg.astype(np.float64))), 1.0)
+        pp, mm, vv = p[:k].copy(), m[:k].copy(), v[:k].copy()
+        OO.adamw_update(pp, gg * s, mm, vv, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t)
+        t = time.perf_counter() - t0
+        cpu = {"value": round((5 + 7) * k * dt.itemsize / t / 1e9, 2), "unit": "GB/s", "cores": _threads(),
+               "kind": "port", "sample": f"oracle average + clip + AdamW over {k} of the {n} elements ({t:.2f} s)"}
+    return _line("gradient bucket average + AdamW bandwidth over 124,439,808 params (4 replicas)",
+                 round(total_bytes / (total_ms * 1e-3) / 1e9, 1), "GB/s", a, 1e3 * dtm / a.steps,
+                 {"workload": f"124,439,808-element 4-replica fixed-order average + clip + AdamW (full + 1/4 shard) "
+                              f"{a.dtype}"},
+                 {"bound": "hbm", "kernel": "adamw_flat_kernel", "achieved": round(ach / 1e9, 1), "peak": 8000.0,
+                  "unit": "GB/s", "frac": round(ach / 8e12, 4), "traffic": None}, cpu,
+                 {"bucket_average": {"GB/s": round(bwork / (bms * 1e-3) / 1e9, 1), "ms": round(bms / max(bn, 1), 4)},
+                  "adamw": {"GB/s": round(ach / 1e9, 1), "ms": round(ams / max(an, 1), 4)}})
+
+
+def micro_chargpt(a):
+    """The float64 char-GPT step (vocab 65, ctx 32, dim 64, 4 heads, 2 layers, batch 8)."""
+    from dtmi import nn as N, optim as O, train as S
+    a.dtype = "float64"
+    c = dict(vocab=65, ctx=32, dim=64, heads=4, layers=2, dtype="float64")
+    w = synthetic_weights(c, 0)
+    rng = np.random.default_rng(0)
+    x, y = rng.integers(0, 65, (8, 32)), rng.integers(0, 65, (8, 32))
+    m = N.GPT(N.GPTConfig(**c))
+    m.load_numpy(w)
+    opt = O.AdamW([p.data for p in m.parameters()], lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+    def step():
+        S.step_single(m, opt, [[(x, y)]], clip=1.0)
+    dtm, fams = _timed(a, step, ["gemm", "attn_fwd", "attn_bwd", "other"])
+    ms = 1e3 * dtm / a.steps
+    cpu = None
+    if not a.no_cpu_baseline:
+        from oracle import model as OM, optim as OO, step as OS
+        oc = OM.GPTConfig(**c)
+        P = {k: v.copy() for k, v in w.items()}
+        oo = OO.AdamW(list(P.values()), lr=3e-4)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            OS.single_step(P, oc, [(x, y)], oo, clip=1.0)
+        t = (time.perf_counter() - t0) / 5
+        cpu = {"value": round(256 / t, 1), "unit": "tokens/s", "cores": _threads(), "kind": "port",
+               "sample": f"oracle full step x5 ({t * 1e3:.1f} ms per step)"}
+    n, gms, work = fams["gemm"]
+    return _line("char-GPT float64 fwd+bwd+clip+AdamW tokens/s (launch-bound parity config)", round(256 / (ms * 1e-3), 1),
+                 "tokens/s", a, ms, {"workload": "char-GPT float64 step: vocab 65, ctx 32, dim 64, 4 heads, 2 layers, "
+                                                 "batch 8"},
+                 {"bound": "mfma", "kernel": "gemm_kernel", "achieved": round(work / max(gms, 1e-9) / 1e9, 4),
+                  "peak": 78.6, "unit": "TFLOP/s", "frac": round(work / max(gms, 1e-9) / 1e9 / 78.6, 6),
+                  "traffic": None}, cpu)
+
+
+def micro_copy(a):
+    """A plain 256 MiB device-to-device copy through the flatten kernel (reads
+    256 MiB, writes 256 MiB): the calibration point for HBM byte counters."""
+    from dtmi import device as D, kernels as K
+    n = (256 << 20) // 4
+    src = D.full((n,), 1.0, np.float32)
+    dst = D.empty((n,), np.float32)
+    dtm, fams = _timed(a, lambda: K.bucket_flatten(dst, [src], [n]), ["flatten"])
+    cnt, ms, work = fams["flatten"]
+    ach = work / (ms * 1e-3)
+    return _line("device copy bandwidth (256 MiB read + 256 MiB write)", round(ach / 1e9, 1), "GB/s", a,
+                 1e3 * dtm / a.steps, {"workload": "flatten_kernel copy of 67,108,864 float32"},
+                 {"bound": "hbm", "kernel": "flatten_kernel", "achieved": round(ach / 1e9, 1), "peak": 8000.0,
+                  "unit": "GB/s", "frac": round(ach / 8e12, 4), "traffic": None}, None)
+
+
+MICRO = {"ln_linear": micro_ln_linear, "attention": micro_attention, "bucket_adamw": micro_bucket_adamw,
+         "chargpt": micro_chargpt, "copy": micro_copy}
 
 if __name__ == "__main__":
     sys.exit(main())
