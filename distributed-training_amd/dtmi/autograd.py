@@ -243,21 +243,61 @@ class Tensor:
 
 
 # ------------------------------------------------------------ functional ops
-def embedding(weight: Tensor, idx: np.ndarray) -> Tensor:
-    """dtrain/autograd.py:199-204. `idx` is a host integer array."""
-    idx = np.asarray(idx)
+class Indices:
+    """Integer ids (token ids, positions, targets) mirrored once in HBM.
+
+    dtrain passes index arrays as NumPy arrays (autograd.py:199, 250); every
+    op accepting one also accepts an Indices, so a batch can be uploaded once
+    and reused with no host-to-device copy inside a step. The embedding
+    backward's stable segment order (the order np.add.at adds rows in) is
+    computed on first use and kept with it.
+    """
+
+    __slots__ = ("host", "dev", "shape", "_segs", "_lo", "_hi")
+
+    def __init__(self, idx):
+        self.host = np.asarray(idx)
+        if not np.issubdtype(self.host.dtype, np.integer):
+            raise TypeError("indices must be integers")
+        self.shape = self.host.shape
+        self._lo = int(self.host.min()) if self.host.size else 0
+        self._hi = int(self.host.max()) if self.host.size else -1
+        self.dev = dev.from_numpy(self.host.reshape(-1).astype(np.int64))
+        self._segs = None
+
+    def check(self, n: int, what: str, allow_negative: bool):
+        lo = -n if allow_negative else 0
+        if self.host.size and (self._lo < lo or self._hi >= n):
+            raise IndexError(f"{what} out of bounds for size {n}")
+
+    def wrapped(self, n: int) -> "Indices":
+        """Negative ids taken modulo n (NumPy indexing)."""
+        if self._lo >= 0:
+            return self
+        return Indices(np.where(self.host < 0, self.host + n, self.host))
+
+    def segments(self):
+        if self._segs is None:
+            perm, start, row = K.embedding_segments(self.host)
+            self._segs = (dev.from_numpy(perm), dev.from_numpy(start), dev.from_numpy(row))
+        return self._segs
+
+
+def as_indices(idx) -> Indices:
+    return idx if isinstance(idx, Indices) else Indices(idx)
+
+
+def embedding(weight: Tensor, idx) -> Tensor:
+    """dtrain/autograd.py:199-204. `idx`: a host integer array or an Indices."""
     V = weight.shape[0]
-    if idx.size and (idx.min() < -V or idx.max() >= V):
-        raise IndexError(f"index out of bounds for axis 0 with size {V}")
-    flat = np.where(idx < 0, idx + V, idx).astype(np.int64).reshape(-1)
-    didx = dev.from_numpy(flat)
+    ix = as_indices(idx)
+    ix.check(V, "index", allow_negative=True)
+    ix = ix.wrapped(V)
     w = weight.data if weight.data.is_contiguous else weight.data.contiguous()
-    out = K.embedding_fwd(w, didx, idx.shape)
+    out = K.embedding_fwd(w, ix.dev, ix.shape)
 
     def bw(g):
-        perm, start, row = K.embedding_segments(flat)
-        segs = (dev.from_numpy(perm), dev.from_numpy(start), dev.from_numpy(row))
-        return (K.embedding_bwd(_contig(g).reshape(-1, weight.shape[1]), V, segs),)
+        return (K.embedding_bwd(_contig(g).reshape(-1, weight.shape[1]), V, ix.segments()),)
     return Tensor._make(out, (weight,), bw)
 
 
@@ -285,16 +325,15 @@ def causal_attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
     return Tensor._make(o, (q, k, v), bw)
 
 
-def cross_entropy(logits: Tensor, targets: np.ndarray) -> Tensor:
-    """dtrain/autograd.py:250-266: mean cross-entropy; `targets` is a host array."""
+def cross_entropy(logits: Tensor, targets) -> Tensor:
+    """dtrain/autograd.py:250-266: mean cross-entropy; `targets`: a host integer
+    array or an Indices."""
     z = _contig(logits.data)
     V = z.shape[-1]
-    t = np.asarray(targets).reshape(-1)
-    if t.size and (t.min() < 0 or t.max() >= V):
-        raise IndexError(f"target out of bounds for {V} classes")
-    dt = dev.from_numpy(t.astype(np.int64))
-    loss, rmax, rsum = K.xent_fwd(z, dt)
+    t = as_indices(targets)
+    t.check(V, "target", allow_negative=False)
+    loss, rmax, rsum = K.xent_fwd(z, t.dev)
 
     def bw(g):
-        return (K.xent_bwd(z, dt, rmax, rsum, g=_contig(g).reshape(1)),)
+        return (K.xent_bwd(z, t.dev, rmax, rsum, g=_contig(g).reshape(1)),)
     return Tensor._make(loss, (logits,), bw)

@@ -23,7 +23,7 @@ import numpy as np
 
 from . import device as dev
 from . import kernels as K
-from .autograd import Tensor, _contig, cross_entropy, embedding, layer_norm
+from .autograd import Indices, Tensor, _contig, as_indices, cross_entropy, embedding, layer_norm
 
 
 class Module:
@@ -193,9 +193,17 @@ class GPT(Module):
     def state_numpy(self) -> dict:
         return {name: p.numpy() for name, p in self.named_parameters()}
 
-    def forward(self, idx: np.ndarray, targets: np.ndarray | None = None):
+    def _positions(self, T: int) -> Indices:
+        cache = self.__dict__.setdefault("_pos_ids", {})
+        if T not in cache:
+            cache[T] = Indices(np.arange(T))
+        return cache[T]
+
+    def forward(self, idx, targets=None):
+        """idx, targets: host integer arrays or Indices (uploaded once)."""
+        idx = as_indices(idx)
         B, T = idx.shape
-        x = embedding(self.tok, idx) + embedding(self.pos, np.arange(T))
+        x = embedding(self.tok, idx) + embedding(self.pos, self._positions(T))
         for b in self.blocks:
             x = b(x)
         logits = self.head(self.ln(x))
