@@ -288,17 +288,19 @@ def micro_ln_linear(a):
     cpu = None
     if not a.no_cpu_baseline:
         from oracle import ops as OP
-        rows = 2048
-        t0 = time.perf_counter()
-        hh, cache = OP.layer_norm_fwd(x[:rows], gamma, beta)
-        gh, gW = OP.matmul_bwd(dY[:rows], hh, W)
-        OP.unbroadcast(dY[:rows], (N,))
-        OP.layer_norm_bwd(gh, cache, gamma)
-        t = time.perf_counter() - t0
-        cpu = {"value": round(2 * 2 * rows * Cin * N / t / 1e9, 2), "unit": "GFLOP/s", "cores": _threads(),
-               "kind": "port", "sample": f"oracle LN+Linear backward on {rows} of the {M} rows ({t:.1f} s)"}
+        reps, t0 = 0, time.perf_counter()
+        while reps == 0 or (time.perf_counter() - t0 < 3.0 and reps < 20):
+            hh, cache = OP.layer_norm_fwd(x, gamma, beta)
+            gh, gW = OP.matmul_bwd(dY, hh, W)
+            OP.unbroadcast(dY, (N,))
+            OP.layer_norm_bwd(gh, cache, gamma)
+            reps += 1
+        t = (time.perf_counter() - t0) / reps
+        cpu = {"value": round(flop / t / 1e9, 2), "unit": "GFLOP/s", "cores": _threads(),
+               "kind": "port", "sample": f"oracle LN forward + Linear and LN backward on all {M} rows, "
+                                         f"{reps} repetitions, {t:.2f} s each"}
     return _line("LN + Linear backward GEMM throughput (dX, dW) at x[16384,768] W[768,3072]",
-                 round(flop / (1e-3 * ms / n) / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
+                 round(flop / (1e-3 * ms / a.steps) / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"LayerNorm + Linear backward, x [16384,768], W [768,3072], dY [16384,3072], {a.dtype}"},
                  {"bound": "mfma", "kernel": "gemm_kernel", "achieved": round(ach / 1e12, 2),
                   "peak": _mfma_peak(a.dtype) / 1e12, "unit": "TFLOP/s",

@@ -7,12 +7,18 @@
 //   A "KC": A(m,k) = A[m*lda + k]  (X, dY)      A "MC": A(m,k) = A[k*lda + m]  (X^T)
 //   B "NC": B(k,n) = B[k*ldb + n]  (W, dY)      B "KC": B(k,n) = B[n*ldb + k]  (W^T)
 //
-// Tiling. 256 threads = 4 waves in a 2x2 grid; block tile 128x128, k-tile 16
-// floats or 8 doubles, wave tile 64x64 (2x2 MFMA tiles of 32x32 in float32, 4x4 of 16x16 in
-// float64). Each operand tile is staged in LDS in its global orientation
-// (global -> LDS is a straight 16-byte vector copy, fully coalesced along the
-// contiguous dimension), double-buffered with one barrier per k-tile and the
-// next tile's global loads in flight during the MFMAs.
+// Tiling. 256 threads = 4 waves in a 2x2 grid; block tile 128x128; k-tile
+// 16 floats or 8 doubles; MFMA tiles of 32x32 (float32) or 16x16 (float64).
+// Each operand tile is staged in LDS in its global orientation (global -> LDS
+// is a straight 16-byte vector copy, fully coalesced along the contiguous
+// dimension), double-buffered with one barrier per k-tile and the next tile's
+// global loads in flight during the MFMAs. The loads go through per-thread
+// pointers set up once and advanced by one k-tile per load (rows past the
+// matrix edge clamped onto the last row), so the main loop has no index
+// arithmetic and no divergent branches; only a partial last k-tile is masked.
+// (256x128 and 128x256 tiles, a second register set for a two-tile-deep
+// prefetch, 32-wide k-tiles and higher occupancy measured no faster on the
+// GPT-2 shapes.)
 //
 // MFMA k-slots. An MFMA takes k in lane groups g = lane / MT (2 groups of 32
 // lanes for 32x32x2, 4 groups of 16 for 16x16x4). Within each 8-wide k chunk,
@@ -72,32 +78,33 @@ struct GemmArgs {
   int accumulate;
 };
 
-constexpr int kBM = 128, kBN = 128, kKC = 8;
-// k-tile: 16 floats or 8 doubles (the float64 double-buffered tiles then fit 40 KB of LDS)
+constexpr int kKC = 8;
+// k-tile: 16 floats or 8 doubles
 template <typename T>
 constexpr int kBKT = sizeof(T) == 4 ? 16 : 8;
 
-template <typename T, bool KCONTIG>
+// One operand tile of BMN rows/columns (along M or N) by kBK.
+template <typename T, bool KCONTIG, int BMN>
 struct TileLayout {
   static constexpr int VEC = MF<T>::VEC;
   static constexpr int kBK = kBKT<T>;
-  // k-contiguous: [mn][kBK + VEC]; mn-contiguous: [kBK][128 + 8]
-  static constexpr int STRIDE = KCONTIG ? (kBK + VEC) : (128 + 8);
-  static constexpr int SIZE = KCONTIG ? 128 * STRIDE : kBK * STRIDE;
-  static constexpr int NVEC = 128 * kBK / VEC / 256;  // 16-byte vectors per thread per tile
+  // k-contiguous: [mn][kBK + VEC]; mn-contiguous: [kBK][BMN + 8]
+  static constexpr int STRIDE = KCONTIG ? (kBK + VEC) : (BMN + 8);
+  static constexpr int SIZE = KCONTIG ? BMN * STRIDE : kBK * STRIDE;
+  static constexpr int NVEC = BMN * kBK / VEC / 256;  // 16-byte vectors per thread per tile
 };
 
-template <typename T, bool KCONTIG>
+template <typename T, bool KCONTIG, int BMN>
 struct TileRegs {
-  typename MF<T>::vec_t v[TileLayout<T, KCONTIG>::NVEC];
+  typename MF<T>::vec_t v[TileLayout<T, KCONTIG, BMN>::NVEC];
 };
 
-// Global -> registers for one 128 x kBK operand tile (mn0 = first row/col of
+// Global -> registers for one BMN x kBK operand tile (mn0 = first row/col of
 // the tile along M or N, k0 = first k). Out-of-range elements read as 0.
-template <typename T, bool KCONTIG, bool VECLD>
-__device__ __forceinline__ void load_tile(TileRegs<T, KCONTIG>& r, const T* __restrict__ P, int64_t ld, int64_t mn0, int64_t MN, int64_t k0,
-                                          int64_t kend) {
-  using L = TileLayout<T, KCONTIG>;
+template <typename T, bool KCONTIG, int BMN, bool VECLD>
+__device__ __forceinline__ void load_tile(TileRegs<T, KCONTIG, BMN>& r, const T* __restrict__ P, int64_t ld,
+                                          int64_t mn0, int64_t MN, int64_t k0, int64_t kend) {
+  using L = TileLayout<T, KCONTIG, BMN>;
   constexpr int VEC = L::VEC;
   constexpr int kBK = L::kBK;
 #pragma unroll
@@ -108,8 +115,8 @@ __device__ __forceinline__ void load_tile(TileRegs<T, KCONTIG>& r, const T* __re
       mn = mn0 + f / (kBK / VEC);
       k = k0 + (f % (kBK / VEC)) * VEC;
     } else {
-      k = k0 + f / (128 / VEC);
-      mn = mn0 + (f % (128 / VEC)) * VEC;
+      k = k0 + f / (BMN / VEC);
+      mn = mn0 + (f % (BMN / VEC)) * VEC;
     }
     if (VECLD) {
       // every dimension that vectors run along is a multiple of VEC
@@ -130,9 +137,75 @@ __device__ __forceinline__ void load_tile(TileRegs<T, KCONTIG>& r, const T* __re
   }
 }
 
-template <typename T, bool KCONTIG>
-__device__ __forceinline__ void store_tile(T* __restrict__ lds, const TileRegs<T, KCONTIG>& r) {
-  using L = TileLayout<T, KCONTIG>;
+// Per-thread source pointers for the vector loads of the k-tiles that lie
+// wholly inside [kbeg, kend): set up once, advanced by one k-tile per load,
+// so the main loop carries no index arithmetic and no bounds branches. Rows
+// (or columns) past the matrix edge are clamped onto its last row/column:
+// they feed only output rows/columns that the epilogue never stores.
+template <typename T, bool KCONTIG, int BMN>
+struct TilePtr {
+  const T* p[TileLayout<T, KCONTIG, BMN>::NVEC];
+  int64_t step;
+};
+
+template <typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void init_ptr(TilePtr<T, KCONTIG, BMN>& t, const T* __restrict__ P, int64_t ld,
+                                         int64_t mn0, int64_t MN, int64_t kbeg) {
+  using L = TileLayout<T, KCONTIG, BMN>;
+  constexpr int VEC = L::VEC;
+  constexpr int kBK = L::kBK;
+#pragma unroll
+  for (int i = 0; i < L::NVEC; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    if (KCONTIG) {
+      int64_t mn = mn0 + f / (kBK / VEC);
+      mn = mn < MN ? mn : MN - 1;
+      t.p[i] = P + mn * ld + kbeg + (f % (kBK / VEC)) * VEC;
+    } else {
+      int64_t mn = mn0 + (f % (BMN / VEC)) * VEC;
+      mn = mn < MN ? mn : MN - VEC;
+      t.p[i] = P + (kbeg + f / (BMN / VEC)) * ld + mn;
+    }
+  }
+  t.step = KCONTIG ? (int64_t)kBK : (int64_t)kBK * ld;
+}
+
+template <typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void load_fast(TileRegs<T, KCONTIG, BMN>& r, TilePtr<T, KCONTIG, BMN>& t) {
+#pragma unroll
+  for (int i = 0; i < TileLayout<T, KCONTIG, BMN>::NVEC; ++i) {
+    r.v[i] = *reinterpret_cast<const typename MF<T>::vec_t*>(t.p[i]);
+    t.p[i] += t.step;
+  }
+}
+
+// The last k-tile when it extends past kend: the same number of loads as a
+// full tile, from addresses clamped into [kbeg, kend) (k past kend is zeroed
+// when the tile is stored to LDS, see store_tile_masked).
+template <typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void load_tail(TileRegs<T, KCONTIG, BMN>& r, const TilePtr<T, KCONTIG, BMN>& t,
+                                          int64_t ld, int64_t k0, int64_t kend) {
+  using L = TileLayout<T, KCONTIG, BMN>;
+  constexpr int VEC = L::VEC;
+  constexpr int kBK = L::kBK;
+#pragma unroll
+  for (int i = 0; i < L::NVEC; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    const T* q;
+    if (KCONTIG) {
+      const int64_t k = k0 + (f % (kBK / VEC)) * VEC;
+      q = t.p[i] - (k < kend ? 0 : k - (kend - VEC));
+    } else {
+      const int64_t k = k0 + f / (BMN / VEC);
+      q = t.p[i] - (k < kend ? 0 : (k - (kend - 1)) * ld);
+    }
+    r.v[i] = *reinterpret_cast<const typename MF<T>::vec_t*>(q);
+  }
+}
+
+template <typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void store_tile(T* __restrict__ lds, const TileRegs<T, KCONTIG, BMN>& r) {
+  using L = TileLayout<T, KCONTIG, BMN>;
   constexpr int VEC = L::VEC;
   constexpr int kBK = L::kBK;
 #pragma unroll
@@ -142,16 +215,40 @@ __device__ __forceinline__ void store_tile(T* __restrict__ lds, const TileRegs<T
     if (KCONTIG)
       off = (f / (kBK / VEC)) * L::STRIDE + (f % (kBK / VEC)) * VEC;
     else
-      off = (f / (128 / VEC)) * L::STRIDE + (f % (128 / VEC)) * VEC;
+      off = (f / (BMN / VEC)) * L::STRIDE + (f % (BMN / VEC)) * VEC;
     *reinterpret_cast<typename MF<T>::vec_t*>(lds + off) = r.v[i];
+  }
+}
+
+// store_tile for the last, partial k-tile: vectors whose k is at or past
+// kend are stored as zeros.
+template <typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void store_tile_masked(T* __restrict__ lds, const TileRegs<T, KCONTIG, BMN>& r,
+                                                  int64_t k0, int64_t kend) {
+  using L = TileLayout<T, KCONTIG, BMN>;
+  constexpr int VEC = L::VEC;
+  constexpr int kBK = L::kBK;
+#pragma unroll
+  for (int i = 0; i < L::NVEC; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    int off;
+    int64_t k;
+    if (KCONTIG) {
+      off = (f / (kBK / VEC)) * L::STRIDE + (f % (kBK / VEC)) * VEC;
+      k = k0 + (f % (kBK / VEC)) * VEC;
+    } else {
+      off = (f / (BMN / VEC)) * L::STRIDE + (f % (BMN / VEC)) * VEC;
+      k = k0 + f / (BMN / VEC);
+    }
+    *reinterpret_cast<typename MF<T>::vec_t*>(lds + off) = k < kend ? r.v[i] : typename MF<T>::vec_t(0);
   }
 }
 
 // The VEC k-values lane (group g, position c) feeds for operand rows/cols
 // `base + c` at chunk `kk`.
-template <typename T, bool KCONTIG>
+template <typename T, bool KCONTIG, int BMN>
 __device__ __forceinline__ typename MF<T>::vec_t read_frag(const T* __restrict__ lds, int base, int kk, int g, int c) {
-  using L = TileLayout<T, KCONTIG>;
+  using L = TileLayout<T, KCONTIG, BMN>;
   constexpr int VEC = L::VEC;
   typename MF<T>::vec_t v;
   if (KCONTIG) {
@@ -177,19 +274,22 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn)
   tn = r / gsz;
 }
 
-template <typename T, bool AKC, bool BKC, bool VECA, bool VECB>
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
+// Block tile BM x BN, 4 waves in a 2 x 2 grid of (BM/2) x (BN/2) wave tiles.
+template <typename T, int BM, int BN, bool AKC, bool BKC, bool VECA, bool VECB>
+__global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs a) {
   constexpr int kBK = kBKT<T>;
   using MFT = MF<T>;
-  using LA = TileLayout<T, AKC>;
-  using LB = TileLayout<T, BKC>;
+  using LA = TileLayout<T, AKC, BM>;
+  using LB = TileLayout<T, BKC, BN>;
   constexpr int MT = MFT::MT, VEC = MFT::VEC, NACC = MFT::NACC;
-  constexpr int TM = 64 / MT, TN = 64 / MT;
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / MT, TN = WN / MT;
+  constexpr int NCH = kBK / kKC;  // 8-wide k chunks per k-tile
   __shared__ __attribute__((aligned(16))) T lds[2 * (LA::SIZE + LB::SIZE)];
 
   int tm, tn;
   tile_coords(a, tm, tn);
-  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   const int split = blockIdx.y;
   const int64_t batch = blockIdx.z;
   const int64_t kbeg = (int64_t)split * a.k_per_split;
@@ -199,7 +299,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
-  const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
 
   typename MFT::acc_t acc[TM][TN];
 #pragma unroll
@@ -207,31 +307,61 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = typename MFT::acc_t(0);
 
-  TileRegs<T, AKC> ra;
-  TileRegs<T, BKC> rb;
+  // LDS is double-buffered with one barrier per k-tile: iteration kt issues
+  // the global loads of tile kt+1 into registers, computes tile kt from LDS
+  // stage kt&1 while they are in flight, then stores them to the other stage.
+  TileRegs<T, AKC, BM> ra;
+  TileRegs<T, BKC, BN> rb;
   const int64_t ntiles = kend > kbeg ? (kend - kbeg + kBK - 1) / kBK : 0;
+  const int64_t nfull = kend > kbeg ? (kend - kbeg) / kBK : 0;  // tiles with every k in range
+  TilePtr<T, AKC, BM> pa;
+  TilePtr<T, BKC, BN> pb;
+  if (VECA) init_ptr<T, AKC, BM>(pa, A, a.lda, m0, a.M, kbeg);
+  if (VECB) init_ptr<T, BKC, BN>(pb, B, a.ldb, n0, a.N, kbeg);
+  // Tiles are loaded strictly in order kt = 0, 1, 2, ...; only the last one
+  // can be partial. Every tile issues the same loads with no divergent
+  // branch and no index arithmetic beyond one pointer increment.
+  auto load = [&](int64_t kt, TileRegs<T, AKC, BM>& la, TileRegs<T, BKC, BN>& lb) {
+    const int64_t k0 = kbeg + kt * kBK;
+    if (kt < nfull) {
+      if (VECA) load_fast<T, AKC, BM>(la, pa);
+      if (VECB) load_fast<T, BKC, BN>(lb, pb);
+    } else {
+      if (VECA) load_tail<T, AKC, BM>(la, pa, a.lda, k0, kend);
+      if (VECB) load_tail<T, BKC, BN>(lb, pb, a.ldb, k0, kend);
+    }
+    if (!VECA) load_tile<T, AKC, BM, false>(la, A, a.lda, m0, a.M, k0, kend);
+    if (!VECB) load_tile<T, BKC, BN, false>(lb, B, a.ldb, n0, a.N, k0, kend);
+  };
+  auto store = [&](int64_t kt, int stage, const TileRegs<T, AKC, BM>& sa, const TileRegs<T, BKC, BN>& sb) {
+    T* As = lds + stage * LA::SIZE;
+    T* Bs = lds + 2 * LA::SIZE + stage * LB::SIZE;
+    if (kt < nfull) {
+      store_tile<T, AKC, BM>(As, sa);
+      store_tile<T, BKC, BN>(Bs, sb);
+    } else {
+      const int64_t k0 = kbeg + kt * kBK;
+      store_tile_masked<T, AKC, BM>(As, sa, k0, kend);
+      store_tile_masked<T, BKC, BN>(Bs, sb, k0, kend);
+    }
+  };
   if (ntiles > 0) {
-    load_tile<T, AKC, VECA>(ra, A, a.lda, m0, a.M, kbeg, kend);
-    load_tile<T, BKC, VECB>(rb, B, a.ldb, n0, a.N, kbeg, kend);
-    store_tile<T, AKC>(lds, ra);
-    store_tile<T, BKC>(lds + 2 * LA::SIZE, rb);
+    load(0, ra, rb);
+    store(0, 0, ra, rb);
   }
   __syncthreads();
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int cur = kt & 1;
-    const bool more = kt + 1 < ntiles;
-    if (more) {
-      const int64_t k0 = kbeg + (kt + 1) * kBK;
-      load_tile<T, AKC, VECA>(ra, A, a.lda, m0, a.M, k0, kend);
-      load_tile<T, BKC, VECB>(rb, B, a.ldb, n0, a.N, k0, kend);
-    }
+    if (kt + 1 < ntiles) load(kt + 1, ra, rb);
+    const T* As = lds + cur * LA::SIZE;
+    const T* Bs = lds + 2 * LA::SIZE + cur * LB::SIZE;
 #pragma unroll
-    for (int kk = 0; kk < kBK; kk += kKC) {
+    for (int ch = 0; ch < NCH; ++ch) {
       typename MFT::vec_t fa[TM], fb[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = read_frag<T, AKC>(lds + cur * LA::SIZE, wm0 + i * MT, kk, g, c);
+      for (int i = 0; i < TM; ++i) fa[i] = read_frag<T, AKC, BM>(As, wm0 + i * MT, ch * kKC, g, c);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = read_frag<T, BKC>(lds + 2 * LA::SIZE + cur * LB::SIZE, wn0 + j * MT, kk, g, c);
+      for (int j = 0; j < TN; ++j) fb[j] = read_frag<T, BKC, BN>(Bs, wn0 + j * MT, ch * kKC, g, c);
 #pragma unroll
       for (int s = 0; s < VEC; ++s)
 #pragma unroll
@@ -239,10 +369,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
 #pragma unroll
           for (int j = 0; j < TN; ++j) acc[i][j] = MFT::mma(fa[i][s], fb[j][s], acc[i][j]);
     }
-    if (more) {
-      store_tile<T, AKC>(lds + (cur ^ 1) * LA::SIZE, ra);
-      store_tile<T, BKC>(lds + 2 * LA::SIZE + (cur ^ 1) * LB::SIZE, rb);
-    }
+    if (kt + 1 < ntiles) store(kt + 1, cur ^ 1, ra, rb);
     __syncthreads();
   }
 
@@ -272,7 +399,6 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
     }
 }
 
-// C[b][m][n] = (sum over splits in order of ws[s][b][m][n]) (+ bias[n]) (+ C)
 template <typename T>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(T* __restrict__ C, const T* __restrict__ ws,
                                                              const T* __restrict__ bias, int splits, int64_t batch,
@@ -293,16 +419,28 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(T* __restrict__ C, c
   }
 }
 
-template <typename T, bool AKC, bool BKC>
+template <typename T, int BM, int BN, bool AKC, bool BKC>
 static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb) {
   if (veca && vecb)
-    gemm_kernel<T, AKC, BKC, true, true><<<grid, 256, 0, stream()>>>(a);
+    gemm_kernel<T, BM, BN, AKC, BKC, true, true><<<grid, 256, 0, stream()>>>(a);
   else if (veca)
-    gemm_kernel<T, AKC, BKC, true, false><<<grid, 256, 0, stream()>>>(a);
+    gemm_kernel<T, BM, BN, AKC, BKC, true, false><<<grid, 256, 0, stream()>>>(a);
   else if (vecb)
-    gemm_kernel<T, AKC, BKC, false, true><<<grid, 256, 0, stream()>>>(a);
+    gemm_kernel<T, BM, BN, AKC, BKC, false, true><<<grid, 256, 0, stream()>>>(a);
   else
-    gemm_kernel<T, AKC, BKC, false, false><<<grid, 256, 0, stream()>>>(a);
+    gemm_kernel<T, BM, BN, AKC, BKC, false, false><<<grid, 256, 0, stream()>>>(a);
+}
+
+template <typename T, int BM, int BN>
+static void launch_layout(const GemmArgs& a, dim3 grid, int akc, int bkc, bool veca, bool vecb) {
+  if (akc && bkc)
+    launch_variant<T, BM, BN, true, true>(a, grid, veca, vecb);
+  else if (akc)
+    launch_variant<T, BM, BN, true, false>(a, grid, veca, vecb);
+  else if (bkc)
+    launch_variant<T, BM, BN, false, true>(a, grid, veca, vecb);
+  else
+    launch_variant<T, BM, BN, false, false>(a, grid, veca, vecb);
 }
 
 template <typename T>
@@ -325,31 +463,32 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   a.sB = sB;
   a.sC = sC;
   a.accumulate = accumulate;
-  a.tiles_m = (int)cdiv(M, kBM);
-  a.tiles_n = (int)cdiv(N, kBN);
-  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
-  DTMI_CHECK(tiles < (1LL << 31) && batch < 65536, "dtmi_gemm: problem too large");
-  // Split K so that the blocks fill whole waves of the CUs: a grid of b
-  // blocks on C CUs runs ceil(b / C) rounds, so its useful fraction is
-  // b / (C * ceil(b / C)). Take the fewest splits (each split keeps >= 256 of
-  // K) that reach 90 %, else the best one found.
+  // K splits. A grid of b blocks on C CUs runs ceil(b / C) rounds, so its
+  // useful fraction is b / (C * ceil(b / C)); take the fewest splits (each
+  // keeping >= 256 of K) that reach 90 % of rounds, else the best found.
+  const int64_t cus = num_cus() > 0 ? num_cus() : 256;
+  constexpr int bm = 128, bn = 128;
+  const int64_t tmn = cdiv(M, bm) * cdiv(N, bn);
   int splits = 1;
   if (force_splits > 0) {
     splits = force_splits;
   } else {
-    const int64_t cus = num_cus() > 0 ? num_cus() : 256;
-    double best = 0.0;
-    for (int s = 1; s <= 16; ++s) {
-      if (s > 1 && K / s < 256) break;
-      const int64_t blocks = tiles * batch * s;
+    double e_best = 0.0;
+    for (int sp = 1; sp <= 16; ++sp) {
+      if (sp > 1 && K / sp < 256) break;
+      const int64_t blocks = tmn * batch * sp;
       const double eff = (double)blocks / (double)(cus * cdiv(blocks, cus));
-      if (eff > best + 1e-9) {
-        best = eff;
-        splits = s;
+      if (eff > e_best + 1e-9) {
+        e_best = eff;
+        splits = sp;
       }
       if (eff >= 0.9) break;
     }
   }
+  a.tiles_m = (int)cdiv(M, bm);
+  a.tiles_n = (int)cdiv(N, bn);
+  const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
+  DTMI_CHECK(tiles < (1LL << 31) && batch < 65536, "dtmi_gemm: problem too large");
   constexpr int kBK = kBKT<T>;
   int64_t kps = cdiv(cdiv(K, splits), kBK) * kBK;
   if (kps < kBK) kps = kBK;
@@ -367,14 +506,7 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
   {
     TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
-    if (akc && bkc)
-      launch_variant<T, true, true>(a, grid, veca, vecb);
-    else if (akc)
-      launch_variant<T, true, false>(a, grid, veca, vecb);
-    else if (bkc)
-      launch_variant<T, false, true>(a, grid, veca, vecb);
-    else
-      launch_variant<T, false, false>(a, grid, veca, vecb);
+    launch_layout<T, bm, bn>(a, grid, akc, bkc, veca, vecb);
     if (splits > 1) {
       int64_t total = batch * M * N;
       int rg = (int)(cdiv(total, 256 * 4) < 8192 ? cdiv(total, 256 * 4) : 8192);

@@ -101,7 +101,7 @@ def _gemm_ref(a, b, akc, bkc):
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
 @pytest.mark.parametrize("akc,bkc", [(True, False), (True, True), (False, False), (False, True)])
 @pytest.mark.parametrize("M,N,K", [(256, 192, 64), (300, 65, 64), (1, 1, 1), (129, 257, 33), (8, 5, 7),
-                                   (512, 2304, 768)])
+                                   (512, 2304, 768), (132, 68, 36), (260, 132, 1000), (4, 4, 4)])
 def test_gemm_layouts_and_ragged_shapes(dev, dt, akc, bkc, M, N, K):
     D, K_ = _dev()
     rng = np.random.default_rng(M * 7 + N * 3 + K)
@@ -122,6 +122,23 @@ def test_gemm_split_k_is_deterministic_and_correct(dev, dt):
     ref = a.astype(np.float64).T @ g.astype(np.float64)
     outs = [K_.gemm(D.from_numpy(a), D.from_numpy(g), a_kcontig=False, b_kcontig=False, splits=s).numpy()
             for s in (1, 4, 4, 0)]
+    for o in outs:
+        assert rel_err(o, ref) <= TOL[dt]
+    assert bits_equal(outs[1], outs[2])
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("akc,bkc", [(True, False), (False, False), (True, True)])
+def test_gemm_split_k_with_partial_last_tile(dev, dt, akc, bkc):
+    """K = 1000 over 3 splits: the last split ends in a partial k-tile."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(13)
+    M, N, K = 200, 132, 1000
+    a = rng.standard_normal((M, K) if akc else (K, M)).astype(dt)
+    b = rng.standard_normal((N, K) if bkc else (K, N)).astype(dt)
+    ref = _gemm_ref(a.astype(np.float64), b.astype(np.float64), akc, bkc)
+    outs = [K_.gemm(D.from_numpy(a), D.from_numpy(b), a_kcontig=akc, b_kcontig=bkc, splits=s).numpy()
+            for s in (1, 3, 3)]
     for o in outs:
         assert rel_err(o, ref) <= TOL[dt]
     assert bits_equal(outs[1], outs[2])
