@@ -3,10 +3,11 @@
 // deterministic sum of squares and the clip factor.
 //
 // All of these are HBM-bound streaming kernels: 16-byte vector loads and stores
-// (float4 / double2) when every operand is 16-byte aligned, several vectors in
-// flight per thread, and grid-stride loops over a grid that depends only on the
-// problem size (so per-block partial sums, and therefore results, are the same
-// on every run and every device).
+// (4 floats / 2 doubles) when every operand is 16-byte aligned, over a grid
+// that depends only on the problem size (so per-block partial sums, and
+// therefore results, are the same on every run and every device). AdamW and
+// the replica average run one pass of 1024-element blocks with non-temporal
+// accesses; the multi-tensor kernels walk 32768-element chunks.
 //
 // Bit-exactness: this file is compiled with -ffp-contract=off and every update
 // below is written as the same sequence of IEEE operations NumPy performs for
@@ -22,39 +23,42 @@ template <typename T>
 struct V16;
 template <>
 struct V16<float> {
-  using type = float4;
+  typedef float type __attribute__((ext_vector_type(4)));
   static constexpr int N = 4;
 };
 template <>
 struct V16<double> {
-  using type = double2;
+  typedef double type __attribute__((ext_vector_type(2)));
   static constexpr int N = 2;
 };
 
 template <typename T>
-__device__ __forceinline__ T vget(const typename V16<T>::type& v, int i);
-template <>
-__device__ __forceinline__ float vget<float>(const float4& v, int i) {
-  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
-}
-template <>
-__device__ __forceinline__ double vget<double>(const double2& v, int i) {
-  return i == 0 ? v.x : v.y;
+__device__ __forceinline__ T vget(const typename V16<T>::type& v, int i) {
+  return v[i];
 }
 template <typename T>
-__device__ __forceinline__ void vset(typename V16<T>::type& v, int i, T x);
-template <>
-__device__ __forceinline__ void vset<float>(float4& v, int i, float x) {
-  if (i == 0) v.x = x;
-  else if (i == 1) v.y = x;
-  else if (i == 2) v.z = x;
-  else v.w = x;
+__device__ __forceinline__ void vset(typename V16<T>::type& v, int i, T x) {
+  v[i] = x;
 }
-template <>
-__device__ __forceinline__ void vset<double>(double2& v, int i, double x) {
-  if (i == 0) v.x = x;
-  else v.y = x;
+
+// Streaming accesses of data touched once per kernel: non-temporal loads and
+// stores (measured fastest for these one-pass kernels on MI355X HBM).
+template <typename V>
+__device__ __forceinline__ V ld_nt(const V* p) {
+  return __builtin_nontemporal_load(p);
 }
+template <typename V>
+__device__ __forceinline__ void st_nt(V v, V* p) {
+  __builtin_nontemporal_store(v, p);
+}
+
+// One-pass kernels over n elements use blocks of kBlockElems consecutive
+// elements (256 threads x 16 bytes for float32, 2 x 16 bytes for float64):
+// every load of a block is issued at once and blocks retire after one pass.
+// The grid is a function of n alone, so per-block partial sums are too.
+constexpr int64_t kBlockElems = 1024;
+
+static int64_t onepass_grid(int64_t n) { return n > 0 ? (n + kBlockElems - 1) / kBlockElems : 1; }
 
 // --------------------------------------------------------------- AdamW
 template <typename T>
@@ -103,36 +107,32 @@ __device__ __forceinline__ T load_gscale(const AdamWScalars<T>& s, const double*
   return gdev ? (T)(*gdev) : s.gscale;
 }
 
-constexpr int kUnroll = 4;
-
 template <typename T, bool VEC>
 __global__ void __launch_bounds__(256) adamw_flat_kernel(T* __restrict__ p, const T* __restrict__ g,
                                                           T* __restrict__ m, T* __restrict__ v, int64_t n,
                                                           AdamWScalars<T> s, const double* gdev) {
   const T gs = load_gscale(s, gdev);
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+  const int64_t base = (int64_t)blockIdx.x * kBlockElems;
   if (VEC) {
     using VT = typename V16<T>::type;
     constexpr int N = V16<T>::N;
-    const int64_t nv = n / N;
-    VT* pv = reinterpret_cast<VT*>(p);
-    const VT* gv = reinterpret_cast<const VT*>(g);
-    VT* mv = reinterpret_cast<VT*>(m);
-    VT* vv = reinterpret_cast<VT*>(v);
-    int64_t i = tid;
-    for (; i + (kUnroll - 1) * nthreads < nv; i += kUnroll * nthreads) {
-      VT P[kUnroll], G[kUnroll], M[kUnroll], W[kUnroll];
+    constexpr int PER = kBlockElems / 256 / N;  // vectors per thread
+    VT P[PER], G[PER], M[PER], W[PER];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        int64_t k = i + u * nthreads;
-        P[u] = pv[k];
-        G[u] = gv[k];
-        M[u] = mv[k];
-        W[u] = vv[k];
+    for (int u = 0; u < PER; ++u) {
+      const int64_t e0 = base + (int64_t)(u * 256 + threadIdx.x) * N;
+      if (e0 + N <= n) {
+        const int64_t k = e0 / N;
+        P[u] = ld_nt(reinterpret_cast<const VT*>(p) + k);
+        G[u] = ld_nt(reinterpret_cast<const VT*>(g) + k);
+        M[u] = ld_nt(reinterpret_cast<const VT*>(m) + k);
+        W[u] = ld_nt(reinterpret_cast<const VT*>(v) + k);
       }
+    }
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < PER; ++u) {
+      const int64_t e0 = base + (int64_t)(u * 256 + threadIdx.x) * N;
+      if (e0 + N <= n) {
 #pragma unroll
         for (int e = 0; e < N; ++e) {
           T pe = vget<T>(P[u], e), me = vget<T>(M[u], e), ve = vget<T>(W[u], e);
@@ -141,51 +141,32 @@ __global__ void __launch_bounds__(256) adamw_flat_kernel(T* __restrict__ p, cons
           vset<T>(M[u], e, me);
           vset<T>(W[u], e, ve);
         }
-        int64_t k = i + u * nthreads;
-        pv[k] = P[u];
-        mv[k] = M[u];
-        vv[k] = W[u];
+        const int64_t k = e0 / N;
+        st_nt(P[u], reinterpret_cast<VT*>(p) + k);
+        st_nt(M[u], reinterpret_cast<VT*>(m) + k);
+        st_nt(W[u], reinterpret_cast<VT*>(v) + k);
+      } else if (e0 < n) {
+        for (int64_t k = e0; k < n; ++k) adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);  // ragged end
       }
     }
-    for (; i < nv; i += nthreads) {
-      VT P = pv[i], G = gv[i], M = mv[i], W = vv[i];
-#pragma unroll
-      for (int e = 0; e < N; ++e) {
-        T pe = vget<T>(P, e), me = vget<T>(M, e), ve = vget<T>(W, e);
-        adamw_elem<T>(pe, vget<T>(G, e), me, ve, s, gs);
-        vset<T>(P, e, pe);
-        vset<T>(M, e, me);
-        vset<T>(W, e, ve);
-      }
-      pv[i] = P;
-      mv[i] = M;
-      vv[i] = W;
-    }
-    for (int64_t k = nv * N + tid; k < n; k += nthreads) adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);
   } else {
-    for (int64_t k = tid; k < n; k += nthreads) adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);
+    for (int64_t k = base + threadIdx.x; k < base + kBlockElems && k < n; k += 256)
+      adamw_elem<T>(p[k], g[k], m[k], v[k], s, gs);
   }
-}
-
-static int stream_grid(int64_t units, int per_thread) {
-  int64_t b = cdiv(units, 256LL * per_thread);
-  if (b < 1) b = 1;
-  // At least a few waves per CU on the largest problems; never more blocks
-  // than there is work for.
-  const int64_t cap = 2048;
-  return (int)(b < cap ? b : cap);
 }
 
 template <typename T>
 static int launch_adamw_flat(void* p, const void* g, void* m, void* v, int64_t n, const AdamWScalars<T>& s,
                              const double* gdev) {
   bool vec = aligned(p, 16) && aligned(g, 16) && aligned(m, 16) && aligned(v, 16);
-  int grid = stream_grid(vec ? n / V16<T>::N + 1 : n, vec ? kUnroll : 4);
+  const int64_t grid = onepass_grid(n);
+  DTMI_CHECK(grid < (1LL << 31), "dtmi_adamw: too many elements");
   TimedLaunch tl(DTMI_FAM_ADAMW, 7.0 * (double)n * sizeof(T));
   if (vec)
-    adamw_flat_kernel<T, true><<<grid, 256, 0, stream()>>>((T*)p, (const T*)g, (T*)m, (T*)v, n, s, gdev);
+    adamw_flat_kernel<T, true><<<(unsigned)grid, 256, 0, stream()>>>((T*)p, (const T*)g, (T*)m, (T*)v, n, s, gdev);
   else
-    adamw_flat_kernel<T, false><<<grid, 256, 0, stream()>>>((T*)p, (const T*)g, (T*)m, (T*)v, n, s, gdev);
+    adamw_flat_kernel<T, false><<<(unsigned)grid, 256, 0, stream()>>>((T*)p, (const T*)g, (T*)m, (T*)v, n, s,
+                                                                       gdev);
   LAUNCH_CHECK("adamw_flat_kernel");
   return DTMI_OK;
 }
@@ -318,42 +299,43 @@ __device__ __forceinline__ double sq64(T x) {
 }
 
 // ------------------------------------------------- fixed-order average
+// out[i] = (((rep_0[i] + rep_1[i]) + ...) + rep_{W-1}[i]) * inv; with SUMSQ the
+// block's float64 sum of out^2 goes to partials[blockIdx.x] (fixed pattern).
 template <typename T, bool VEC, bool SUMSQ>
 __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out, const T* __restrict__ rep,
                                                               int world, int64_t n, int64_t stride, T inv,
                                                               double* __restrict__ partials) {
   __shared__ double lds[4];
-  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+  const int64_t base = (int64_t)blockIdx.x * kBlockElems;
   double acc = 0.0;
   if (VEC) {
     using VT = typename V16<T>::type;
     constexpr int N = V16<T>::N;
-    const int64_t nv = n / N;
-    for (int64_t i = tid; i < nv; i += nthreads) {
-      VT a = reinterpret_cast<const VT*>(rep)[i];
-      for (int r = 1; r < world; ++r) {
-        VT b = reinterpret_cast<const VT*>(rep + (int64_t)r * stride)[i];
+    constexpr int PER = kBlockElems / 256 / N;
 #pragma unroll
-        for (int e = 0; e < N; ++e) vset<T>(a, e, vget<T>(a, e) + vget<T>(b, e));
-      }
+    for (int u = 0; u < PER; ++u) {
+      const int64_t e0 = base + (int64_t)(u * 256 + threadIdx.x) * N;
+      if (e0 + N <= n) {
+        const int64_t k = e0 / N;
+        VT a = ld_nt(reinterpret_cast<const VT*>(rep) + k);
+        for (int r = 1; r < world; ++r) a = a + ld_nt(reinterpret_cast<const VT*>(rep + (int64_t)r * stride) + k);
+        a = a * inv;
+        if (SUMSQ)
 #pragma unroll
-      for (int e = 0; e < N; ++e) {
-        T o = vget<T>(a, e) * inv;
-        vset<T>(a, e, o);
-        if (SUMSQ) acc += sq64(o);
+          for (int e = 0; e < N; ++e) acc += sq64(vget<T>(a, e));
+        st_nt(a, reinterpret_cast<VT*>(out) + k);
+      } else if (e0 < n) {
+        for (int64_t k = e0; k < n; ++k) {  // ragged end
+          T a = rep[k];
+          for (int r = 1; r < world; ++r) a = a + rep[(int64_t)r * stride + k];
+          T o = a * inv;
+          out[k] = o;
+          if (SUMSQ) acc += sq64(o);
+        }
       }
-      reinterpret_cast<VT*>(out)[i] = a;
-    }
-    for (int64_t k = nv * N + tid; k < n; k += nthreads) {
-      T a = rep[k];
-      for (int r = 1; r < world; ++r) a = a + rep[(int64_t)r * stride + k];
-      T o = a * inv;
-      out[k] = o;
-      if (SUMSQ) acc += sq64(o);
     }
   } else {
-    for (int64_t k = tid; k < n; k += nthreads) {
+    for (int64_t k = base + threadIdx.x; k < base + kBlockElems && k < n; k += 256) {
       T a = rep[k];
       for (int r = 1; r < world; ++r) a = a + rep[(int64_t)r * stride + k];
       T o = a * inv;
@@ -367,12 +349,7 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
   }
 }
 
-static int average_grid(int64_t n) {
-  // Function of n only: the per-block partial sums must not depend on the device.
-  int64_t b = cdiv(n, 256LL * 16);
-  if (b < 1) b = 1;
-  return (int)(b < 2048 ? b : 2048);
-}
+static int average_grid(int64_t n) { return (int)onepass_grid(n); }
 
 // -------------------------------------------------------- sum of squares
 struct SumsqEntry {

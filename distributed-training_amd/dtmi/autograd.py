@@ -73,7 +73,8 @@ def _broadcast_to(g: DeviceArray, shape) -> DeviceArray:
 
 
 class Tensor:
-    __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "_hooks", "name", "__weakref__")
+    __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "_hooks", "name", "grad_dest",
+                 "_dest_live", "__weakref__")
 
     def __init__(self, data, requires_grad=False, _parents=(), _backward=None, name=None):
         self.data = data if isinstance(data, DeviceArray) else dev.asarray(np.asarray(data))
@@ -83,6 +84,11 @@ class Tensor:
         self._backward = _backward
         self._hooks = []
         self.name = name
+        # Optional preallocated home for this leaf's gradient (same shape and
+        # dtype), e.g. its slot in a gradient bucket: the kernel producing
+        # the gradient writes straight into it, so the bucket needs no copy.
+        self.grad_dest = None
+        self._dest_live = None
 
     # ------------------------------------------------------------ utilities
     @property
@@ -221,25 +227,54 @@ class Tensor:
                 users[id(p)] = users.get(id(p), 0) + 1
                 if id(p) not in seen:
                     stack.append((p, False))
-        grads = {id(self): grad}
-        for node in reversed(order):
-            g = grads.pop(id(node), None)
-            if g is None:
-                continue
-            if node._backward is None:
-                if node.requires_grad:
-                    node.grad = g if node.grad is None else K.binary("add", node.grad, g)
-                    for h in node._hooks:
-                        h(node)
-                continue
-            for p, pg in zip(node._parents, node._backward(g)):
-                if not p.requires_grad or pg is None:
+        # A leaf with a grad_dest, no gradient yet and exactly one incoming
+        # edge lets its producing node write the gradient straight into the
+        # destination (grad_out); any other case goes through a new array.
+        live = []
+        for node in order:
+            if node._backward is None and node.grad_dest is not None and node.requires_grad:
+                if node.grad is None and users.get(id(node), 0) == 1:
+                    node._dest_live = node.grad_dest
+                    live.append(node)
+        try:
+            grads = {id(self): grad}
+            for node in reversed(order):
+                g = grads.pop(id(node), None)
+                if g is None:
                     continue
-                if tuple(pg.shape) != tuple(p.shape):
-                    raise RuntimeError(f"gradient shape {pg.shape} != {p.shape}")
-                k = id(p)
-                grads[k] = pg if k not in grads else K.binary("add", grads[k], pg)
+                if node._backward is None:
+                    if node.requires_grad:
+                        node._dest_live = None
+                        if node.grad is None:
+                            node.grad = g
+                        elif node.grad_dest is not None and node.grad.ptr == node.grad_dest.ptr:
+                            node.grad = K.binary("add", node.grad, g, out=node.grad)  # accumulate in place
+                        else:
+                            node.grad = K.binary("add", node.grad, g)
+                        for h in node._hooks:
+                            h(node)
+                    continue
+                self._backprop(node, g, grads)
+        finally:
+            for node in live:
+                node._dest_live = None
         return None
+
+    @staticmethod
+    def _backprop(node, g, grads):
+        for p, pg in zip(node._parents, node._backward(g)):
+            if not p.requires_grad or pg is None:
+                continue
+            if tuple(pg.shape) != tuple(p.shape):
+                raise RuntimeError(f"gradient shape {pg.shape} != {p.shape}")
+            k = id(p)
+            grads[k] = pg if k not in grads else K.binary("add", grads[k], pg)
+
+
+def grad_out(t: Tensor):
+    """Where a backward function should write the gradient of `t`: its live
+    grad_dest during backward() (see Tensor.grad_dest), else None."""
+    return t._dest_live
 
 
 # ------------------------------------------------------------ functional ops
@@ -297,7 +332,7 @@ def embedding(weight: Tensor, idx) -> Tensor:
     out = K.embedding_fwd(w, ix.dev, ix.shape)
 
     def bw(g):
-        return (K.embedding_bwd(_contig(g).reshape(-1, weight.shape[1]), V, ix.segments()),)
+        return (K.embedding_bwd(_contig(g).reshape(-1, weight.shape[1]), V, ix.segments(), out=grad_out(weight)),)
     return Tensor._make(out, (weight,), bw)
 
 
@@ -307,7 +342,7 @@ def layer_norm(x: Tensor, w: Tensor, b: Tensor, eps=1e-5) -> Tensor:
     y, mean, rstd = K.layernorm_fwd(xd, _contig(w.data), _contig(b.data), eps)
 
     def bw(g):
-        return K.layernorm_bwd(_contig(g), xd, _contig(w.data), mean, rstd)
+        return K.layernorm_bwd(_contig(g), xd, _contig(w.data), mean, rstd, dw_out=grad_out(w), db_out=grad_out(b))
     return Tensor._make(y, (x, w, b), bw)
 
 

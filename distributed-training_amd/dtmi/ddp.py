@@ -8,20 +8,30 @@ dtrain/ddp.py on one GPU. Same constructor, attributes and step protocol:
   definition order, closing a bucket as soon as it reaches the limit
   (ddp.py:46-56);
 * a grad-ready hook on every parameter hands its gradient to the bucket; when
-  all of a bucket's gradients of the running replica are in, one multi-tensor
-  flatten kernel copies them into that replica's row of the bucket (ddp.py:73-81
-  copies one parameter at a time); when the last replica's row is complete the
-  fixed-order average of the bucket is launched right away (`overlap=True`) or
-  at `finish()` (`overlap=False`);
+  all of a bucket's gradients of the last replica are in, the fixed-order
+  average of the bucket is launched right away (`overlap=True`) or at
+  `finish()` (`overlap=False`);
 * `no_sync()` skips all of this for gradient-accumulation micro-steps;
 * `finish()` zero-fills missing gradients (ddp.py:88-94), reduces what is left,
-  and points every `param.grad` at its slice of the averaged bucket
+  and points every `param.grad` at its slice of the averaged gradients
   (ddp.py:104-110). The average is
   (((g_0 + g_1) + g_2) + ... + g_{W-1}) * (1.0 / W), dtrain's `--algo direct`
-  order (comm.py:374-391), bit-exact to NumPy. The same kernel accumulates
-  the squares of the averaged gradients per block; `grad_sq` (a 1-element
-  float64 device array) is their deterministic sum after `finish()`, the
-  global-norm input of dtrain/train.py:155-156 without another pass.
+  order (comm.py:374-391), bit-exact to NumPy. `grad_sq` (a 1-element
+  float64 device array) is the deterministic float64 sum of squares of all
+  averaged gradients after `finish()`, the global-norm input of
+  dtrain/train.py:155-156. It is one pass over the flat averaged buffer, so
+  neither it nor the clip factor depends on the bucket size.
+
+Memory layout. A bucket is a run of consecutive parameters, so in forward
+order it is one contiguous range [lo, hi) of the flat parameter numbering.
+Every replica's gradients live in one [W, n] buffer (`ReplicaGrads`) in
+forward order, and the backward kernels write each parameter's gradient
+straight into its slot there (no flatten copy); bucket b's "buffer" of
+replica r is row r, columns [lo, hi). The averaged gradients go to one [n]
+buffer in the same order, so after `finish()` the `param.grad` views are
+back to back and the optimizer runs as one flat launch. Element order inside
+a bucket differs from dtrain's concatenation order (reverse definition
+order); the reduction is elementwise, so no value changes.
 
 The ring order of dtrain's default `--algo ring` (each chunk starts at a
 different rank, comm.py:342-372) is not reproduced; see the module docstring
@@ -37,6 +47,7 @@ import numpy as np
 from . import device as dev
 from . import kernels as K
 from .device import DeviceArray
+from .replicas import ReplicaGrads
 
 
 def bucket_layout(sizes, itemsize, bucket_mb=1.0):
@@ -56,22 +67,18 @@ def bucket_layout(sizes, itemsize, bucket_mb=1.0):
 
 
 class _Bucket:
-    def __init__(self, params, dtype, world):
-        self.params = params
-        self.offsets = []
-        off = 0
-        for p in params:
-            self.offsets.append(off)
-            off += p.data.size
-        self.n = off
-        self.rows = dev.empty((world, off), dtype)  # one row per replica (dtrain's b.buf, per rank)
-        self.ready = [dict() for _ in range(world)]
-        self.pending = [len(params)] * world
+    def __init__(self, idx, grads: ReplicaGrads, avg: DeviceArray):
+        self.idx = idx  # parameter indices, reverse definition order (dtrain's bucket order)
+        self.params = [grads.params[i] for i in idx]
+        self.lo = grads.offsets[min(idx)]
+        self.hi = grads.offsets[max(idx)] + grads.params[max(idx)].data.size
+        self.n = self.hi - self.lo
+        self.rows = grads.columns(self.lo, self.hi)  # [W, n]: every replica's gradients of this bucket
+        self.out = avg[self.lo:self.hi]  # averaged gradients of this bucket
+        world = grads.pg.world
+        self.ready = [set() for _ in range(world)]
         self.flushed = [False] * world
-        self.out = None  # averaged gradients of the last reduction
         self.reduced = False
-        self.partial_off = 0
-        self.nblocks = K.average_blocks(off) if off else 0
 
     @property
     def buf(self) -> DeviceArray:
@@ -89,18 +96,16 @@ class DDP:
             pg.broadcast(p.data, root=0)
         dtype = self.params[0].data.dtype
         sizes = [p.data.size for p in self.params]
-        self.buckets = [_Bucket([self.params[i] for i in idx], dtype, pg.world)
+        self.grads = ReplicaGrads(self.params, pg, dtype)
+        self.avg = dev.empty((max(self.grads.n, 1),), dtype)
+        self.buckets = [_Bucket(idx, self.grads, self.avg)
                         for idx in bucket_layout(sizes, np.dtype(dtype).itemsize, bucket_mb)]
         self._where = {}
-        off = 0
         for bi, b in enumerate(self.buckets):
-            b.partial_off = off
-            off += b.nblocks
-            for pi, p in enumerate(b.params):
-                self._where[id(p)] = (bi, pi)
-                p.register_grad_ready_hook(self._on_grad)
-        self._partials = dev.empty((max(off, 1),), np.float64)
-        self._nparts = off
+            for i in b.idx:
+                self._where[id(self.params[i])] = (bi, i)
+        for p in self.params:
+            p.register_grad_ready_hook(self._on_grad)
         self._sync = True
         self.comm_wait_s = 0.0
         self.grad_sq = None
@@ -113,14 +118,11 @@ class DDP:
         finally:
             self._sync = prev
 
-    def _flatten(self, b: _Bucket, r: int):
-        srcs = []
-        for pi, p in enumerate(b.params):
-            g = b.ready[r].get(pi)
-            if g is not None and not g.is_contiguous:
-                g = g.contiguous()
-            srcs.append(g.reshape(-1) if g is not None else None)  # missing: zeros (ddp.py:88-94)
-        K.bucket_flatten(b.rows[r], srcs, [p.data.size for p in b.params])
+    def _complete(self, b: _Bucket, r: int):
+        """Zero-fill replica r's slots of the bucket that received no gradient."""
+        for i in b.idx:
+            if i not in b.ready[r]:
+                self.grads.zero(r, i)  # missing: zeros (ddp.py:88-94)
         b.ready[r].clear()
         b.flushed[r] = True
 
@@ -128,22 +130,20 @@ class DDP:
         if b.reduced or b.n == 0:
             b.reduced = True
             return
-        b.out = dev.empty((b.n,), b.rows.dtype)
-        parts = self._partials[b.partial_off:b.partial_off + b.nblocks]
-        self.pg.average(b.out, b.rows, partials=parts)
+        self.pg.average(b.out, b.rows)
         b.reduced = True
 
     def _on_grad(self, p):
         if not self._sync:
             return
         r = self.pg.rank
-        bi, pi = self._where[id(p)]
+        bi, i = self._where[id(p)]
         b = self.buckets[bi]
-        if pi not in b.ready[r]:
-            b.pending[r] -= 1
-        b.ready[r][pi] = p.grad
-        if b.pending[r] == 0:
-            self._flatten(b, r)
+        self.grads.place(r, i, p.grad)
+        b.ready[r].add(i)
+        if len(b.ready[r]) == len(b.idx):
+            b.ready[r].clear()
+            b.flushed[r] = True
             if self.overlap and all(b.flushed):
                 self._reduce(b)
 
@@ -154,15 +154,13 @@ class DDP:
         for b in self.buckets:
             for r in range(W):
                 if not b.flushed[r]:
-                    self._flatten(b, r)
+                    self._complete(b, r)
             self._reduce(b)
         self.grad_sq = dev.empty((1,), np.float64)
-        K.sumsq_finish(self._partials, self._nparts, self.grad_sq)
+        K.sumsq([self.avg[:self.grads.n]], self.grad_sq)
+        for p, o in zip(self.params, self.grads.offsets):
+            p.grad = self.avg[o:o + p.data.size].reshape(p.data.shape)
         for b in self.buckets:
-            for pi, p in enumerate(b.params):
-                off = b.offsets[pi]
-                p.grad = b.out[off:off + p.data.size].reshape(p.data.shape)
-            b.pending = [len(b.params)] * W
             b.flushed = [False] * W
             b.reduced = False
         self.comm_wait_s += time.perf_counter() - t0

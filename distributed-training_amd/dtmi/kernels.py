@@ -272,8 +272,18 @@ def layernorm_fwd(x: DeviceArray, w: DeviceArray, b: DeviceArray, eps: float = 1
     return y, mean, rstd
 
 
-def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceArray, rstd: DeviceArray):
-    """Returns (dx, dw, db)."""
+def _out_or_new(out, shape, dtype, what):
+    """A caller-provided output (contiguous, of `shape` and `dtype`) or a new array."""
+    if out is None:
+        return empty(shape, dtype)
+    if tuple(out.shape) != tuple(shape) or out.dtype != np.dtype(dtype) or not out.is_contiguous:
+        raise ValueError(f"{what}: output must be a contiguous {np.dtype(dtype).name} array of shape {tuple(shape)}")
+    return out
+
+
+def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceArray, rstd: DeviceArray,
+                  dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None):
+    """Returns (dx, dw, db); dw / db are written into dw_out / db_out when given."""
     _contig(dy, x, w, mean, rstd)
     if dy.shape != x.shape:
         raise ValueError("layernorm_bwd: dy/x shape mismatch")
@@ -282,8 +292,8 @@ def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceA
     if mean.size != rows or rstd.size != rows:
         raise ValueError("layernorm_bwd: bad row statistics")
     dx = empty(x.shape, x.dtype)
-    dw = empty((C_,), x.dtype)
-    db = empty((C_,), x.dtype)
+    dw = _out_or_new(dw_out, (C_,), x.dtype, "layernorm_bwd")
+    db = _out_or_new(db_out, (C_,), x.dtype, "layernorm_bwd")
     _c("dtmi_layernorm_bwd", _dt(dy, x, w, mean, rstd), dx.ptr, dw.ptr, db.ptr, dy.ptr, x.ptr, w.ptr, mean.ptr,
        rstd.ptr, rows, C_, 0)
     return dx, dw, db
@@ -352,12 +362,13 @@ def embedding_segments(idx: np.ndarray):
     return perm, seg_start, seg_row
 
 
-def embedding_bwd(dout: DeviceArray, V: int, segs) -> DeviceArray:
-    """segs: device int32 arrays (perm, seg_start, seg_row)."""
+def embedding_bwd(dout: DeviceArray, V: int, segs, out: DeviceArray | None = None) -> DeviceArray:
+    """segs: device int32 arrays (perm, seg_start, seg_row); the [V, C] table
+    gradient is written into `out` when given."""
     _contig(dout)
     C_ = dout.shape[-1]
     perm, seg_start, seg_row = segs
-    dw = empty((V, C_), dout.dtype)
+    dw = _out_or_new(out, (V, C_), dout.dtype, "embedding_bwd")
     _c("dtmi_embedding_bwd", _dt(dout), dw.ptr, dout.ptr, perm.ptr, seg_start.ptr, seg_row.ptr, seg_row.size, V,
        C_, 1)
     return dw
@@ -411,8 +422,10 @@ def linear_fwd(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None) -> Device
     return y
 
 
-def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, need_db=True):
-    """Returns (dx, dw, db) for y = x @ w + b with x [M, K], w [K, N]."""
+def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, need_db=True,
+               dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None):
+    """Returns (dx, dw, db) for y = x @ w + b with x [M, K], w [K, N]; dw / db
+    are written into dw_out / db_out when given."""
     _contig(x2, w, dy2)
     M, K = x2.shape
     N = w.shape[1]
@@ -423,8 +436,8 @@ def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, 
     if need_dx:
         dx = empty((M, K), x2.dtype)
         _c("dtmi_linear_bwd_dx", dt, dx.ptr, dy2.ptr, w.ptr, M, K, N, 0)
-    dw = empty((K, N), x2.dtype)
-    db = empty((N,), x2.dtype) if need_db else None
+    dw = _out_or_new(dw_out, (K, N), x2.dtype, "linear_bwd")
+    db = _out_or_new(db_out, (N,), x2.dtype, "linear_bwd") if need_db else None
     _c("dtmi_linear_bwd_dw", dt, dw.ptr, db.ptr if db is not None else None, x2.ptr, dy2.ptr, M, K, N, 0)
     return dx, dw, db
 

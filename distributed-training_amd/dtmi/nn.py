@@ -23,7 +23,7 @@ import numpy as np
 
 from . import device as dev
 from . import kernels as K
-from .autograd import Indices, Tensor, _contig, as_indices, cross_entropy, embedding, layer_norm
+from .autograd import Indices, Tensor, _contig, as_indices, cross_entropy, embedding, grad_out, layer_norm
 
 
 class Module:
@@ -83,7 +83,8 @@ def linear(x: Tensor, w: Tensor, b: Tensor | None) -> Tensor:
 
     def bw(g):
         g2 = _contig(g).reshape(-1, W.shape[1])
-        dx, dw, db = K.linear_bwd(X2, W, g2, need_dx=x.requires_grad, need_db=b is not None)
+        dx, dw, db = K.linear_bwd(X2, W, g2, need_dx=x.requires_grad, need_db=b is not None, dw_out=grad_out(w),
+                                  db_out=grad_out(b) if b is not None else None)
         dx = dx.reshape(X.shape) if dx is not None else None
         return (dx, dw, db) if b is not None else (dx, dw)
     parents = (x, w, b) if b is not None else (x, w)

@@ -20,6 +20,20 @@ from . import kernels as K
 from .device import DeviceArray
 
 
+def _one_run(arrays):
+    """A 1-D view covering `arrays` when they are contiguous and lie back to
+    back in one allocation (in list order), else None."""
+    if not arrays or any(a is None or not a.is_contiguous for a in arrays):
+        return None
+    a0 = arrays[0]
+    end = a0.offset + a0.nbytes
+    for a in arrays[1:]:
+        if a.block is not a0.block or a.offset != end or a.dtype != a0.dtype:
+            return None
+        end += a.nbytes
+    return DeviceArray(a0.block, ((end - a0.offset) // a0.itemsize,), a0.dtype, a0.offset)
+
+
 class AdamW:
     def __init__(self, params, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1):
         self.params = list(params)  # DeviceArrays, updated in place
@@ -45,8 +59,12 @@ class AdamW:
         gs_dev = grad_scale if isinstance(grad_scale, DeviceArray) else None
         gs = 1.0 if gs_dev is not None else float(grad_scale)
         grads = list(grads)
-        if len(self.params) == 1 and grads[0] is not None and grads[0].is_contiguous and self.params[0].is_contiguous:
-            K.adamw(self.params[0], grads[0], self.m[0], self.v[0], self.lr, self.b1, self.b2, self.eps, self.wd,
+        P, G = _one_run(self.params), _one_run(grads)
+        if P is not None and G is not None:
+            # parameters and gradients are each one contiguous run (e.g. a
+            # packed model and DDP's averaged gradients): one flat launch
+            n = P.size
+            K.adamw(P, G, self._mflat[:n], self._vflat[:n], self.lr, self.b1, self.b2, self.eps, self.wd,
                     b1t, b2t, gscale=gs, gscale_dev=gs_dev)
             return
         gl = [None if g is None else (g if g.is_contiguous else g.contiguous()) for g in grads]

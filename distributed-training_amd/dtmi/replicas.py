@@ -17,6 +17,7 @@ from __future__ import annotations
 import contextlib
 
 from . import _lib
+from . import device as dev
 from . import kernels as K
 from .device import DeviceArray
 
@@ -38,6 +39,7 @@ class SimGroup:
         self.world = world
         self.rank = 0
         self._listeners = []
+        self._after = []
 
     def set_rank(self, r: int):
         if not 0 <= r < self.world:
@@ -45,7 +47,9 @@ class SimGroup:
         if r != self.rank:
             for fn in self._listeners:
                 fn(self.rank)
-        self.rank = r
+            self.rank = r
+            for fn in self._after:
+                fn(r)
 
     @contextlib.contextmanager
     def replica(self, r: int):
@@ -57,6 +61,10 @@ class SimGroup:
         """fn(previous_rank) is called before the running replica changes."""
         self._listeners.append(fn)
 
+    def on_rank_set(self, fn):
+        """fn(new_rank) is called after the running replica has changed."""
+        self._after.append(fn)
+
     def broadcast(self, arr, root=0):
         """Replicas share one copy of the parameters: identical by construction."""
         return arr
@@ -67,3 +75,56 @@ class SimGroup:
     def average(self, out: DeviceArray, rows: DeviceArray, partials: DeviceArray | None = None):
         """out = (((rows[0] + rows[1]) + ...) + rows[W-1]) * (1.0 / W)."""
         K.bucket_average(out, rows, self.world, 1.0 / self.world, partials=partials)
+
+
+class ReplicaGrads:
+    """Every replica's gradients in HBM: a [W, n] buffer, one row per replica,
+    each row holding all parameters' gradients back to back in forward
+    (definition) order.
+
+    The running replica's slot for each parameter is installed as that
+    parameter's `grad_dest`, so the backward kernels that produce parameter
+    gradients (Linear dW/db, LayerNorm dgamma/dbeta, the embedding table)
+    write them straight into the row: the copy dtrain makes to fill its
+    buckets (ddp.py:73-81, zero.py:46-53) is needed only for a gradient that
+    did not land in its slot (`place`). Slots of parameters that received no
+    gradient are zero-filled (`zero`).
+    """
+
+    def __init__(self, params, pg: "SimGroup", dtype):
+        self.params = list(params)
+        self.pg = pg
+        self.offsets = []
+        off = 0
+        for p in self.params:
+            self.offsets.append(off)
+            off += p.data.size
+        self.n = off
+        self.rows = dev.empty((pg.world, max(off, 1)), dtype)
+        self.index = {id(p): i for i, p in enumerate(self.params)}
+        self._dest = [[self.rows[r][o:o + p.data.size].reshape(p.data.shape)
+                       for p, o in zip(self.params, self.offsets)] for r in range(pg.world)]
+        self.attach(pg.rank)
+        pg.on_rank_set(self.attach)
+
+    def attach(self, r: int):
+        for p, d in zip(self.params, self._dest[r]):
+            p.grad_dest = d
+
+    def slot(self, r: int, i: int) -> DeviceArray:
+        return self._dest[r][i]
+
+    def place(self, r: int, i: int, g: DeviceArray):
+        """Make replica r's slot i hold g (a copy unless g already is the slot)."""
+        d = self._dest[r][i]
+        if g.ptr != d.ptr:
+            K.copy_into(d, g)
+
+    def zero(self, r: int, i: int):
+        self._dest[r][i].zero_()
+
+    def columns(self, lo: int, hi: int) -> DeviceArray:
+        """The [W, hi - lo] view of columns lo..hi of every replica's row."""
+        isz = self.rows.itemsize
+        return DeviceArray(self.rows.block, (self.pg.world, hi - lo), self.rows.dtype, self.rows.offset + lo * isz,
+                           (self.rows.strides[0], 1))

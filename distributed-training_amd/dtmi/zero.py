@@ -4,8 +4,9 @@ All parameters live in one contiguous device buffer in forward order and each
 parameter's `.data` is a view into it (zero.py:29-35); the buffer is
 partitioned with dtrain's `partition` and rank r owns flat[b[r]:b[r+1]]
 (`.shard`, `.bounds`). Each replica's backward flattens its gradients into its
-own row of a [W, n] buffer (grad-ready hooks; zero.py:46-53 flattens after
-backward). `step()` then, for every shard in rank order: the fixed-order sum of
+own row of a [W, n] buffer in forward order: the backward kernels write
+each gradient straight into its slot (see dtmi.replicas.ReplicaGrads), where
+zero.py:46-53 flattens after backward. `step()` then, for every shard in rank order: the fixed-order sum of
 the replicas' rows times 1/W (the reduce-scatter plus `g *= 1/W` of
 zero.py:54-55, in dtrain's direct order), its float64 sum of squares, summed
 over shards in rank order (the all-reduce of zero.py:56-57); the clip factor
@@ -23,7 +24,7 @@ from . import device as dev
 from . import kernels as K
 from .device import DeviceArray
 from .optim import AdamW, clip_scale_device
-from .replicas import partition
+from .replicas import ReplicaGrads, partition
 
 
 class _ShardOpt:
@@ -81,18 +82,14 @@ class ZeroAdamW:
         pg.broadcast(self.flat, root=0)
         self.n = n
         self.bounds = partition(n, pg.world)
-        self.gflat = dev.empty((pg.world, n), dtype)
+        self.grads = ReplicaGrads(self.params, pg, dtype)
+        self.gflat = self.grads.rows  # [W, n]: each replica's gradients in forward order
         self._full = AdamW([self.flat], **adam)
         self.opts = [_ShardOpt(self._full, self.bounds[r], self.bounds[r + 1]) for r in range(pg.world)]
         self.max_grad_norm = max_grad_norm
         self._norm = None
-        self._offsets = []
-        off = 0
-        for p in self.params:
-            self._offsets.append(off)
-            off += p.data.size
-        self._ready = [dict() for _ in range(pg.world)]
-        self._index = {id(p): i for i, p in enumerate(self.params)}
+        self._ready = [set() for _ in range(pg.world)]
+        self._index = self.grads.index
         for p in self.params:
             p.register_grad_ready_hook(self._on_grad)
         self._nblocks = [K.average_blocks(self.bounds[r + 1] - self.bounds[r]) for r in range(pg.world)]
@@ -117,22 +114,20 @@ class ZeroAdamW:
         return self._norm
 
     def _on_grad(self, p):
-        self._ready[self.pg.rank][self._index[id(p)]] = p.grad
+        r, i = self.pg.rank, self._index[id(p)]
+        self.grads.place(r, i, p.grad)
+        self._ready[r].add(i)
 
-    def _flatten(self, r):
-        srcs = []
-        for i, p in enumerate(self.params):
-            g = self._ready[r].get(i)
-            if g is not None and not g.is_contiguous:
-                g = g.contiguous()
-            srcs.append(g.reshape(-1) if g is not None else None)  # zero.py:49-50
-        K.bucket_flatten(self.gflat[r], srcs, [p.data.size for p in self.params])
+    def _complete(self, r):
+        for i in range(len(self.params)):
+            if i not in self._ready[r]:
+                self.grads.zero(r, i)  # zero.py:49-50
         self._ready[r].clear()
 
     def step(self):
         W = self.pg.world
         for r in range(W):
-            self._flatten(r)
+            self._complete(r)
         g = dev.empty((self.n,), self.flat.dtype)
         sq = dev.empty((1,), np.float64)
         isz = np.dtype(self.flat.dtype).itemsize
