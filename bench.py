@@ -24,6 +24,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -183,7 +184,7 @@ def main(argv=None):
     gemm_tflops = work / (ms * 1e-3) / 1e12 if ms else 0.0
     roofline = {"bound": "mfma", "kernel": "gemm_kernel (MFMA f32 32x32x2, Linear fwd/dX/dW)",
                 "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                "frac": round(gemm_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": None,
+                "frac": round(gemm_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": _profiled_traffic(),
                 "launches": n, "avg_launch_ms": round(ms / max(n, 1), 4),
                 "flop_per_step": gemm_flops_per_step(CFG, BATCH, WORLD)}
     kernels = {}
@@ -256,6 +257,20 @@ def _line(metric, value, unit, a, ms, config, roofline, cpu, extra=None):
     if extra:
         out.update(extra)
     return out
+
+
+TRAFFIC_PROFILE = ROOT / "profiles" / "gpt2_small_step_traffic.md"
+
+
+def _profiled_traffic():
+    """HBM-side bytes per GEMM launch of this workload, as measured with
+    rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-calibrated) and recorded in
+    profiles/gpt2_small_step_traffic.md; None when that file is absent."""
+    try:
+        m = re.search(r"traffic_bytes_per_launch = (\d+)", TRAFFIC_PROFILE.read_text())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
 
 
 def _mfma_peak(dtype):
@@ -381,7 +396,7 @@ def micro_bucket_adamw(a):
     if not a.no_cpu_baseline:
         from oracle import optim as OO
         from oracle.ddp import fixed_order_sum
-        k = n // 16
+        k = n
         rr = rng.standard_normal((W, k)).astype(dt)
         t0 = time.perf_counter()
         gg = fixed_order_sum(list(rr))
@@ -391,7 +406,7 @@ def micro_bucket_adamw(a):
         OO.adamw_update(pp, gg * s, mm, vv, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t)
         t = time.perf_counter() - t0
         cpu = {"value": round((5 + 7) * k * dt.itemsize / t / 1e9, 2), "unit": "GB/s", "cores": _threads(),
-               "kind": "port", "sample": f"oracle average + clip + AdamW over {k} of the {n} elements ({t:.2f} s)"}
+               "kind": "port", "sample": f"oracle average + clip + AdamW over all {k} elements ({t:.2f} s)"}
     return _line("gradient bucket average + AdamW bandwidth over 124,439,808 params (4 replicas)",
                  round(total_bytes / (total_ms * 1e-3) / 1e9, 1), "GB/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"124,439,808-element 4-replica fixed-order average + clip + AdamW (full + 1/4 shard) "
