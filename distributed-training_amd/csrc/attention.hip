@@ -231,6 +231,20 @@ __device__ __forceinline__ void store_result(T* __restrict__ lds, const typename
 
 // ----------------------------------------------------------------- forward
 // rowmax is kept in base-2 units: m = log2(e) * max_j (q . k_j * scale).
+// Blocks are dealt to the 8 XCDs round-robin by linear block id, and every
+// query (or key) block of one (batch, head) reads the same K/V (or Q/dO)
+// rows. Remap the linear id so each XCD gets a contiguous range of
+// (batch, head) pairs with all of their blocks: those rows are fetched once
+// per XCD's L2 instead of once per XCD.
+__device__ __forceinline__ void xcd_block(int& bx, int& by) {
+  const int gx = (int)gridDim.x;
+  const int total = gx * (int)gridDim.y;
+  int L = (int)blockIdx.x + gx * (int)blockIdx.y;
+  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
+  bx = L % gx;
+  by = L / gx;
+}
+
 template <typename T, int DP>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
   using M = AM<T>;
@@ -241,10 +255,11 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
   constexpr int LDS_N = 2 * STAGE > QB * LD ? 2 * STAGE : QB * LD;
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
 
-  const int bh = blockIdx.y;
+  int bx, bh;
+  xcd_block(bx, bh);
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
-  const int q0 = (int)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
+  const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
   const int wq0 = q0 + wave * MT;
@@ -364,10 +379,11 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
   __shared__ T stats[2][3][QT];
 
-  const int bh = blockIdx.y;
+  int bx, bh;
+  xcd_block(bx, bh);
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
-  const int k0 = (int)blockIdx.x * KBB;
+  const int k0 = bx * KBB;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
   const int wk0 = k0 + wave * MT;
@@ -473,10 +489,11 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   constexpr int LDS_N = 2 * STAGE > QB * LD ? 2 * STAGE : QB * LD;
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
 
-  const int bh = blockIdx.y;
+  int bx, bh;
+  xcd_block(bx, bh);
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
-  const int q0 = (int)(gridDim.x - 1 - blockIdx.x) * QB;  // longest causal rows first
+  const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
   const int wq0 = q0 + wave * MT;
