@@ -35,6 +35,7 @@
 // Small tile counts with long K are split along K; the split partials are
 // summed in split order by a second kernel (deterministic, no atomics).
 #include "common.h"
+#include "gelu.h"
 
 namespace dtmi {
 
@@ -76,7 +77,32 @@ struct GemmArgs {
   int64_t k_per_split;
   int tiles_m, tiles_n;
   int accumulate;
+  // Epilogue fusions (applied after the bias, in this order):
+  const void* addend;  // residual: v = addend[m, n] + v   (row stride ldc)
+  int epi;             // kEpiGeluFwd: aux = gelu(v), C keeps v; kEpiGeluBwd: C = gelu'(aux) * v
+  void* aux;           // [M, N] with row stride ldc
 };
+
+constexpr int kEpiNone = 0, kEpiGeluFwd = 1, kEpiGeluBwd = 2;
+
+// The fused epilogue of one output element v (the k-sum of row m, column n):
+// bias, residual, accumulate, GELU -- the operation order of the unfused
+// graph (Linear adds its bias, then the residual add, then GELU / its
+// backward as dtrain/autograd.py:133-144 computes them).
+template <typename T>
+__device__ __forceinline__ void epilogue_store(const GemmArgs& a, T* __restrict__ C, int64_t ldc, int64_t m,
+                                               int64_t n, T v, int64_t batch) {
+  if (a.bias) v = v + ((const T*)a.bias)[n];
+  const int64_t o = m * ldc + n;
+  if (a.addend) v = ((const T*)a.addend)[batch * a.sC + o] + v;
+  if (a.accumulate) v = C[o] + v;
+  if (a.epi == kEpiGeluFwd) {
+    ((T*)a.aux)[batch * a.sC + o] = gelu_f<T>(v);
+  } else if (a.epi == kEpiGeluBwd) {
+    v = gelu_b<T>(((const T*)a.aux)[batch * a.sC + o], v);
+  }
+  C[o] = v;
+}
 
 constexpr int kKC = 8;
 // k-tile: 16 floats or 8 doubles
@@ -373,49 +399,86 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs a) {
     __syncthreads();
   }
 
-  // epilogue
+  // epilogue: split-K partials go to the workspace as they are; otherwise
+  // the fused epilogue writes C (and aux)
   const bool to_ws = a.ws != nullptr;
   T* C = to_ws ? (T*)a.ws + ((int64_t)split * gridDim.z + batch) * a.M * a.N : (T*)a.C + batch * a.sC;
   const int64_t ldc = to_ws ? a.N : a.ldc;
-  const T* bias = (const T*)a.bias;
+  const bool plain = to_ws || (a.addend == nullptr && a.epi == kEpiNone && !a.accumulate);
+  if (plain) {  // raw split-K partial, or v + bias
+    const T* bias = to_ws ? nullptr : (const T*)a.bias;
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int64_t n = n0 + wn0 + j * MT + c;
-      if (n >= a.N) continue;
-      const T bn = (!to_ws && bias) ? bias[n] : T(0);
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = n0 + wn0 + j * MT + c;
+        if (n >= a.N) continue;
+        const T bn = bias ? bias[n] : T(0);
 #pragma unroll
-      for (int r = 0; r < NACC; ++r) {
-        const int64_t m = m0 + wm0 + i * MT + MFT::row(r, g);
-        if (m >= a.M) continue;
-        T v = acc[i][j][r];
-        if (!to_ws) {
+        for (int r = 0; r < NACC; ++r) {
+          const int64_t m = m0 + wm0 + i * MT + MFT::row(r, g);
+          if (m >= a.M) continue;
+          T v = acc[i][j][r];
           if (bias) v = v + bn;
-          if (a.accumulate) v = C[m * ldc + n] + v;
+          C[m * ldc + n] = v;
         }
-        C[m * ldc + n] = v;
       }
-    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = n0 + wn0 + j * MT + c;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int r = 0; r < NACC; ++r) {
+          const int64_t m = m0 + wm0 + i * MT + MFT::row(r, g);
+          if (m >= a.M) continue;
+          epilogue_store<T>(a, C, ldc, m, n, acc[i][j][r], batch);
+        }
+      }
+  }
 }
 
-template <typename T>
-__global__ void __launch_bounds__(256) splitk_reduce_kernel(T* __restrict__ C, const T* __restrict__ ws,
-                                                             const T* __restrict__ bias, int splits, int64_t batch,
-                                                             int64_t M, int64_t N, int64_t ldc, int64_t sC,
-                                                             int accumulate) {
+// Sum of the split-K partials in split order 0, 1, ..., S-1, then the
+// epilogue. PLAIN (bias only): VEC consecutive columns per thread.
+template <typename T, bool PLAIN, int VEC>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T* __restrict__ ws, int splits,
+                                                             int64_t batch) {
+  const int64_t M = a.M, N = a.N;
   const int64_t total = batch * M * N;
+  const int64_t nvec = total / VEC;  // VEC divides N
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+  const T* __restrict__ bias = (const T*)a.bias;
+  for (int64_t iv = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; iv < nvec; iv += stride) {
+    const int64_t idx = iv * VEC;
     const int64_t b = idx / (M * N);
     const int64_t rem = idx - b * M * N;
-    const int64_t m = rem / N, n = rem - (rem / N) * N;
-    T v = ws[idx];
-    for (int s = 1; s < splits; ++s) v = v + ws[(int64_t)s * total + idx];
-    if (bias) v = v + bias[n];
-    T* dst = C + b * sC + m * ldc + n;
-    if (accumulate) v = *dst + v;
-    *dst = v;
+    const int64_t m = rem / N, n = rem - m * N;
+    T* C = (T*)a.C + b * a.sC;
+    if (VEC > 1) {  // 16-byte vectors: every operand is aligned (checked by the host)
+      typedef T vt __attribute__((ext_vector_type(VEC)));
+      vt v = *reinterpret_cast<const vt*>(ws + idx);
+      for (int s = 1; s < splits; ++s) v = v + *reinterpret_cast<const vt*>(ws + (int64_t)s * total + idx);
+      if (bias) v = v + *reinterpret_cast<const vt*>(bias + n);
+      *reinterpret_cast<vt*>(C + m * a.ldc + n) = v;
+      continue;
+    }
+    T v[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) v[e] = ws[idx + e];
+    for (int s = 1; s < splits; ++s) {
+      const T* w = ws + (int64_t)s * total + idx;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) v[e] = v[e] + w[e];
+    }
+    if (PLAIN) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) C[m * a.ldc + n + e] = bias ? v[e] + bias[n + e] : v[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) epilogue_store<T>(a, C, a.ldc, m, n + e, v[e], b);
+    }
   }
 }
 
@@ -443,10 +506,16 @@ static void launch_layout(const GemmArgs& a, dim3 grid, int akc, int bkc, bool v
     launch_variant<T, BM, BN, false, false>(a, grid, veca, vecb);
 }
 
+struct EpiArgs {
+  const void* addend = nullptr;
+  int epi = kEpiNone;
+  void* aux = nullptr;
+};
+
 template <typename T>
 static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int64_t sA,
                      const void* B, int64_t ldb, int64_t sB, void* C, int64_t ldc, int64_t sC, int64_t batch,
-                     const void* bias, int accumulate, int force_splits) {
+                     const void* bias, int accumulate, int force_splits, const EpiArgs& ep) {
   constexpr int VEC = MF<T>::VEC;
   GemmArgs a{};
   a.A = A;
@@ -463,6 +532,9 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   a.sB = sB;
   a.sC = sC;
   a.accumulate = accumulate;
+  a.addend = ep.addend;
+  a.epi = ep.epi;
+  a.aux = ep.aux;
   // K splits. A grid of b blocks on C CUs runs ceil(b / C) rounds, so its
   // useful fraction is b / (C * ceil(b / C)); take the fewest splits (each
   // keeping >= 256 of K) that reach 90 % of rounds, else the best found.
@@ -510,8 +582,18 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
     if (splits > 1) {
       int64_t total = batch * M * N;
       int rg = (int)(cdiv(total, 256 * 4) < 8192 ? cdiv(total, 256 * 4) : 8192);
-      splitk_reduce_kernel<T><<<rg, 256, 0, stream()>>>((T*)C, (const T*)ws, (const T*)bias, splits, batch, M, N,
-                                                        ldc, sC, accumulate);
+      GemmArgs r = a;
+      r.ws = nullptr;
+      const bool plain = a.addend == nullptr && a.epi == kEpiNone && !a.accumulate;
+      constexpr int V = 16 / sizeof(T);
+      const bool vec_ok = N % V == 0 && ldc % V == 0 && (batch == 1 || sC % V == 0) && aligned(C, 16) &&
+                          (!bias || aligned(bias, 16));
+      if (plain && vec_ok)
+        splitk_reduce_kernel<T, true, V><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
+      else if (plain)
+        splitk_reduce_kernel<T, true, 1><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
+      else
+        splitk_reduce_kernel<T, false, 1><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
     }
   }
   hipError_t le = hipGetLastError();
@@ -522,7 +604,8 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
 
 static int gemm_dispatch(int dtype, int akc, int bkc, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
                          int64_t sA, const void* B, int64_t ldb, int64_t sB, void* C, int64_t ldc, int64_t sC,
-                         int64_t batch, const void* bias, int accumulate, int force_splits) {
+                         int64_t batch, const void* bias, int accumulate, int force_splits,
+                         const EpiArgs& ep = EpiArgs()) {
   DTMI_DTYPE_OK(dtype);
   DTMI_CHECK(M >= 0 && N >= 0 && K >= 0 && batch >= 1, "dtmi_gemm: bad sizes M=%lld N=%lld K=%lld batch=%lld",
              (long long)M, (long long)N, (long long)K, (long long)batch);
@@ -531,11 +614,12 @@ static int gemm_dispatch(int dtype, int akc, int bkc, int64_t M, int64_t N, int6
   DTMI_CHECK(ldc >= N, "dtmi_gemm: ldc %lld < N %lld", (long long)ldc, (long long)N);
   DTMI_CHECK(K == 0 || (akc ? lda >= K : lda >= M), "dtmi_gemm: lda too small");
   DTMI_CHECK(K == 0 || (bkc ? ldb >= K : ldb >= N), "dtmi_gemm: ldb too small");
+  DTMI_CHECK(ep.epi == kEpiNone || ep.aux != nullptr, "dtmi_gemm: GELU epilogue without its array");
   if (dtype == DTMI_F32)
     return gemm_impl<float>(akc, bkc, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, batch, bias, accumulate,
-                            force_splits);
+                            force_splits, ep);
   return gemm_impl<double>(akc, bkc, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, batch, bias, accumulate,
-                           force_splits);
+                           force_splits, ep);
 }
 
 }  // namespace dtmi
@@ -558,6 +642,31 @@ DTMI_EXPORT int dtmi_linear_fwd(int dtype, void* Y, const void* X, const void* W
   DTMI_BODY_BEGIN
   DTMI_REQUIRE_INIT();
   return gemm_dispatch(dtype, 1, 0, M, N, K, X, K, 0, W, N, 0, Y, N, 0, 1, b, 0, 0);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_fwd_fused(int dtype, void* Y, void* act, const void* X, const void* W, const void* b,
+                                      const void* residual, int64_t M, int64_t K, int64_t N) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  EpiArgs ep;
+  ep.addend = residual;
+  ep.epi = act ? kEpiGeluFwd : kEpiNone;
+  ep.aux = act;
+  DTMI_CHECK(!(act && residual), "dtmi_linear_fwd_fused: GELU and residual are not fused together");
+  return gemm_dispatch(dtype, 1, 0, M, N, K, X, K, 0, W, N, 0, Y, N, 0, 1, b, 0, 0, ep);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_bwd_dx_gelu(int dtype, void* dX, const void* dY, const void* W, const void* pre,
+                                        int64_t M, int64_t K, int64_t N) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_CHECK(pre != nullptr, "dtmi_linear_bwd_dx_gelu: NULL pre-activation");
+  EpiArgs ep;
+  ep.epi = kEpiGeluBwd;
+  ep.aux = const_cast<void*>(pre);
+  return gemm_dispatch(dtype, 1, 1, M, K, N, dY, N, 0, W, N, 0, dX, K, 0, 1, nullptr, 0, 0, ep);
   DTMI_BODY_END
 }
 

@@ -70,6 +70,8 @@ SIGNATURES: dict[str, list] = {
     "dtmi_linear_fwd": [i32, vp, vp, vp, vp, i64, i64, i64],
     "dtmi_linear_bwd_dx": [i32, vp, vp, vp, i64, i64, i64, i32],
     "dtmi_linear_bwd_dw": [i32, vp, vp, vp, vp, i64, i64, i64, i32],
+    "dtmi_linear_fwd_fused": [i32, vp, vp, vp, vp, vp, vp, i64, i64, i64],
+    "dtmi_linear_bwd_dx_gelu": [i32, vp, vp, vp, vp, i64, i64, i64],
     "dtmi_attn_fwd": [i32, i64, i64, i64, i64, f64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, vp],
     "dtmi_attn_bwd": [i32, i64, i64, i64, i64, f64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, vp,
                       vp, pi64, vp, pi64, vp, pi64],

@@ -422,10 +422,32 @@ def linear_fwd(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None) -> Device
     return y
 
 
+def linear_fwd_fused(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None, residual: DeviceArray | None = None,
+                     gelu: bool = False):
+    """y = x @ w + b, plus `residual` (y = residual + (x @ w + b)) or, with
+    gelu=True, also act = gelu(y). Returns (y, act or None)."""
+    _contig(x2, w)
+    M, K = x2.shape
+    K2, N = w.shape
+    if K != K2:
+        raise ValueError("linear: shape mismatch")
+    if residual is not None:
+        _contig(residual)
+        if residual.shape != (M, N) or residual.dtype != x2.dtype:
+            raise ValueError("linear: residual must match the output")
+    y = empty((M, N), x2.dtype)
+    act = empty((M, N), x2.dtype) if gelu else None
+    _c("dtmi_linear_fwd_fused", _dt(x2, w), y.ptr, act.ptr if act is not None else None, x2.ptr, w.ptr,
+       b.ptr if b is not None else None, residual.ptr if residual is not None else None, M, K, N)
+    return y, act
+
+
 def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, need_db=True,
-               dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None):
+               dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None,
+               gelu_pre: DeviceArray | None = None):
     """Returns (dx, dw, db) for y = x @ w + b with x [M, K], w [K, N]; dw / db
-    are written into dw_out / db_out when given."""
+    are written into dw_out / db_out when given. With gelu_pre (the [M, K]
+    pre-activation whose GELU is x), dx is the gradient of that pre-activation."""
     _contig(x2, w, dy2)
     M, K = x2.shape
     N = w.shape[1]
@@ -435,7 +457,13 @@ def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, 
     dx = None
     if need_dx:
         dx = empty((M, K), x2.dtype)
-        _c("dtmi_linear_bwd_dx", dt, dx.ptr, dy2.ptr, w.ptr, M, K, N, 0)
+        if gelu_pre is not None:
+            _contig(gelu_pre)
+            if gelu_pre.shape != (M, K):
+                raise ValueError("linear_bwd: pre-activation shape mismatch")
+            _c("dtmi_linear_bwd_dx_gelu", dt, dx.ptr, dy2.ptr, w.ptr, gelu_pre.ptr, M, K, N)
+        else:
+            _c("dtmi_linear_bwd_dx", dt, dx.ptr, dy2.ptr, w.ptr, M, K, N, 0)
     dw = _out_or_new(dw_out, (K, N), x2.dtype, "linear_bwd")
     db = _out_or_new(db_out, (N,), x2.dtype, "linear_bwd") if need_db else None
     _c("dtmi_linear_bwd_dw", dt, dw.ptr, db.ptr if db is not None else None, x2.ptr, dy2.ptr, M, K, N, 0)

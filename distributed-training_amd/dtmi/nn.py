@@ -8,12 +8,15 @@ very values a dtrain GPT of the same config and seed holds. After construction
 GPT packs every parameter into one contiguous device buffer in that order
 (`GPT.flat`); each parameter's `.data` is a view into it.
 
-Two ops are fused relative to dtrain's graph without changing the arithmetic:
+Ops are fused relative to dtrain's graph without changing the arithmetic:
 Linear runs x @ w + b as one GEMM with the bias added in its epilogue (the add
-node's backward becomes the GEMM's column-sum), and the attention block reads
-q, k, v straight out of the qkv projection and writes its output in [B, T, C]
-order, so the reshape / transpose / split of Block.forward (nn.py:100-103)
-cost no copies and the backward writes d(qkv) in place.
+node's backward becomes the GEMM's column-sum); the residual adds of
+Block.forward happen in the epilogue of the GEMM that produces the branch;
+the MLP's GELU and its backward run in the epilogues of the fc and out GEMMs;
+and the attention block reads q, k, v straight out of the qkv projection and
+writes its output in [B, T, C] order, so the reshape / transpose / split of
+Block.forward (nn.py:100-103) cost no copies and the backward writes d(qkv)
+in place.
 """
 from __future__ import annotations
 
@@ -73,22 +76,64 @@ def param(arr, name=None):
     return Tensor(arr, requires_grad=True, name=name)
 
 
-def linear(x: Tensor, w: Tensor, b: Tensor | None) -> Tensor:
-    """y = x @ w (+ b) for x [..., K], w [K, N], b [N]: one GEMM, bias fused."""
+def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = None) -> Tensor:
+    """y = x @ w (+ b) for x [..., K], w [K, N], b [N]: one GEMM, bias fused.
+    With `residual` (same shape as y): y = residual + (x @ w + b), the add
+    fused into the same epilogue; its gradient passes straight through."""
     X = _contig(x.data)
     lead = X.shape[:-1]
     X2 = X.reshape(-1, X.shape[-1])
     W = w.data
-    y = K.linear_fwd(X2, W, b.data if b is not None else None).reshape(*lead, W.shape[1])
+    R2 = _contig(residual.data).reshape(-1, W.shape[1]) if residual is not None else None
+    y, _ = K.linear_fwd_fused(X2, W, b.data if b is not None else None, residual=R2)
+    y = y.reshape(*lead, W.shape[1])
 
     def bw(g):
         g2 = _contig(g).reshape(-1, W.shape[1])
         dx, dw, db = K.linear_bwd(X2, W, g2, need_dx=x.requires_grad, need_db=b is not None, dw_out=grad_out(w),
                                   db_out=grad_out(b) if b is not None else None)
-        dx = dx.reshape(X.shape) if dx is not None else None
-        return (dx, dw, db) if b is not None else (dx, dw)
-    parents = (x, w, b) if b is not None else (x, w)
-    return Tensor._make(y, parents, bw)
+        out = [dx.reshape(X.shape) if dx is not None else None, dw]
+        if b is not None:
+            out.append(db)
+        if residual is not None:
+            out.append(g)
+        return tuple(out)
+    parents = [x, w] + ([b] if b is not None else []) + ([residual] if residual is not None else [])
+    return Tensor._make(y, tuple(parents), bw)
+
+
+def mlp(x: Tensor, fc: "Linear", out: "Linear", residual: Tensor) -> Tensor:
+    """residual + out(gelu(fc(x))), Block's MLP branch (dtrain/nn.py:105) as two
+    GEMMs: the fc GEMM's epilogue adds the bias and also writes gelu of the
+    result, the out GEMM's epilogue adds bias and residual; in the backward
+    the out layer's input-gradient GEMM applies the GELU backward in its
+    epilogue (dh = gelu'(h) * (g @ W_out^T)). Same operations, same order."""
+    X = _contig(x.data)
+    lead = X.shape[:-1]
+    X2 = X.reshape(-1, X.shape[-1])
+    Wf, Wo = fc.w.data, out.w.data
+    bf, bo = fc.b, out.b
+    h, act = K.linear_fwd_fused(X2, Wf, bf.data if bf is not None else None, gelu=True)
+    R2 = _contig(residual.data).reshape(-1, Wo.shape[1])
+    y, _ = K.linear_fwd_fused(act, Wo, bo.data if bo is not None else None, residual=R2)
+    y = y.reshape(*lead, Wo.shape[1])
+
+    def bw(g):
+        g2 = _contig(g).reshape(-1, Wo.shape[1])
+        dh, dwo, dbo = K.linear_bwd(act, Wo, g2, need_dx=True, need_db=bo is not None, dw_out=grad_out(out.w),
+                                    db_out=grad_out(bo) if bo is not None else None, gelu_pre=h)
+        dx, dwf, dbf = K.linear_bwd(X2, Wf, dh, need_dx=x.requires_grad, need_db=bf is not None,
+                                    dw_out=grad_out(fc.w), db_out=grad_out(bf) if bf is not None else None)
+        res = [dx.reshape(X.shape) if dx is not None else None, dwf]
+        if bf is not None:
+            res.append(dbf)
+        res.append(dwo)
+        if bo is not None:
+            res.append(dbo)
+        res.append(g)
+        return tuple(res)
+    parents = [x, fc.w] + ([bf] if bf is not None else []) + [out.w] + ([bo] if bo is not None else []) + [residual]
+    return Tensor._make(y, tuple(parents), bw)
 
 
 def qkv_attention(qkv: Tensor, heads: int) -> Tensor:
@@ -153,8 +198,8 @@ class Block(Module):
 
     def forward(self, x):
         a = qkv_attention(self.qkv(self.ln1(x)), self.c.heads)
-        x = x + self.proj(a)
-        return x + self.out(self.fc(self.ln2(x)).gelu())
+        x = linear(a, self.proj.w, self.proj.b, residual=x)  # x + self.proj(a)
+        return mlp(self.ln2(x), self.fc, self.out, residual=x)  # x + self.out(self.fc(self.ln2(x)).gelu())
 
 
 class GPT(Module):

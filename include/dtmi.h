@@ -248,6 +248,20 @@ int dtmi_linear_bwd_dx(int dtype, void* dX, const void* dY, const void* W, int64
 int dtmi_linear_bwd_dw(int dtype, void* dW, void* db, const void* X, const void* dY, int64_t M, int64_t K, int64_t N,
                        int accumulate);
 
+/* Linear with its neighbours fused into the GEMM epilogue, in the operation
+ * order of the unfused graph:
+ *  - residual != NULL: Y = residual + (X W + b), Block's `x + self.proj(...)`
+ *    and `x + self.out(...)` (dtrain/nn.py:104-105, the add of autograd.py:76-84);
+ *  - act != NULL: Y = X W + b is kept (the pre-activation) and act = gelu(Y)
+ *    (dtrain/autograd.py:133-138 applied to Linear's output, nn.py:105).
+ * The two are not combined in one call. */
+int dtmi_linear_fwd_fused(int dtype, void* Y, void* act, const void* X, const void* W, const void* b,
+                          const void* residual, int64_t M, int64_t K, int64_t N);
+/* dX = gelu'(pre) * (dY W^T): the Linear input gradient followed by the GELU
+ * backward of autograd.py:139-143 (pre = the saved pre-activation [M, K]). */
+int dtmi_linear_bwd_dx_gelu(int dtype, void* dX, const void* dY, const void* W, const void* pre, int64_t M, int64_t K,
+                            int64_t N);
+
 /* ------------------------------------------------------- causal attention
  * dtrain/autograd.py:226-247: o = softmax(q k^T * scale + causal mask) v over
  * (B, H, T, D), D <= 64 contiguous; each *_strides argument points at three

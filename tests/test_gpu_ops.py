@@ -183,3 +183,31 @@ def test_linear_forward_backward_at_layernorm_linear_workload(dev, dt):
     assert rel_err(dx.numpy(), gx) <= TOL[dt]
     assert rel_err(dgam.numpy(), ggam) <= TOL[dt]
     assert rel_err(dbet.numpy(), gbet) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("M,K,N", [(1024, 256, 512), (256, 4096, 96), (300, 68, 132)])
+def test_fused_linear_epilogues_equal_the_unfused_ops(dev, dt, M, K, N):
+    """Residual add, GELU and GELU backward in the GEMM epilogue give the same
+    bits as the separate kernels (with and without split-K)."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(M + K + N)
+    x = D.from_numpy(rng.standard_normal((M, K)).astype(dt))
+    w = D.from_numpy((rng.standard_normal((K, N)) * 0.05).astype(dt))
+    b = D.from_numpy(rng.standard_normal(N).astype(dt))
+    r = D.from_numpy(rng.standard_normal((M, N)).astype(dt))
+    y0 = K_.linear_fwd(x, w, b)
+    y_res, none = K_.linear_fwd_fused(x, w, b, residual=r)
+    assert none is None
+    assert bits_equal(y_res.numpy(), K_.binary("add", r, y0).numpy())
+    h, act = K_.linear_fwd_fused(x, w, b, gelu=True)
+    assert bits_equal(h.numpy(), y0.numpy())
+    assert bits_equal(act.numpy(), K_.gelu_fwd(y0).numpy())
+    # backward through gelu: dx of the pre-activation whose GELU is the input x
+    pre = D.from_numpy(rng.standard_normal((M, K)).astype(dt))
+    g = D.from_numpy(rng.standard_normal((M, N)).astype(dt))
+    dx_plain, _, _ = K_.linear_bwd(x, w, g, need_db=False)
+    dx_fused, _, _ = K_.linear_bwd(x, w, g, need_db=False, gelu_pre=pre)
+    assert bits_equal(dx_fused.numpy(), K_.gelu_bwd(pre, dx_plain).numpy())
+    ref = (x.numpy().astype(np.float64) @ w.numpy().astype(np.float64)) + b.numpy() + r.numpy()
+    assert rel_err(y_res.numpy(), ref) <= TOL[dt]
