@@ -21,9 +21,12 @@
 // both operands, so every product is a plain sum over the reduction index.
 //
 // Backward without atomics: kernel A owns a key block and loops over the query
-// blocks that see it (dK, dV accumulate in registers); kernel B owns a query
-// block and loops over its key blocks (dQ in registers). Both recompute
-// P = exp(s - max) / sum. Results are deterministic.
+// tiles that see it, recomputing P = exp(s - max) / sum (dK, dV accumulate in
+// registers) and writing dS = P * (dP - rowsum(dO * O)) to a [B, H, T, T]
+// workspace; kernel B owns a query block and accumulates dQ = dS K from it
+// (when the workspace would exceed 4 GiB, kernel B recomputes dS instead).
+// Float32 kernel A keeps its query and dO tiles also transposed in LDS so the
+// dK / dV MFMAs read them with 16-byte vectors. Results are deterministic.
 #include <cmath>
 
 #include "common.h"
@@ -77,6 +80,7 @@ struct AttnArgs {
   void *out, *dq, *dk, *dv;
   void *rowmax, *rowsum;  // [B, H, T]
   const void* drow;       // [B, H, T] rowsum(dO * O)
+  void* ds;               // [B, H, T, T] dS written by the key-block pass for the dQ pass (or NULL)
   Strides3 sq, sk, sv, so, sdo, sdq, sdk, sdv;
   int64_t B, H, T, D;
   double scale;
@@ -207,7 +211,39 @@ struct TileFetch {
       *reinterpret_cast<V*>(lds + rr * LD + d) = r[i];
     }
   }
+
+  // The same tile transposed: ldsT[d][row], row stride NR + 4 (keeps 16-byte
+  // alignment for the vector reads of mma_ldsT_regs).
+  static constexpr int LDT = NR + 4;
+  __device__ __forceinline__ void store_t(T* __restrict__ ldsT) const {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      if (TOTAL % 256 != 0 && f >= TOTAL) continue;
+      const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) ldsT[(d + e) * LDT + rr] = r[i][e];
+    }
+  }
 };
+
+// float32 form of mma_lds_t_regs reading a transposed tile ldsT[d][j] (row
+// stride LDT): MFMA steps i = 4a .. 4a+3 of lane group g use rows
+// j = 8a + 4g + 0..3, four consecutive floats, so one 16-byte read feeds four
+// MFMAs instead of one scalar read per MFMA.
+template <int DP, int LDT>
+__device__ __forceinline__ void mma_ldsT_regs(AM<float>::acc_t (&out)[DP / 32], const float* __restrict__ ldsT,
+                                              int jbase, const AM<float>::acc_t& pacc, int g, int c) {
+#pragma unroll
+  for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+    for (int dt = 0; dt < DP / 32; ++dt) {
+      const AM<float>::vec_t v =
+          *reinterpret_cast<const AM<float>::vec_t*>(ldsT + (dt * 32 + c) * LDT + jbase + 8 * a4 + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[dt] = AM<float>::mma(v[e], pacc[4 * a4 + e], out[dt]);
+    }
+}
 
 // Write a wave's MT x DP result (held transposed: lane column c = row of the
 // result, register rows = d) through LDS to global rows r0 + (0 .. NROWS).
@@ -372,12 +408,15 @@ template <typename T, int DP>
 __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  constexpr bool F32 = sizeof(T) == 4;
   constexpr int QT = MT;      // queries per tile
   constexpr int KBB = 4 * MT;  // keys per block
-  constexpr int TILE = QT * LD, STAGE = 2 * TILE;
+  constexpr int LDT = QT + 4;  // transposed tiles (float32): [DP][QT + 4]
+  constexpr int TILE = QT * LD, TILE_T = F32 ? DP * LDT : 0;
+  constexpr int STAGE = 2 * TILE + 2 * TILE_T;  // Q, dO (+ their transposes)
   constexpr int LDS_N = 2 * STAGE > KBB * LD ? 2 * STAGE : KBB * LD;
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
-  __shared__ T stats[2][3][QT];
+  __shared__ __attribute__((aligned(16))) T stats[2][3][QT];  // row max (base 2), 1 / row sum, rowsum(dO * O)
 
   int bx, bh;
   xcd_block(bx, bh);
@@ -395,6 +434,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   const T* RM = (const T*)a.rowmax + (int64_t)bh * Tn;
   const T* RS = (const T*)a.rowsum + (int64_t)bh * Tn;
   const T* DR = (const T*)a.drow + (int64_t)bh * Tn;
+  T* DS = a.ds ? (T*)a.ds + (int64_t)bh * Tn * Tn : nullptr;
   const T sl2 = (T)(a.scale * 1.4426950408889634);
   const bool vec = a.vec != 0;
 
@@ -414,11 +454,18 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
       const int r = qs + threadIdx.x;
       const bool ok = r < Tn;
       st0 = ok ? RM[r] : T(0);
-      st1 = ok ? RS[r] : T(1);
+      st1 = ok ? T(1) / RS[r] : T(1);
       st2 = ok ? DR[r] : T(0);
     }
   };
-  auto store_stats = [&](int stage) {
+  auto store_stage = [&](int stage) {
+    T* base = lds + stage * STAGE;
+    fq.store(base);
+    fg.store(base + TILE);
+    if constexpr (F32) {
+      fq.store_t(base + 2 * TILE);
+      fg.store_t(base + 2 * TILE + TILE_T);
+    }
     if (threadIdx.x < QT) {
       stats[stage][0][threadIdx.x] = st0;
       stats[stage][1][threadIdx.x] = st1;
@@ -429,9 +476,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
     fq.fetch(Q, a.sq.t, qs0, Tn, D, vec);
     fg.fetch(G, a.sdo.t, qs0, Tn, D, vec);
     fetch_stats(qs0);
-    fq.store(lds);
-    fg.store(lds + TILE);
-    store_stats(0);
+    store_stage(0);
   }
   __syncthreads();
   for (int it = 0; it < nqt; ++it) {
@@ -449,26 +494,43 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
     typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Qs, 0, kf, g, c);
     typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Gs, 0, vf, g, c);
     const bool mask = (qs < wk0 + MT - 1) || (qs + QT > Tn) || (wk0 + MT > Tn);
-#pragma unroll
-    for (int i = 0; i < NACC; ++i) {
-      const int rl = M::row(i, g);
-      T p = ex2(s[i] * sl2 - stats[cur][0][rl]) / stats[cur][1][rl];
+    auto prob = [&](int i, T m, T linv, T dr) {
+      T p = ex2(s[i] * sl2 - m) * linv;
       if (mask) {
-        const int r = qs + rl;
+        const int r = qs + M::row(i, g);
         p = (kj <= r && r < Tn && kj < Tn) ? p : T(0);
       }
       s[i] = p;
-      dp[i] = p * (dp[i] - stats[cur][2][rl]);
+      dp[i] = p * (dp[i] - dr);
+      if (DS) {
+        const int r = qs + M::row(i, g);
+        if (r < Tn && kj < Tn) DS[(int64_t)r * Tn + kj] = dp[i];
+      }
+    };
+    if constexpr (F32) {
+      // rows 8a + 4g + 0..3 of MFMA steps 4a .. 4a+3: one 16-byte read per statistic
+#pragma unroll
+      for (int a4 = 0; a4 < NACC / 4; ++a4) {
+        const int r0 = 8 * a4 + 4 * g;
+        const typename M::vec_t m4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][0][r0]);
+        const typename M::vec_t l4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][1][r0]);
+        const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) prob(4 * a4 + e, m4[e], l4[e], d4[e]);
+      }
+      // dV^T += dO^T P ; dK^T += Q^T dS (transposed tiles: vector reads)
+      mma_ldsT_regs<DP, LDT>(dv, Qs + 2 * TILE + TILE_T, 0, s, g, c);
+      mma_ldsT_regs<DP, LDT>(dk, Qs + 2 * TILE, 0, dp, g, c);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NACC; ++i) {
+        const int rl = M::row(i, g);
+        prob(i, stats[cur][0][rl], stats[cur][1][rl], stats[cur][2][rl]);
+      }
+      mma_lds_t_regs<T, DP>(dv, Gs, 0, s, g, c);
+      mma_lds_t_regs<T, DP>(dk, Qs, 0, dp, g, c);
     }
-    // dV^T += dO^T P ; dK^T += Q^T dS
-    mma_lds_t_regs<T, DP>(dv, Gs, 0, s, g, c);
-    mma_lds_t_regs<T, DP>(dk, Qs, 0, dp, g, c);
-    if (more) {
-      T* nxt = lds + (cur ^ 1) * STAGE;
-      fq.store(nxt);
-      fg.store(nxt + TILE);
-      store_stats(cur ^ 1);
-    }
+    if (more) store_stage(cur ^ 1);
     __syncthreads();
   }
   T* DK = (T*)a.dk + b * a.sdk.b + h * a.sdk.h;
@@ -479,6 +541,100 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
 }
 
 // ------------------------------------------------------- backward B: dQ
+// dQ from the dS the key-block pass wrote: dQ^T += K^T dS^T over the key
+// tiles up to the block's last query, with dS read straight into the MFMA B
+// operand (lane column = query, k-slot = key), so S, P and dP are not
+// recomputed. Key tiles wholly above a wave's queries are skipped by that
+// wave (their dS is zero).
+template <typename T, int DP>
+__global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
+  using M = AM<T>;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  constexpr bool F32 = sizeof(T) == 4;
+  constexpr int KT = MT;      // keys per tile
+  constexpr int QB = 4 * MT;  // queries per block
+  constexpr int LDT = KT + 4;
+  constexpr int TILE = F32 ? DP * LDT : KT * LD;  // K^T [DP][KT + 4] (float32) or K [KT][LD]
+  constexpr int LDS_N = 2 * TILE > QB * LD ? 2 * TILE : QB * LD;
+  __shared__ __attribute__((aligned(16))) T lds[LDS_N];
+
+  int bx, bh;
+  xcd_block(bx, bh);
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int Tn = (int)a.T, D = (int)a.D;
+  const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / MT, c = lane % MT;
+  const int wq0 = q0 + wave * MT;
+  const int qr = wq0 + c;
+  const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+  const T* DS = (const T*)a.ds + (int64_t)bh * Tn * Tn;
+  const bool vec = a.vec != 0;
+  const bool ds_vec = F32 && (Tn % 4) == 0;
+
+  typename M::acc_t dq[DP / MT];
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt) dq[dt] = typename M::acc_t(0);
+
+  const int qlast = (q0 + QB < Tn ? q0 + QB : Tn) - 1;
+  const int nkt = q0 < Tn ? qlast / KT + 1 : 0;
+  auto live = [&](int kt) { return kt * KT <= wq0 + MT - 1 && wq0 < Tn; };
+  // lane (c, g), register i: dS[qr][kt * KT + row(i, g)]
+  auto load_ds = [&](int kt, typename M::acc_t& r) {
+    const int j0 = kt * KT;
+    if constexpr (F32) {
+      if (ds_vec && qr < Tn && j0 + KT <= Tn) {
+#pragma unroll
+        for (int a4 = 0; a4 < NACC / 4; ++a4) {
+          const typename M::vec_t v =
+              *reinterpret_cast<const typename M::vec_t*>(DS + (int64_t)qr * Tn + j0 + 8 * a4 + 4 * g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r[4 * a4 + e] = v[e];
+        }
+        return;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) {
+      const int j = j0 + M::row(i, g);
+      r[i] = (qr < Tn && j < Tn) ? DS[(int64_t)qr * Tn + j] : T(0);
+    }
+  };
+  TileFetch<T, KT, DP> fk;
+  auto store_k = [&](int stage) {
+    if constexpr (F32)
+      fk.store_t(lds + stage * TILE);
+    else
+      fk.store(lds + stage * TILE);
+  };
+  typename M::acc_t dsr = typename M::acc_t(0), dsn = typename M::acc_t(0);
+  if (nkt > 0) {
+    fk.fetch(K, a.sk.t, 0, Tn, D, vec);
+    store_k(0);
+    if (live(0)) load_ds(0, dsr);
+  }
+  __syncthreads();
+  for (int kt = 0; kt < nkt; ++kt) {
+    const int cur = kt & 1;
+    const bool more = kt + 1 < nkt;
+    if (more) {
+      fk.fetch(K, a.sk.t, (kt + 1) * KT, Tn, D, vec);
+      if (live(kt + 1)) load_ds(kt + 1, dsn);
+    }
+    if (live(kt)) {
+      if constexpr (F32)
+        mma_ldsT_regs<DP, LDT>(dq, lds + cur * TILE, 0, dsr, g, c);
+      else
+        mma_lds_t_regs<T, DP>(dq, lds + cur * TILE, 0, dsr, g, c);
+    }
+    if (more) store_k(cur ^ 1);
+    dsr = dsn;
+    __syncthreads();
+  }
+  T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h;
+  store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c);
+}
+
 template <typename T, int DP>
 __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   using M = AM<T>;
@@ -595,6 +751,8 @@ static int attn_fwd_impl(AttnArgs& a) {
   return DTMI_OK;
 }
 
+constexpr double kMaxDsBytes = 4.0 * (1 << 30);
+
 template <typename T>
 static int attn_bwd_impl(AttnArgs& a) {
   constexpr int MT = AM<T>::MT;
@@ -605,16 +763,31 @@ static int attn_bwd_impl(AttnArgs& a) {
   int rc = pool_alloc(&drow, (size_t)rows * sizeof(T));
   if (rc) return rc;
   a.drow = drow;
+  // dS for the dQ pass: B*H*T*T elements, up to kMaxDsBytes; beyond that the
+  // dQ pass recomputes S, P and dP itself.
+  a.ds = nullptr;
+  const double ds_bytes = (double)a.B * a.H * a.T * a.T * sizeof(T);
+  if (ds_bytes <= kMaxDsBytes) {
+    rc = pool_alloc(&a.ds, (size_t)ds_bytes);
+    if (rc) {
+      pool_free(drow);
+      return rc;
+    }
+  }
   {
     // causal-exact FLOP of the 5 backward GEMMs (S recompute, dV, dP, dQ, dK)
     TimedLaunch tl(DTMI_FAM_ATTN_BWD, 5.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
     attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
     dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
     DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
-    DP_SWITCH(dp, attn_bwd_q_kernel, T, grid)
+    if (a.ds)
+      DP_SWITCH(dp, attn_bwd_q_ds_kernel, T, grid)
+    else
+      DP_SWITCH(dp, attn_bwd_q_kernel, T, grid)
   }
   hipError_t le = hipGetLastError();
   pool_free(drow);
+  if (a.ds) pool_free(a.ds);
   if (le != hipSuccess) return fail_hip(le, "attention backward kernels", __FILE__, __LINE__);
   return DTMI_OK;
 }

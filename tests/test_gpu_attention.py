@@ -91,3 +91,26 @@ def test_attention_on_fused_qkv_layout(dev, dt):
     assert rel_err(got[:, :, 0].transpose(0, 2, 1, 3), gq) <= TOL[dt]
     assert rel_err(got[:, :, 1].transpose(0, 2, 1, 3), gk) <= TOL[dt]
     assert rel_err(got[:, :, 2].transpose(0, 2, 1, 3), gv) <= TOL[dt]
+
+
+def test_backward_without_the_ds_workspace_matches_with_it():
+    """B*H*T*T float32 above 4 GiB: the dQ pass recomputes dS instead of
+    reading it from a workspace. Splitting the heads in two keeps each half
+    under the limit (dS path); the two paths must agree."""
+    D, K = _dev()
+    B, H, T, Dh = 1, 32, 6144, 64
+    rng = np.random.default_rng(21)
+    hq, hk, hv, hg = (rng.standard_normal((B, H, T, Dh)).astype(np.float32) for _ in range(4))
+    q, k, v, g = (D.from_numpy(x) for x in (hq, hk, hv, hg))
+    o, rmax, rsum = K.attn_fwd(q, k, v)
+    dq, dk, dv = K.attn_bwd(q, k, v, o, g, rmax, rsum)  # 4.8 GB of dS: recompute path
+    ho, hm, hs = o.numpy(), rmax.numpy(), rsum.numpy()
+    halves = []
+    for lo in (0, H // 2):
+        sl = slice(lo, lo + H // 2)
+        sub = [D.from_numpy(np.ascontiguousarray(x[:, sl])) for x in (hq, hk, hv, ho, hg)]
+        stats = [D.from_numpy(np.ascontiguousarray(x[:, sl])) for x in (hm, hs)]
+        halves.append([t.numpy() for t in K.attn_bwd(*sub, *stats)])  # 2.4 GB each: dS path
+    for i, full in enumerate((dq, dk, dv)):
+        ref = np.concatenate([halves[0][i], halves[1][i]], axis=1)
+        assert rel_err(full.numpy(), ref) <= 1e-6
