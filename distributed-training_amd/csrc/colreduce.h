@@ -11,9 +11,16 @@
 
 namespace dtmi {
 
+// blockIdx.y selects one of two (out, parts) pairs, so two reductions of the
+// same shape (LayerNorm's dgamma and dbeta) share one launch.
 template <typename T>
 __global__ void __launch_bounds__(256) colreduce_kernel(T* __restrict__ out, const T* __restrict__ parts, int nparts,
-                                                         int64_t cols, int accumulate) {
+                                                         int64_t cols, int accumulate, T* __restrict__ out1,
+                                                         const T* __restrict__ parts1) {
+  if (blockIdx.y == 1) {
+    out = out1;
+    parts = parts1;
+  }
   __shared__ T sh[8][32];
   const int cl = threadIdx.x & 31, grp = threadIdx.x >> 5;
   const int64_t c = (int64_t)blockIdx.x * 32 + cl;
@@ -40,8 +47,10 @@ __global__ void __launch_bounds__(256) colreduce_kernel(T* __restrict__ out, con
 }
 
 template <typename T>
-inline void launch_colreduce(T* out, const T* parts, int nparts, int64_t cols, int accumulate) {
-  colreduce_kernel<T><<<(unsigned)cdiv(cols, 32), 256, 0, stream()>>>(out, parts, nparts, cols, accumulate);
+inline void launch_colreduce(T* out, const T* parts, int nparts, int64_t cols, int accumulate, T* out1 = nullptr,
+                             const T* parts1 = nullptr) {
+  dim3 grid((unsigned)cdiv(cols, 32), out1 ? 2u : 1u);
+  colreduce_kernel<T><<<grid, 256, 0, stream()>>>(out, parts, nparts, cols, accumulate, out1, parts1);
 }
 
 }  // namespace dtmi

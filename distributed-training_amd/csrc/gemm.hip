@@ -81,6 +81,13 @@ struct GemmArgs {
   const void* addend;  // residual: v = addend[m, n] + v   (row stride ldc)
   int epi;             // kEpiGeluFwd: aux = gelu(v), C keeps v; kEpiGeluBwd: C = gelu'(aux) * v
   void* aux;           // [M, N] with row stride ldc
+  // Column sums of B over k (the bias gradient of dW = X^T dY: db = sum over
+  // rows of dY), taken by the blocks of the first row of tiles from the B
+  // tiles already in LDS. Unbatched only. With split-K each split's sums go to
+  // colsum_ws[split][n] and the reduction kernel adds them in split order.
+  void* colsum;
+  void* colsum_ws;
+  int colsum_accumulate;
 };
 
 constexpr int kEpiNone = 0, kEpiGeluFwd = 1, kEpiGeluBwd = 2;
@@ -376,6 +383,8 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs a) {
     store(0, 0, ra, rb);
   }
   __syncthreads();
+  const bool take_colsum = a.colsum != nullptr && tm == 0 && (int)threadIdx.x < BN;
+  double csum = 0.0;
   for (int64_t kt = 0; kt < ntiles; ++kt) {
     const int cur = kt & 1;
     if (kt + 1 < ntiles) load(kt + 1, ra, rb);
@@ -395,8 +404,27 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs a) {
 #pragma unroll
           for (int j = 0; j < TN; ++j) acc[i][j] = MFT::mma(fa[i][s], fb[j][s], acc[i][j]);
     }
+    if (take_colsum) {
+      // this thread's column of the B tile: its kBK values in k order, then into
+      // the running float64 sum (rows past kend were stored as zeros)
+      T t = T(0);
+#pragma unroll
+      for (int k = 0; k < kBK; ++k) t = t + (BKC ? Bs[threadIdx.x * LB::STRIDE + k] : Bs[k * LB::STRIDE + threadIdx.x]);
+      csum += (double)t;
+    }
     if (kt + 1 < ntiles) store(kt + 1, cur ^ 1, ra, rb);
     __syncthreads();
+  }
+  if (take_colsum) {
+    const int64_t n = n0 + threadIdx.x;
+    if (n < a.N) {
+      if (a.colsum_ws) {
+        ((T*)a.colsum_ws)[(int64_t)split * a.N + n] = (T)csum;
+      } else {
+        T* cs = (T*)a.colsum;
+        cs[n] = a.colsum_accumulate ? cs[n] + (T)csum : (T)csum;
+      }
+    }
   }
 
   // epilogue: split-K partials go to the workspace as they are; otherwise
@@ -450,6 +478,15 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
   const int64_t nvec = total / VEC;  // VEC divides N
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const T* __restrict__ bias = (const T*)a.bias;
+  if (a.colsum_ws) {  // column sums of the splits, in split order
+    T* cs = (T*)a.colsum;
+    const T* w = (const T*)a.colsum_ws;
+    for (int64_t n = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; n < N; n += stride) {
+      T v = w[n];
+      for (int s = 1; s < splits; ++s) v = v + w[(int64_t)s * N + n];
+      cs[n] = a.colsum_accumulate ? cs[n] + v : v;
+    }
+  }
   for (int64_t iv = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; iv < nvec; iv += stride) {
     const int64_t idx = iv * VEC;
     const int64_t b = idx / (M * N);
@@ -510,6 +547,8 @@ struct EpiArgs {
   const void* addend = nullptr;
   int epi = kEpiNone;
   void* aux = nullptr;
+  void* colsum = nullptr;  // column sums of B (length N), unbatched
+  int colsum_accumulate = 0;
 };
 
 template <typename T>
@@ -535,6 +574,8 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   a.addend = ep.addend;
   a.epi = ep.epi;
   a.aux = ep.aux;
+  a.colsum = ep.colsum;
+  a.colsum_accumulate = ep.colsum_accumulate;
   // K splits. A grid of b blocks on C CUs runs ceil(b / C) rounds, so its
   // useful fraction is b / (C * ceil(b / C)); take the fewest splits (each
   // keeping >= 256 of K) that reach 90 % of rounds, else the best found.
@@ -571,9 +612,12 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   bool vecb = aligned(B, 16) && ldb % VEC == 0 && (batch == 1 || sB % VEC == 0) && (bkc ? K % VEC == 0 : N % VEC == 0);
   void* ws = nullptr;
   if (splits > 1) {
-    int rc = pool_alloc(&ws, (size_t)splits * batch * M * N * es);
+    const size_t main_bytes = (size_t)splits * batch * M * N * es;
+    const size_t cs_bytes = a.colsum ? (size_t)splits * N * es : 0;
+    int rc = pool_alloc(&ws, main_bytes + cs_bytes);
     if (rc) return rc;
     a.ws = ws;
+    if (a.colsum) a.colsum_ws = (char*)ws + main_bytes;
   }
   dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
   {
@@ -615,6 +659,7 @@ static int gemm_dispatch(int dtype, int akc, int bkc, int64_t M, int64_t N, int6
   DTMI_CHECK(K == 0 || (akc ? lda >= K : lda >= M), "dtmi_gemm: lda too small");
   DTMI_CHECK(K == 0 || (bkc ? ldb >= K : ldb >= N), "dtmi_gemm: ldb too small");
   DTMI_CHECK(ep.epi == kEpiNone || ep.aux != nullptr, "dtmi_gemm: GELU epilogue without its array");
+  DTMI_CHECK(ep.colsum == nullptr || batch == 1, "dtmi_gemm: column sums are for unbatched products");
   if (dtype == DTMI_F32)
     return gemm_impl<float>(akc, bkc, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, batch, bias, accumulate,
                             force_splits, ep);
@@ -683,10 +728,12 @@ DTMI_EXPORT int dtmi_linear_bwd_dw(int dtype, void* dW, void* db, const void* X,
                                    int64_t K, int64_t N, int accumulate) {
   DTMI_BODY_BEGIN
   DTMI_REQUIRE_INIT();
-  // dW[k, n] = sum_m X[m, k] dY[m, n]: A(k, m) = X[m, k] (k-major storage), B(m, n) = dY[m, n]
-  int rc = gemm_dispatch(dtype, 0, 0, K, N, M, X, K, 0, dY, N, 0, dW, N, 0, 1, nullptr, accumulate, 0);
-  if (rc) return rc;
-  if (db) return dtmi_colsum(dtype, db, dY, M, N, accumulate);
-  return DTMI_OK;
+  // dW[k, n] = sum_m X[m, k] dY[m, n]: A(k, m) = X[m, k] (k-major storage), B(m, n) = dY[m, n];
+  // db[n] = sum_m dY[m, n], the column sums of B, taken inside the same GEMM
+  if (K == 0) return db ? dtmi_colsum(dtype, db, dY, M, N, accumulate) : DTMI_OK;  // no dW tiles to carry db
+  EpiArgs ep;
+  ep.colsum = db;
+  ep.colsum_accumulate = accumulate;
+  return gemm_dispatch(dtype, 0, 0, K, N, M, X, K, 0, dY, N, 0, dW, N, 0, 1, nullptr, accumulate, 0, ep);
   DTMI_BODY_END
 }

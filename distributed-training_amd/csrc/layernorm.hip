@@ -308,8 +308,7 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
       LN_NV_SWITCH(nv, CALLS)
 #undef CALLS
     }
-    launch_colreduce<T>((T*)dw, pdw, grid, cols, (accumulate & 2) ? 1 : 0);
-    launch_colreduce<T>((T*)db, pdb, grid, cols, (accumulate & 2) ? 1 : 0);
+    launch_colreduce<T>((T*)dw, pdw, grid, cols, (accumulate & 2) ? 1 : 0, (T*)db, pdb);
   }
   hipError_t le = hipGetLastError();
   pool_free(parts);
