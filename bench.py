@@ -129,7 +129,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seq", type=int, default=2, help="sequences in the CPU baseline sample")
+    ap.add_argument("--cpu-seq", type=int, default=3, help="sequences in the CPU baseline sample")
     ap.add_argument("--seed", type=int, default=5)
     ap.add_argument("--workload", default="gpt2",
                     choices=["gpt2", "ln_linear", "attention", "bucket_adamw", "chargpt", "copy"],
