@@ -498,7 +498,22 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
       vt v = *reinterpret_cast<const vt*>(ws + idx);
       for (int s = 1; s < splits; ++s) v = v + *reinterpret_cast<const vt*>(ws + (int64_t)s * total + idx);
       if (bias) v = v + *reinterpret_cast<const vt*>(bias + n);
-      *reinterpret_cast<vt*>(C + m * a.ldc + n) = v;
+      const int64_t o = m * a.ldc + n;
+      if (!PLAIN) {  // the epilogue_store sequence, VEC elements at a time
+        if (a.addend) v = *reinterpret_cast<const vt*>((const T*)a.addend + b * a.sC + o) + v;
+        if (a.accumulate) v = *reinterpret_cast<const vt*>(C + o) + v;
+        if (a.epi == kEpiGeluFwd) {
+          vt y;
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) y[e] = gelu_f<T>(v[e]);
+          *reinterpret_cast<vt*>((T*)a.aux + b * a.sC + o) = y;
+        } else if (a.epi == kEpiGeluBwd) {
+          const vt x = *reinterpret_cast<const vt*>((const T*)a.aux + b * a.sC + o);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) v[e] = gelu_b<T>(x[e], v[e]);
+        }
+      }
+      *reinterpret_cast<vt*>(C + o) = v;
       continue;
     }
     T v[VEC];
@@ -631,9 +646,12 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
       const bool plain = a.addend == nullptr && a.epi == kEpiNone && !a.accumulate;
       constexpr int V = 16 / sizeof(T);
       const bool vec_ok = N % V == 0 && ldc % V == 0 && (batch == 1 || sC % V == 0) && aligned(C, 16) &&
-                          (!bias || aligned(bias, 16));
+                          (!bias || aligned(bias, 16)) && (!a.addend || aligned(a.addend, 16)) &&
+                          (!a.aux || aligned(a.aux, 16));
       if (plain && vec_ok)
         splitk_reduce_kernel<T, true, V><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
+      else if (vec_ok)
+        splitk_reduce_kernel<T, false, V><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
       else if (plain)
         splitk_reduce_kernel<T, true, 1><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
       else
