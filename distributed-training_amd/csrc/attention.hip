@@ -331,44 +331,48 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
       fk.fetch(K, a.sk.t, k0 + KB, Tn, D, vec);
       fv.fetch(V, a.sv.t, k0 + KB, Tn, D, vec);
     }
-    typename M::acc_t sacc[KB / MT];
+    // a wave whose queries all precede the tile's keys has nothing to add (all
+    // its probabilities would be 0 and its max/sum unchanged): skip the work
+    if (k0 <= wq0 + MT - 1) {
+      typename M::acc_t sacc[KB / MT];
 #pragma unroll
-    for (int jt = 0; jt < KB / MT; ++jt) sacc[jt] = mma_rows_frag<T, DP>(typename M::acc_t(0), Ks, jt * MT, qf, g, c);
-    // causal mask only where a key of the tile can exceed a query of the wave
-    const bool mask = (k0 + KB - 1 > wq0) || (k0 + KB > Tn);
-    T bmax = ninf;
+      for (int jt = 0; jt < KB / MT; ++jt) sacc[jt] = mma_rows_frag<T, DP>(typename M::acc_t(0), Ks, jt * MT, qf, g, c);
+      // causal mask only where a key of the tile can exceed a query of the wave
+      const bool mask = (k0 + KB - 1 > wq0) || (k0 + KB > Tn);
+      T bmax = ninf;
 #pragma unroll
-    for (int jt = 0; jt < KB / MT; ++jt)
+      for (int jt = 0; jt < KB / MT; ++jt)
 #pragma unroll
-      for (int i = 0; i < NACC; ++i) {
-        T s = sacc[jt][i] * sl2;
-        if (mask) {
-          const int j = k0 + jt * MT + M::row(i, g);
-          s = (j <= qr && j < Tn) ? s : ninf;
+        for (int i = 0; i < NACC; ++i) {
+          T s = sacc[jt][i] * sl2;
+          if (mask) {
+            const int j = k0 + jt * MT + M::row(i, g);
+            s = (j <= qr && j < Tn) ? s : ninf;
+          }
+          sacc[jt][i] = s;
+          bmax = fmax(bmax, s);
         }
-        sacc[jt][i] = s;
-        bmax = fmax(bmax, s);
-      }
-    bmax = group_max(bmax);
-    const T mnew = fmax(mrow, bmax);
-    const bool live = mnew != ninf;
-    const T alpha = live ? ex2(mrow - mnew) : T(1);
-    T psum = T(0);
+      bmax = group_max(bmax);
+      const T mnew = fmax(mrow, bmax);
+      const bool live = mnew != ninf;
+      const T alpha = live ? ex2(mrow - mnew) : T(1);
+      T psum = T(0);
 #pragma unroll
-    for (int jt = 0; jt < KB / MT; ++jt)
+      for (int jt = 0; jt < KB / MT; ++jt)
 #pragma unroll
-      for (int i = 0; i < NACC; ++i) {
-        const T p = live ? ex2(sacc[jt][i] - mnew) : T(0);
-        sacc[jt][i] = p;
-        psum += p;
-      }
-    psum = group_sum(psum);
-    lrow = lrow * alpha + psum;
-    mrow = mnew;
+        for (int i = 0; i < NACC; ++i) {
+          const T p = live ? ex2(sacc[jt][i] - mnew) : T(0);
+          sacc[jt][i] = p;
+          psum += p;
+        }
+      psum = group_sum(psum);
+      lrow = lrow * alpha + psum;
+      mrow = mnew;
 #pragma unroll
-    for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
+      for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
 #pragma unroll
-    for (int jt = 0; jt < KB / MT; ++jt) mma_lds_t_regs<T, DP>(oacc, Vs, jt * MT, sacc[jt], g, c);
+      for (int jt = 0; jt < KB / MT; ++jt) mma_lds_t_regs<T, DP>(oacc, Vs, jt * MT, sacc[jt], g, c);
+    }
     if (more) {
       T* nxt = lds + ((kb + 1) & 1) * STAGE;
       fk.store(nxt);
@@ -490,45 +494,49 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
       fg.fetch(G, a.sdo.t, qs + QT, Tn, D, vec);
       fetch_stats(qs + QT);
     }
-    // S(r, j) and dP(r, j): rows r = the tile's queries (LDS), columns j = this wave's keys
-    typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Qs, 0, kf, g, c);
-    typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Gs, 0, vf, g, c);
-    const bool mask = (qs < wk0 + MT - 1) || (qs + QT > Tn) || (wk0 + MT > Tn);
-    auto prob = [&](int i, T m, T linv, T dr) {
-      T p = ex2(s[i] * sl2 - m) * linv;
-      if (mask) {
-        const int r = qs + M::row(i, g);
-        p = (kj <= r && r < Tn && kj < Tn) ? p : T(0);
-      }
-      s[i] = p;
-      dp[i] = p * (dp[i] - dr);
-      if (DS) {
-        const int r = qs + M::row(i, g);
-        if (r < Tn && kj < Tn) DS[(int64_t)r * Tn + kj] = dp[i];
-      }
-    };
-    if constexpr (F32) {
-      // rows 8a + 4g + 0..3 of MFMA steps 4a .. 4a+3: one 16-byte read per statistic
+    // a tile whose queries all precede this wave's keys contributes nothing
+    // (and its dS is never read): skip it
+    if (qs + QT - 1 >= wk0) {
+      // S(r, j) and dP(r, j): rows r = the tile's queries (LDS), columns j = this wave's keys
+      typename M::acc_t s = mma_rows_frag<T, DP>(typename M::acc_t(0), Qs, 0, kf, g, c);
+      typename M::acc_t dp = mma_rows_frag<T, DP>(typename M::acc_t(0), Gs, 0, vf, g, c);
+      const bool mask = (qs < wk0 + MT - 1) || (qs + QT > Tn) || (wk0 + MT > Tn);
+      auto prob = [&](int i, T m, T linv, T dr) {
+        T p = ex2(s[i] * sl2 - m) * linv;
+        if (mask) {
+          const int r = qs + M::row(i, g);
+          p = (kj <= r && r < Tn && kj < Tn) ? p : T(0);
+        }
+        s[i] = p;
+        dp[i] = p * (dp[i] - dr);
+        if (DS) {
+          const int r = qs + M::row(i, g);
+          if (r < Tn && kj < Tn) DS[(int64_t)r * Tn + kj] = dp[i];
+        }
+      };
+      if constexpr (F32) {
+        // rows 8a + 4g + 0..3 of MFMA steps 4a .. 4a+3: one 16-byte read per statistic
 #pragma unroll
-      for (int a4 = 0; a4 < NACC / 4; ++a4) {
-        const int r0 = 8 * a4 + 4 * g;
-        const typename M::vec_t m4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][0][r0]);
-        const typename M::vec_t l4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][1][r0]);
-        const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
+        for (int a4 = 0; a4 < NACC / 4; ++a4) {
+          const int r0 = 8 * a4 + 4 * g;
+          const typename M::vec_t m4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][0][r0]);
+          const typename M::vec_t l4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][1][r0]);
+          const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) prob(4 * a4 + e, m4[e], l4[e], d4[e]);
-      }
-      // dV^T += dO^T P ; dK^T += Q^T dS (transposed tiles: vector reads)
-      mma_ldsT_regs<DP, LDT>(dv, Qs + 2 * TILE + TILE_T, 0, s, g, c);
-      mma_ldsT_regs<DP, LDT>(dk, Qs + 2 * TILE, 0, dp, g, c);
-    } else {
+          for (int e = 0; e < 4; ++e) prob(4 * a4 + e, m4[e], l4[e], d4[e]);
+        }
+        // dV^T += dO^T P ; dK^T += Q^T dS (transposed tiles: vector reads)
+        mma_ldsT_regs<DP, LDT>(dv, Qs + 2 * TILE + TILE_T, 0, s, g, c);
+        mma_ldsT_regs<DP, LDT>(dk, Qs + 2 * TILE, 0, dp, g, c);
+      } else {
 #pragma unroll
-      for (int i = 0; i < NACC; ++i) {
-        const int rl = M::row(i, g);
-        prob(i, stats[cur][0][rl], stats[cur][1][rl], stats[cur][2][rl]);
+        for (int i = 0; i < NACC; ++i) {
+          const int rl = M::row(i, g);
+          prob(i, stats[cur][0][rl], stats[cur][1][rl], stats[cur][2][rl]);
+        }
+        mma_lds_t_regs<T, DP>(dv, Gs, 0, s, g, c);
+        mma_lds_t_regs<T, DP>(dk, Qs, 0, dp, g, c);
       }
-      mma_lds_t_regs<T, DP>(dv, Gs, 0, s, g, c);
-      mma_lds_t_regs<T, DP>(dk, Qs, 0, dp, g, c);
     }
     if (more) store_stage(cur ^ 1);
     __syncthreads();
