@@ -109,6 +109,12 @@ __device__ __forceinline__ void load_rows(T* __restrict__ lds, const T* __restri
   }
 }
 
+// s_waitcnt vmcnt(0): drain this wave's outstanding global loads. Placed
+// before a loop whose body first reads registers loaded ahead of it, so that
+// the wait is paid once there and not, at the loop's first use of them, on
+// every iteration (the wait analysis merges the loop entry into the loop head).
+__device__ __forceinline__ void drain_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 // A lane's VEC-vectors of one row (its column c of the wave tile), d-chunked:
 // element s of vector ch is d = 8*ch + VEC*g + s.
 template <typename T, int DP>
@@ -172,25 +178,71 @@ __device__ __forceinline__ double ex2(double x) { return exp2(x); }
 // Registers for one NR x DP tile in flight from global memory (16-byte
 // vectors, 256 threads), stored to LDS [NR][DP + PAD] after the current tile's
 // MFMAs. Rows >= Tn and columns >= D are zero.
-template <typename T, int NR, int DP>
+//
+// FAST (16-byte access allowed, D == DP and T a multiple of 64, so every tile
+// lies inside [0, T)): every thread issues the same loads from persistent
+// pointers with no branch. Otherwise each element is bounds-checked.
+template <typename T, int NR, int DP, bool FAST>
 struct TileFetch {
   typedef typename AM<T>::vec_t V;
   static constexpr int VEC = AM<T>::VEC, LD = DP + AM<T>::PAD;
   static constexpr int TOTAL = NR * DP / VEC;
   static constexpr int NV = (TOTAL + 255) / 256;
   V r[NV];
+  // FAST: per-thread source pointers, advanced one tile per next(); kept in
+  // registers for the whole loop, so no load address is a temporary that the
+  // compiler could hand to an MFMA result while the load is in flight (which
+  // makes it wait for every outstanding load first)
+  const T* p[NV];
+  int64_t step = 0;
+  const T* base_ = nullptr;
+  int64_t rs_ = 0;
+  int r0_ = 0, tn_ = 0, d_ = 0;
+  bool vec_ = false;
 
+  // tiles are then fetched at rows r0, r0 + NR, r0 + 2 NR, ...
+  __device__ __forceinline__ void start(const T* __restrict__ base, int64_t rs, int r0, int Tn, int D, bool vec) {
+    base_ = base;
+    rs_ = rs;
+    r0_ = r0;
+    tn_ = Tn;
+    d_ = D;
+    vec_ = vec;
+    if (FAST) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        int f = threadIdx.x + 256 * i;
+        if (TOTAL % 256 != 0) f = f < TOTAL ? f : TOTAL - 1;
+        const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
+        p[i] = base + (int64_t)(r0 + rr) * rs + d;
+      }
+      step = (int64_t)NR * rs;
+    }
+  }
+
+  // Load the next tile (FAST: every row is inside [0, Tn), the caller's contract).
+  __device__ __forceinline__ void next() {
+    if (FAST) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        r[i] = *reinterpret_cast<const V*>(p[i]);
+        p[i] += step;
+      }
+    } else {
+      fetch(base_, rs_, r0_, tn_, d_, vec_);
+    }
+    r0_ += NR;
+  }
+
+  // bounds-checked load of the tile at rows [r0, r0 + NR)
   __device__ __forceinline__ void fetch(const T* __restrict__ base, int64_t rs, int r0, int Tn, int D, bool vec) {
-    const bool full = vec && (r0 + NR <= Tn) && (D == DP);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int f = threadIdx.x + 256 * i;
       if (TOTAL % 256 != 0 && f >= TOTAL) continue;
       const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
       const T* src = base + (int64_t)(r0 + rr) * rs + d;
-      if (full) {
-        r[i] = *reinterpret_cast<const V*>(src);
-      } else if (vec) {
+      if (vec) {
         r[i] = (r0 + rr < Tn && d < D) ? *reinterpret_cast<const V*>(src) : V(0);
       } else {
         V x = V(0);
@@ -202,13 +254,15 @@ struct TileFetch {
     }
   }
 
+  __device__ __forceinline__ V value(int i, int) const { return r[i]; }
+
   __device__ __forceinline__ void store(T* __restrict__ lds) const {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int f = threadIdx.x + 256 * i;
       if (TOTAL % 256 != 0 && f >= TOTAL) continue;
       const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
-      *reinterpret_cast<V*>(lds + rr * LD + d) = r[i];
+      *reinterpret_cast<V*>(lds + rr * LD + d) = value(i, rr);
     }
   }
 
@@ -221,8 +275,9 @@ struct TileFetch {
       const int f = threadIdx.x + 256 * i;
       if (TOTAL % 256 != 0 && f >= TOTAL) continue;
       const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
+      const V x = value(i, rr);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ldsT[(d + e) * LDT + rr] = r[i][e];
+      for (int e = 0; e < VEC; ++e) ldsT[(d + e) * LDT + rr] = x[e];
     }
   }
 };
@@ -281,7 +336,7 @@ __device__ __forceinline__ void xcd_block(int& bx, int& by) {
   by = L / gx;
 }
 
-template <typename T, int DP>
+template <typename T, int DP, bool FAST>
 __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
@@ -316,9 +371,11 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
 
   const int qlast = (q0 + QB < Tn ? q0 + QB : Tn) - 1;
   const int nkb = qlast / KB + 1;
-  TileFetch<T, KB, DP> fk, fv;
-  fk.fetch(K, a.sk.t, 0, Tn, D, vec);
-  fv.fetch(V, a.sv.t, 0, Tn, D, vec);
+  TileFetch<T, KB, DP, FAST> fk, fv;
+  fk.start(K, a.sk.t, 0, Tn, D, vec);
+  fv.start(V, a.sv.t, 0, Tn, D, vec);
+  fk.next();
+  fv.next();
   fk.store(lds);
   fv.store(lds + TILE);
   __syncthreads();
@@ -328,8 +385,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
     const T* Vs = Ks + TILE;
     const bool more = kb + 1 < nkb;
     if (more) {
-      fk.fetch(K, a.sk.t, k0 + KB, Tn, D, vec);
-      fv.fetch(V, a.sv.t, k0 + KB, Tn, D, vec);
+      fk.next();
+      fv.next();
     }
     // a wave whose queries all precede the tile's keys has nothing to add (all
     // its probabilities would be 0 and its max/sum unchanged): skip the work
@@ -408,7 +465,7 @@ __global__ void __launch_bounds__(256) attn_drow_kernel(AttnArgs a) {
 // ------------------------------------------------- backward A: dK and dV
 // One block owns 4*MT keys (MT per wave, as the columns of its tiles) and walks
 // the query tiles of MT rows that can see them, double-buffered.
-template <typename T, int DP>
+template <typename T, int DP, bool FAST>
 __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
@@ -451,14 +508,25 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
 
   const int qs0 = (k0 / QT) * QT;
   const int nqt = k0 < Tn ? (Tn - qs0 + QT - 1) / QT : 0;
-  TileFetch<T, QT, DP> fq, fg;
+  TileFetch<T, QT, DP, FAST> fq, fg;
   T st0 = T(0), st1 = T(1), st2 = T(0);
+  // FAST: every thread loads (lanes past QT re-read a valid row; only the
+  // first QT threads store), from pointers advanced one tile per call
+  const int srow = qs0 + (int)(threadIdx.x % QT);
+  const T *rm_p = RM + srow, *rs_p = RS + srow, *dr_p = DR + srow;
   auto fetch_stats = [&](int qs) {
-    if (threadIdx.x < QT) {
+    if (FAST) {
+      st0 = *rm_p;
+      st1 = *rs_p;
+      st2 = *dr_p;
+      rm_p += QT;
+      rs_p += QT;
+      dr_p += QT;
+    } else if (threadIdx.x < QT) {
       const int r = qs + threadIdx.x;
       const bool ok = r < Tn;
       st0 = ok ? RM[r] : T(0);
-      st1 = ok ? T(1) / RS[r] : T(1);
+      st1 = ok ? RS[r] : T(1);
       st2 = ok ? DR[r] : T(0);
     }
   };
@@ -470,18 +538,21 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
       fq.store_t(base + 2 * TILE);
       fg.store_t(base + 2 * TILE + TILE_T);
     }
-    if (threadIdx.x < QT) {
+    if (threadIdx.x < QT) {  // the loads were issued a tile earlier; 1 / sum only now, after the MFMAs
       stats[stage][0][threadIdx.x] = st0;
-      stats[stage][1][threadIdx.x] = st1;
+      stats[stage][1][threadIdx.x] = T(1) / st1;
       stats[stage][2][threadIdx.x] = st2;
     }
   };
   if (nqt > 0) {
-    fq.fetch(Q, a.sq.t, qs0, Tn, D, vec);
-    fg.fetch(G, a.sdo.t, qs0, Tn, D, vec);
+    fq.start(Q, a.sq.t, qs0, Tn, D, vec);
+    fg.start(G, a.sdo.t, qs0, Tn, D, vec);
+    fq.next();
+    fg.next();
     fetch_stats(qs0);
     store_stage(0);
   }
+  drain_vm();
   __syncthreads();
   for (int it = 0; it < nqt; ++it) {
     const int qs = qs0 + it * QT;
@@ -490,8 +561,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
     const T* Gs = Qs + TILE;
     const bool more = it + 1 < nqt;
     if (more) {
-      fq.fetch(Q, a.sq.t, qs + QT, Tn, D, vec);
-      fg.fetch(G, a.sdo.t, qs + QT, Tn, D, vec);
+      fq.next();
+      fg.next();
       fetch_stats(qs + QT);
     }
     // a tile whose queries all precede this wave's keys contributes nothing
@@ -554,7 +625,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
 // operand (lane column = query, k-slot = key), so S, P and dP are not
 // recomputed. Key tiles wholly above a wave's queries are skipped by that
 // wave (their dS is zero).
-template <typename T, int DP>
+template <typename T, int DP, bool FAST>
 __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
@@ -578,7 +649,6 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
   const T* DS = (const T*)a.ds + (int64_t)bh * Tn * Tn;
   const bool vec = a.vec != 0;
-  const bool ds_vec = F32 && (Tn % 4) == 0;
 
   typename M::acc_t dq[DP / MT];
 #pragma unroll
@@ -590,25 +660,37 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   // lane (c, g), register i: dS[qr][kt * KT + row(i, g)]
   auto load_ds = [&](int kt, typename M::acc_t& r) {
     const int j0 = kt * KT;
-    if constexpr (F32) {
-      if (ds_vec && qr < Tn && j0 + KT <= Tn) {
+    if constexpr (F32 && FAST) {
+      // branch-free 16-byte loads (T is a multiple of 4, so a group of four
+      // columns is wholly in or out); addresses past the end are clamped and
+      // those entries zeroed by valid_ds before use
+      const int row = qr < Tn ? qr : Tn - 1;
 #pragma unroll
-        for (int a4 = 0; a4 < NACC / 4; ++a4) {
-          const typename M::vec_t v =
-              *reinterpret_cast<const typename M::vec_t*>(DS + (int64_t)qr * Tn + j0 + 8 * a4 + 4 * g);
+      for (int a4 = 0; a4 < NACC / 4; ++a4) {
+        int j = j0 + 8 * a4 + 4 * g;
+        j = j + 4 <= Tn ? j : Tn - 4;
+        const typename M::vec_t v = *reinterpret_cast<const typename M::vec_t*>(DS + (int64_t)row * Tn + j);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) r[4 * a4 + e] = v[e];
-        }
-        return;
+        for (int e = 0; e < 4; ++e) r[4 * a4 + e] = v[e];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NACC; ++i) {
+        const int j = j0 + M::row(i, g);
+        r[i] = (qr < Tn && j < Tn) ? DS[(int64_t)qr * Tn + j] : T(0);
       }
     }
+  };
+  auto valid_ds = [&](int kt, typename M::acc_t& r) {
+    if constexpr (F32 && FAST) {
 #pragma unroll
-    for (int i = 0; i < NACC; ++i) {
-      const int j = j0 + M::row(i, g);
-      r[i] = (qr < Tn && j < Tn) ? DS[(int64_t)qr * Tn + j] : T(0);
+      for (int i = 0; i < NACC; ++i) {
+        const int j = kt * KT + M::row(i, g);
+        r[i] = (qr < Tn && j < Tn) ? r[i] : T(0);
+      }
     }
   };
-  TileFetch<T, KT, DP> fk;
+  TileFetch<T, KT, DP, FAST> fk;
   auto store_k = [&](int stage) {
     if constexpr (F32)
       fk.store_t(lds + stage * TILE);
@@ -617,19 +699,22 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   };
   typename M::acc_t dsr = typename M::acc_t(0), dsn = typename M::acc_t(0);
   if (nkt > 0) {
-    fk.fetch(K, a.sk.t, 0, Tn, D, vec);
+    fk.start(K, a.sk.t, 0, Tn, D, vec);
+    fk.next();
     store_k(0);
     if (live(0)) load_ds(0, dsr);
   }
+  drain_vm();
   __syncthreads();
   for (int kt = 0; kt < nkt; ++kt) {
     const int cur = kt & 1;
     const bool more = kt + 1 < nkt;
     if (more) {
-      fk.fetch(K, a.sk.t, (kt + 1) * KT, Tn, D, vec);
+      fk.next();
       if (live(kt + 1)) load_ds(kt + 1, dsn);
     }
     if (live(kt)) {
+      valid_ds(kt, dsr);
       if constexpr (F32)
         mma_ldsT_regs<DP, LDT>(dq, lds + cur * TILE, 0, dsr, g, c);
       else
@@ -643,7 +728,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c);
 }
 
-template <typename T, int DP>
+template <typename T, int DP, bool FAST>
 __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   using M = AM<T>;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
@@ -682,10 +767,12 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
 
   const int qlast = (q0 + QB < Tn ? q0 + QB : Tn) - 1;
   const int nkb = q0 < Tn ? qlast / KB + 1 : 0;
-  TileFetch<T, KB, DP> fk, fv;
+  TileFetch<T, KB, DP, FAST> fk, fv;
   if (nkb > 0) {
-    fk.fetch(K, a.sk.t, 0, Tn, D, vec);
-    fv.fetch(V, a.sv.t, 0, Tn, D, vec);
+    fk.start(K, a.sk.t, 0, Tn, D, vec);
+    fv.start(V, a.sv.t, 0, Tn, D, vec);
+    fk.next();
+    fv.next();
     fk.store(lds);
     fv.store(lds + TILE);
   }
@@ -696,8 +783,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
     const T* Vs = Ks + TILE;
     const bool more = kb + 1 < nkb;
     if (more) {
-      fk.fetch(K, a.sk.t, k0 + KB, Tn, D, vec);
-      fv.fetch(V, a.sv.t, k0 + KB, Tn, D, vec);
+      fk.next();
+      fv.next();
     }
     const bool mask = (k0 + KB - 1 > wq0) || (k0 + KB > Tn) || !qok;
 #pragma unroll 1
@@ -739,11 +826,18 @@ static int pick_dp(int64_t D) {
   return -1;
 }
 
-#define DP_SWITCH(dp, KERNEL, T, grid)                                     \
-  switch (dp) {                                                            \
-    case 16: KERNEL<T, (sizeof(T) == 8 ? 16 : 32)><<<grid, 256, 0, stream()>>>(a); break; \
-    case 32: KERNEL<T, 32><<<grid, 256, 0, stream()>>>(a); break;          \
-    default: KERNEL<T, 64><<<grid, 256, 0, stream()>>>(a); break;         \
+#define DP_SWITCH_F(dp, KERNEL, T, grid, F)                                                  \
+  switch (dp) {                                                                              \
+    case 16: KERNEL<T, (sizeof(T) == 8 ? 16 : 32), F><<<grid, 256, 0, stream()>>>(a); break; \
+    case 32: KERNEL<T, 32, F><<<grid, 256, 0, stream()>>>(a); break;                         \
+    default: KERNEL<T, 64, F><<<grid, 256, 0, stream()>>>(a); break;                        \
+  }
+// FAST tile loads when 16-byte access is allowed and the head dimension fills the padded tile
+#define DP_SWITCH(dp, KERNEL, T, grid)                                              \
+  if (a.vec && a.D == (dp == 16 && sizeof(T) == 4 ? 32 : dp) && a.T % 64 == 0) { \
+    DP_SWITCH_F(dp, KERNEL, T, grid, true)              \
+  } else {                                               \
+    DP_SWITCH_F(dp, KERNEL, T, grid, false)             \
   }
 
 template <typename T>
@@ -788,10 +882,11 @@ static int attn_bwd_impl(AttnArgs& a) {
     attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
     dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
     DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
-    if (a.ds)
+    if (a.ds) {
       DP_SWITCH(dp, attn_bwd_q_ds_kernel, T, grid)
-    else
+    } else {
       DP_SWITCH(dp, attn_bwd_q_kernel, T, grid)
+    }
   }
   hipError_t le = hipGetLastError();
   pool_free(drow);
