@@ -11,14 +11,18 @@
 // 16 floats or 8 doubles; MFMA tiles of 32x32 (float32) or 16x16 (float64).
 // Each operand tile is staged in LDS in its global orientation (global -> LDS
 // is a straight 16-byte vector copy, fully coalesced along the contiguous
-// dimension), double-buffered with one barrier per k-tile and the next tile's
-// global loads in flight during the MFMAs. The loads go through per-thread
-// pointers set up once and advanced by one k-tile per load (rows past the
-// matrix edge clamped onto the last row), so the main loop has no index
-// arithmetic and no divergent branches; only a partial last k-tile is masked.
-// (256x128 and 128x256 tiles, a second register set for a two-tile-deep
-// prefetch, 32-wide k-tiles and higher occupancy measured no faster on the
-// GPT-2 shapes.)
+// dimension), with one barrier per k-tile and the next tiles' global loads in
+// flight during the MFMAs. The loads go through per-thread pointers set up
+// once and advanced by one k-tile per load (rows past the matrix edge clamped
+// onto the last row), so the main loop has no index arithmetic and no
+// divergent branches; only a partial last k-tile is masked.
+//   gemm_dma_kernel (float32, 16-byte aligned operands -- every GPT-2 GEMM):
+//     the loads go straight into LDS (global_load_lds_dwordx4) through three
+//     stages, in swizzled layouts that keep the fragment reads conflict-free.
+//   gemm_kernel (float64, and float32 with unaligned operands): registers ->
+//     LDS, double-buffered.
+// (256x128 and 128x256 tiles, 32-wide k-tiles, a two-tile register prefetch
+// and AGPR accumulators measured no faster on the GPT-2 shapes.)
 //
 // MFMA k-slots. An MFMA takes k in lane groups g = lane / MT (2 groups of 32
 // lanes for 32x32x2, 4 groups of 16 for 16x16x4). Within each 8-wide k chunk,
@@ -307,6 +311,66 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn)
   tn = r / gsz;
 }
 
+// The column sum of one B column over this block's k range: to colsum (or
+// added to it), or, with split-K, to the split's row of colsum_ws.
+template <typename T>
+__device__ __forceinline__ void finish_colsum(const GemmArgs& a, double csum, int64_t n, int split) {
+  if (n >= a.N) return;
+  if (a.colsum_ws) {
+    ((T*)a.colsum_ws)[(int64_t)split * a.N + n] = (T)csum;
+  } else {
+    T* cs = (T*)a.colsum;
+    cs[n] = a.colsum_accumulate ? cs[n] + (T)csum : (T)csum;
+  }
+}
+
+// A wave's TM x TN MFMA accumulators (its tile starts at row m0, column n0):
+// split-K partials go to the workspace as they are; otherwise the fused
+// epilogue writes C (and aux).
+template <typename T, int TM, int TN>
+__device__ __forceinline__ void write_acc(const GemmArgs& a, const typename MF<T>::acc_t (&acc)[TM][TN], int64_t m0,
+                                          int64_t n0, int g, int c, int split, int64_t batch) {
+  using MFT = MF<T>;
+  constexpr int MT = MFT::MT, NACC = MFT::NACC;
+  const bool to_ws = a.ws != nullptr;
+  T* C = to_ws ? (T*)a.ws + ((int64_t)split * gridDim.z + batch) * a.M * a.N : (T*)a.C + batch * a.sC;
+  const int64_t ldc = to_ws ? a.N : a.ldc;
+  const bool plain = to_ws || (a.addend == nullptr && a.epi == kEpiNone && !a.accumulate);
+  if (plain) {  // raw split-K partial, or v + bias
+    const T* bias = to_ws ? nullptr : (const T*)a.bias;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = n0 + j * MT + c;
+        if (n >= a.N) continue;
+        const T bn = bias ? bias[n] : T(0);
+#pragma unroll
+        for (int r = 0; r < NACC; ++r) {
+          const int64_t m = m0 + i * MT + MFT::row(r, g);
+          if (m >= a.M) continue;
+          T v = acc[i][j][r];
+          if (bias) v = v + bn;
+          C[m * ldc + n] = v;
+        }
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = n0 + j * MT + c;
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int r = 0; r < NACC; ++r) {
+          const int64_t m = m0 + i * MT + MFT::row(r, g);
+          if (m >= a.M) continue;
+          epilogue_store<T>(a, C, ldc, m, n, acc[i][j][r], batch);
+        }
+      }
+  }
+}
+
 // Block tile BM x BN, 4 waves in a 2 x 2 grid of (BM/2) x (BN/2) wave tiles.
 template <typename T, int BM, int BN, bool AKC, bool BKC, bool VECA, bool VECB>
 __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs a) {
@@ -415,57 +479,231 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs a) {
     if (kt + 1 < ntiles) store(kt + 1, cur ^ 1, ra, rb);
     __syncthreads();
   }
-  if (take_colsum) {
-    const int64_t n = n0 + threadIdx.x;
-    if (n < a.N) {
-      if (a.colsum_ws) {
-        ((T*)a.colsum_ws)[(int64_t)split * a.N + n] = (T)csum;
-      } else {
-        T* cs = (T*)a.colsum;
-        cs[n] = a.colsum_accumulate ? cs[n] + (T)csum : (T)csum;
-      }
+  if (take_colsum) finish_colsum<T>(a, csum, n0 + threadIdx.x, split);
+  write_acc<T, TM, TN>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
+}
+
+// ---------------------------------------------------------------------------
+// float32 with direct global -> LDS loads (global_load_lds_dwordx4: each lane
+// fetches 16 bytes that land at LDS base + 16 * lane, with no register
+// staging, no LDS store instructions and no wait before a store). Three LDS
+// stages: tile t's loads are issued two iterations before it is computed.
+// LDS layouts (a 1 KB load instruction fills 1 KB contiguously, so conflicts
+// are avoided by choosing which global vector each lane fetches):
+//   KC  (k-contiguous operand, 128 rows x 16 k): 1 KB chunks of 16 rows; the
+//       4-float k-vector v of chunk row r sits in 16-byte slot
+//       4 r + (v ^ kc_swz(r)), so the 16-byte fragment reads of 16
+//       consecutive rows hit distinct banks;
+//   MNC (mn-contiguous operand, 16 k-rows x 128): k-row k holds its 32
+//       mn-vectors u at slots 32 k + (u ^ mnc_swz(k)), so the two lane groups
+//       (k and k + 4) of a fragment read hit different bank halves.
+constexpr int kDmaStages = 3;
+
+__device__ __forceinline__ int kc_swz(int r) { return ((r >> 1) + (r >> 3)) & 3; }
+__device__ __forceinline__ int mnc_swz(int k) { return ((k >> 2) & 1) << 3; }
+
+// Float offset, within one 128 x 16 operand tile, of the 4-float vector of
+// (row/col mn, k-vector v) for KC, or of (k-row k, mn-vector u) for MNC.
+__device__ __forceinline__ int kc_off(int mn, int v) {
+  const int r = mn & 15;
+  return (mn >> 4) * 256 + (4 * r + (v ^ kc_swz(r))) * 4;
+}
+__device__ __forceinline__ int mnc_off(int k, int u) { return k * 128 + ((u ^ mnc_swz(k)) << 2); }
+
+// The two 1 KB load instructions of each wave per operand tile: per-lane
+// source pointers (set up once, advanced one k-tile per issue).
+template <bool KCONTIG>
+struct DmaSrc {
+  const float* p[2];
+  int64_t step;
+};
+
+template <bool KCONTIG>
+__device__ __forceinline__ void dma_init(DmaSrc<KCONTIG>& s, const float* __restrict__ P, int64_t ld, int64_t mn0,
+                                         int64_t MN, int64_t kbeg, int wave, int lane) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int j = wave * 2 + q;  // 1 KB chunk of the tile
+    if (KCONTIG) {
+      const int r = lane >> 2;
+      int64_t mn = mn0 + 16 * j + r;
+      mn = mn < MN ? mn : MN - 1;
+      const int v = (lane & 3) ^ kc_swz(r);
+      s.p[q] = P + mn * ld + kbeg + 4 * v;
+    } else {
+      const int k = 2 * j + (lane >> 5);
+      const int u = (lane & 31) ^ mnc_swz(k);
+      int64_t mn = mn0 + 4 * u;
+      mn = mn < MN ? mn : MN - 4;
+      s.p[q] = P + (kbeg + k) * ld + mn;
     }
   }
+  s.step = KCONTIG ? 16 : 16 * ld;
+}
 
-  // epilogue: split-K partials go to the workspace as they are; otherwise
-  // the fused epilogue writes C (and aux)
-  const bool to_ws = a.ws != nullptr;
-  T* C = to_ws ? (T*)a.ws + ((int64_t)split * gridDim.z + batch) * a.M * a.N : (T*)a.C + batch * a.sC;
-  const int64_t ldc = to_ws ? a.N : a.ldc;
-  const bool plain = to_ws || (a.addend == nullptr && a.epi == kEpiNone && !a.accumulate);
-  if (plain) {  // raw split-K partial, or v + bias
-    const T* bias = to_ws ? nullptr : (const T*)a.bias;
+template <bool KCONTIG>
+__device__ __forceinline__ void dma_issue(DmaSrc<KCONTIG>& s, float* __restrict__ tile, int wave) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int64_t n = n0 + wn0 + j * MT + c;
-        if (n >= a.N) continue;
-        const T bn = bias ? bias[n] : T(0);
-#pragma unroll
-        for (int r = 0; r < NACC; ++r) {
-          const int64_t m = m0 + wm0 + i * MT + MFT::row(r, g);
-          if (m >= a.M) continue;
-          T v = acc[i][j][r];
-          if (bias) v = v + bn;
-          C[m * ldc + n] = v;
-        }
-      }
-  } else {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int64_t n = n0 + wn0 + j * MT + c;
-        if (n >= a.N) continue;
-#pragma unroll
-        for (int r = 0; r < NACC; ++r) {
-          const int64_t m = m0 + wm0 + i * MT + MFT::row(r, g);
-          if (m >= a.M) continue;
-          epilogue_store<T>(a, C, ldc, m, n, acc[i][j][r], batch);
-        }
-      }
+  for (int q = 0; q < 2; ++q) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)s.p[q],
+                                     (__attribute__((address_space(3))) void*)(tile + (wave * 2 + q) * 256), 16, 0, 0);
+    s.p[q] += s.step;
   }
+}
+
+// The partial last k-tile through registers, stored in the same layouts
+// (k at or past kend as zeros).
+template <bool KCONTIG>
+__device__ __forceinline__ void dma_tail_store(float* __restrict__ tile, const TileRegs<float, KCONTIG, 128>& r,
+                                               int64_t k0, int64_t kend) {
+  using L = TileLayout<float, KCONTIG, 128>;
+#pragma unroll
+  for (int i = 0; i < L::NVEC; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    int off;
+    int64_t k;
+    if (KCONTIG) {
+      off = kc_off(f / 4, f % 4);
+      k = k0 + (f % 4) * 4;
+    } else {
+      off = mnc_off(f / 32, f % 32);
+      k = k0 + f / 32;
+    }
+    *reinterpret_cast<MF<float>::vec_t*>(tile + off) = k < kend ? r.v[i] : MF<float>::vec_t(0);
+  }
+}
+
+template <bool AKC, bool BKC>
+__global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
+  using MFT = MF<float>;
+  constexpr int BM = 128, BN = 128, BK = 16;
+  constexpr int MT = MFT::MT, VEC = MFT::VEC;
+  constexpr int TM = 2, TN = 2, NCH = BK / kKC;
+  constexpr int TILE = 128 * BK;  // floats per operand tile
+  constexpr int NST = kDmaStages;
+  __shared__ __attribute__((aligned(1024))) float lds[NST * 2 * TILE];
+
+  int tm, tn;
+  tile_coords(a, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int split = blockIdx.y;
+  const int64_t batch = blockIdx.z;
+  const int64_t kbeg = (int64_t)split * a.k_per_split;
+  const int64_t kend = kbeg + a.k_per_split < a.K ? kbeg + a.k_per_split : a.K;
+  const float* A = (const float*)a.A + batch * a.sA;
+  const float* B = (const float*)a.B + batch * a.sB;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / MT, c = lane % MT;
+  const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+
+  MFT::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = MFT::acc_t(0);
+
+  const int64_t ntiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+  const int64_t nfull = kend > kbeg ? (kend - kbeg) / BK : 0;
+  DmaSrc<AKC> sa;
+  DmaSrc<BKC> sb;
+  dma_init<AKC>(sa, A, a.lda, m0, a.M, kbeg, wave, lane);
+  dma_init<BKC>(sb, B, a.ldb, n0, a.N, kbeg, wave, lane);
+  auto tileA = [&](int st) { return lds + st * 2 * TILE; };
+  auto tileB = [&](int st) { return lds + st * 2 * TILE + TILE; };
+
+  // Per-lane fragment offsets within a tile: KC fragment (rows base + c,
+  // k-vector 2 ch + g); MNC fragment element s (k-row 8 ch + 4 g + s,
+  // column base + c).
+  auto frag = [&](const float* __restrict__ t, bool kcontig, int base, int ch) {
+    MFT::vec_t v;
+    if (kcontig) {
+      v = *reinterpret_cast<const MFT::vec_t*>(t + kc_off(base + c, 2 * ch + g));
+    } else {
+      const int n = base + c;
+#pragma unroll
+      for (int s = 0; s < VEC; ++s) v[s] = t[mnc_off(8 * ch + 4 * g + s, n >> 2) + (n & 3)];
+    }
+    return v;
+  };
+  const bool take_colsum = a.colsum != nullptr && tm == 0 && (int)threadIdx.x < BN;
+  double csum = 0.0;
+  auto compute = [&](int st) {
+    const float* As = tileA(st);
+    const float* Bs = tileB(st);
+#pragma unroll
+    for (int ch = 0; ch < NCH; ++ch) {
+      MFT::vec_t fa[TM], fb[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa[i] = frag(As, AKC, wm0 + i * MT, ch);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[j] = frag(Bs, BKC, wn0 + j * MT, ch);
+#pragma unroll
+      for (int s = 0; s < VEC; ++s)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i][j] = MFT::mma(fa[i][s], fb[j][s], acc[i][j]);
+    }
+    if (take_colsum) {
+      // this thread's column of the B tile, its 16 values in k order, then
+      // into the running float64 sum (k past kend was stored as zero)
+      const int n = threadIdx.x;
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < BK; ++k)
+        t = t + (BKC ? Bs[kc_off(n, k >> 2) + (k & 3)] : Bs[mnc_off(k, n >> 2) + (n & 3)]);
+      csum += (double)t;
+    }
+  };
+
+  // Prologue: tiles 0 .. NST-2 in flight.
+#pragma unroll
+  for (int t = 0; t < NST - 1; ++t) {
+    if (t < nfull) {
+      dma_issue<AKC>(sa, tileA(t), wave);
+      dma_issue<BKC>(sb, tileB(t), wave);
+    }
+  }
+  int st = 0;
+  for (int64_t kt = 0; kt < nfull; ++kt) {
+    // this wave's loads of tile kt have landed (the next tile's 4 may still
+    // be in flight), then every wave's have, and every wave is done with
+    // the stage about to be refilled
+    if (kt + 1 < nfull)
+      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // a bare s_barrier: the workgroup fence of __syncthreads would wait for
+    // every load in flight, the next tile's too (memory clobber: no LDS
+    // access moves across it)
+    asm volatile("s_barrier" ::: "memory");
+    if (kt + NST - 1 < nfull) {
+      const int sn = st == 0 ? NST - 1 : st - 1;  // (kt + NST - 1) % NST
+      dma_issue<AKC>(sa, tileA(sn), wave);
+      dma_issue<BKC>(sb, tileB(sn), wave);
+    }
+    compute(st);
+    st = st == NST - 1 ? 0 : st + 1;
+  }
+  if (ntiles > nfull) {  // the partial last k-tile, through registers
+    const int64_t k0 = kbeg + nfull * BK;
+    TilePtr<float, AKC, 128> pa;
+    TilePtr<float, BKC, 128> pb;
+    TileRegs<float, AKC, 128> ra;
+    TileRegs<float, BKC, 128> rb;
+    init_ptr<float, AKC, 128>(pa, A, a.lda, m0, a.M, k0);
+    init_ptr<float, BKC, 128>(pb, B, a.ldb, n0, a.N, k0);
+    load_tail<float, AKC, 128>(ra, pa, a.lda, k0, kend);
+    load_tail<float, BKC, 128>(rb, pb, a.ldb, k0, kend);
+    __syncthreads();  // every wave is done with the stage being refilled
+    dma_tail_store<AKC>(tileA(st), ra, k0, kend);
+    dma_tail_store<BKC>(tileB(st), rb, k0, kend);
+    __syncthreads();
+    compute(st);
+  }
+  if (take_colsum) finish_colsum<float>(a, csum, n0 + threadIdx.x, split);
+  write_acc<float, TM, TN>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
 }
 
 // Sum of the split-K partials in split order 0, 1, ..., S-1, then the
@@ -536,6 +774,12 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
 
 template <typename T, int BM, int BN, bool AKC, bool BKC>
 static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb) {
+  if constexpr (std::is_same<T, float>::value && BM == 128 && BN == 128) {
+    if (veca && vecb) {
+      gemm_dma_kernel<AKC, BKC><<<grid, 256, 0, stream()>>>(a);
+      return;
+    }
+  }
   if (veca && vecb)
     gemm_kernel<T, BM, BN, AKC, BKC, true, true><<<grid, 256, 0, stream()>>>(a);
   else if (veca)
