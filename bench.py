@@ -182,7 +182,7 @@ def main(argv=None):
     ms_step = 1e3 * dt / a.steps
     n, ms, work = fams["gemm"]
     gemm_tflops = work / (ms * 1e-3) / 1e12 if ms else 0.0
-    roofline = {"bound": "mfma", "kernel": "gemm_kernel (MFMA f32 32x32x2, Linear fwd/dX/dW)",
+    roofline = {"bound": "mfma", "kernel": "gemm_dma_kernel (MFMA f32 32x32x2, Linear fwd/dX/dW)",
                 "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
                 "frac": round(gemm_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": _profiled_traffic(),
                 "launches": n, "avg_launch_ms": round(ms / max(n, 1), 4),
@@ -317,7 +317,7 @@ def micro_ln_linear(a):
     return _line("LN + Linear backward GEMM throughput (dX, dW) at x[16384,768] W[768,3072]",
                  round(flop / (1e-3 * ms / a.steps) / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"LayerNorm + Linear backward, x [16384,768], W [768,3072], dY [16384,3072], {a.dtype}"},
-                 {"bound": "mfma", "kernel": "gemm_kernel", "achieved": round(ach / 1e12, 2),
+                 {"bound": "mfma", "kernel": "gemm_dma_kernel" if a.dtype == "float32" else "gemm_kernel", "achieved": round(ach / 1e12, 2),
                   "peak": _mfma_peak(a.dtype) / 1e12, "unit": "TFLOP/s",
                   "frac": round(ach / _mfma_peak(a.dtype), 4), "traffic": None},
                  cpu, {"ln_bwd": {"GB/s": round(ln_work / (ln_ms * 1e-3) / 1e9, 1),
