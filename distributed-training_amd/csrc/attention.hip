@@ -175,6 +175,11 @@ __device__ __forceinline__ void mma_lds_t_regs(typename AM<T>::acc_t (&out)[DP /
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ double ex2(double x) { return exp2(x); }
 
+// Column swizzle of the transposed LDS tiles: XOR of bits 2-3 of the column
+// with bits 4-5 of the row, so groups of 4 columns stay 16-byte aligned and a
+// wave's transposed stores (16 rows 4 apart, 4 columns) hit 64 distinct banks.
+__device__ __forceinline__ int tswz(int row) { return ((row >> 4) & 3) << 2; }
+
 // Registers for one NR x DP tile in flight from global memory (16-byte
 // vectors, 256 threads), stored to LDS [NR][DP + PAD] after the current tile's
 // MFMAs. Rows >= Tn and columns >= D are zero.
@@ -266,8 +271,9 @@ struct TileFetch {
     }
   }
 
-  // The same tile transposed: ldsT[d][row], row stride NR + 4 (keeps 16-byte
-  // alignment for the vector reads of mma_ldsT_regs).
+  // The same tile transposed: ldsT[d][row ^ tswz(d)], row stride NR + 4
+  // (keeps 16-byte alignment for the vector reads of mma_ldsT_regs; the
+  // swizzle spreads a wave's scalar stores over all banks).
   static constexpr int LDT = NR + 4;
   __device__ __forceinline__ void store_t(T* __restrict__ ldsT) const {
 #pragma unroll
@@ -277,7 +283,7 @@ struct TileFetch {
       const int rr = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
       const V x = value(i, rr);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) ldsT[(d + e) * LDT + rr] = x[e];
+      for (int e = 0; e < VEC; ++e) ldsT[(d + e) * LDT + (rr ^ tswz(d + e))] = x[e];
     }
   }
 };
@@ -293,8 +299,9 @@ __device__ __forceinline__ void mma_ldsT_regs(AM<float>::acc_t (&out)[DP / 32], 
   for (int a4 = 0; a4 < 4; ++a4)
 #pragma unroll
     for (int dt = 0; dt < DP / 32; ++dt) {
+      const int row = dt * 32 + c;
       const AM<float>::vec_t v =
-          *reinterpret_cast<const AM<float>::vec_t*>(ldsT + (dt * 32 + c) * LDT + jbase + 8 * a4 + 4 * g);
+          *reinterpret_cast<const AM<float>::vec_t*>(ldsT + row * LDT + ((jbase + 8 * a4 + 4 * g) ^ tswz(row)));
 #pragma unroll
       for (int e = 0; e < 4; ++e) out[dt] = AM<float>::mma(v[e], pacc[4 * a4 + e], out[dt]);
     }
