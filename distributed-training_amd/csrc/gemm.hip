@@ -502,28 +502,34 @@ constexpr int kDmaStages = 3;
 __device__ __forceinline__ int kc_swz(int r) { return ((r >> 1) + (r >> 3)) & 3; }
 __device__ __forceinline__ int mnc_swz(int k) { return ((k >> 2) & 1) << 3; }
 
-// Float offset, within one 128 x 16 operand tile, of the 4-float vector of
+// Float offset, within one BMN x 16 operand tile, of the 4-float vector of
 // (row/col mn, k-vector v) for KC, or of (k-row k, mn-vector u) for MNC.
 __device__ __forceinline__ int kc_off(int mn, int v) {
   const int r = mn & 15;
   return (mn >> 4) * 256 + (4 * r + (v ^ kc_swz(r))) * 4;
 }
-__device__ __forceinline__ int mnc_off(int k, int u) { return k * 128 + ((u ^ mnc_swz(k)) << 2); }
+template <int BMN>
+__device__ __forceinline__ int mnc_off(int k, int u) {
+  return k * BMN + ((u ^ mnc_swz(k)) << 2);
+}
 
-// The two 1 KB load instructions of each wave per operand tile: per-lane
-// source pointers (set up once, advanced one k-tile per issue).
-template <bool KCONTIG>
+// The BMN / 64 load instructions (1 KB each) of each wave per operand tile:
+// per-lane source pointers, set up once and advanced one k-tile per issue.
+template <bool KCONTIG, int BMN>
 struct DmaSrc {
-  const float* p[2];
+  static constexpr int NQ = BMN / 64;
+  const float* p[NQ];
   int64_t step;
 };
 
-template <bool KCONTIG>
-__device__ __forceinline__ void dma_init(DmaSrc<KCONTIG>& s, const float* __restrict__ P, int64_t ld, int64_t mn0,
-                                         int64_t MN, int64_t kbeg, int wave, int lane) {
+template <bool KCONTIG, int BMN>
+__device__ __forceinline__ void dma_init(DmaSrc<KCONTIG, BMN>& s, const float* __restrict__ P, int64_t ld,
+                                         int64_t mn0, int64_t MN, int64_t kbeg, int wave, int lane) {
+  constexpr int NQ = DmaSrc<KCONTIG, BMN>::NQ;
+  constexpr int RV = BMN / 4;  // mn-vectors per k-row (MNC)
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int j = wave * 2 + q;  // 1 KB chunk of the tile
+  for (int q = 0; q < NQ; ++q) {
+    const int j = wave * NQ + q;  // 1 KB chunk of the tile
     if (KCONTIG) {
       const int r = lane >> 2;
       int64_t mn = mn0 + 16 * j + r;
@@ -531,8 +537,8 @@ __device__ __forceinline__ void dma_init(DmaSrc<KCONTIG>& s, const float* __rest
       const int v = (lane & 3) ^ kc_swz(r);
       s.p[q] = P + mn * ld + kbeg + 4 * v;
     } else {
-      const int k = 2 * j + (lane >> 5);
-      const int u = (lane & 31) ^ mnc_swz(k);
+      const int k = j * (64 / RV) + lane / RV;
+      const int u = (lane % RV) ^ mnc_swz(k);
       int64_t mn = mn0 + 4 * u;
       mn = mn < MN ? mn : MN - 4;
       s.p[q] = P + (kbeg + k) * ld + mn;
@@ -541,22 +547,24 @@ __device__ __forceinline__ void dma_init(DmaSrc<KCONTIG>& s, const float* __rest
   s.step = KCONTIG ? 16 : 16 * ld;
 }
 
-template <bool KCONTIG>
-__device__ __forceinline__ void dma_issue(DmaSrc<KCONTIG>& s, float* __restrict__ tile, int wave) {
+template <bool KCONTIG, int BMN>
+__device__ __forceinline__ void dma_issue(DmaSrc<KCONTIG, BMN>& s, float* __restrict__ tile, int wave) {
+  constexpr int NQ = DmaSrc<KCONTIG, BMN>::NQ;
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
+  for (int q = 0; q < NQ; ++q) {
     __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)s.p[q],
-                                     (__attribute__((address_space(3))) void*)(tile + (wave * 2 + q) * 256), 16, 0, 0);
+                                     (__attribute__((address_space(3))) void*)(tile + (wave * NQ + q) * 256), 16, 0, 0);
     s.p[q] += s.step;
   }
 }
 
 // The partial last k-tile through registers, stored in the same layouts
 // (k at or past kend as zeros).
-template <bool KCONTIG>
-__device__ __forceinline__ void dma_tail_store(float* __restrict__ tile, const TileRegs<float, KCONTIG, 128>& r,
+template <bool KCONTIG, int BMN>
+__device__ __forceinline__ void dma_tail_store(float* __restrict__ tile, const TileRegs<float, KCONTIG, BMN>& r,
                                                int64_t k0, int64_t kend) {
-  using L = TileLayout<float, KCONTIG, 128>;
+  using L = TileLayout<float, KCONTIG, BMN>;
+  constexpr int RV = BMN / 4;
 #pragma unroll
   for (int i = 0; i < L::NVEC; ++i) {
     const int f = threadIdx.x + 256 * i;
@@ -566,22 +574,25 @@ __device__ __forceinline__ void dma_tail_store(float* __restrict__ tile, const T
       off = kc_off(f / 4, f % 4);
       k = k0 + (f % 4) * 4;
     } else {
-      off = mnc_off(f / 32, f % 32);
-      k = k0 + f / 32;
+      off = mnc_off<BMN>(f / RV, f % RV);
+      k = k0 + f / RV;
     }
     *reinterpret_cast<MF<float>::vec_t*>(tile + off) = k < kend ? r.v[i] : MF<float>::vec_t(0);
   }
 }
 
-template <bool AKC, bool BKC>
-__global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
+// Block tile BM x BN (128 or 256 each), 4 waves in a 2 x 2 grid of
+// (BM/2) x (BN/2) wave tiles.
+template <int BM, int BN, bool AKC, bool BKC>
+__global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(GemmArgs a) {
   using MFT = MF<float>;
-  constexpr int BM = 128, BN = 128, BK = 16;
+  constexpr int BK = 16;
   constexpr int MT = MFT::MT, VEC = MFT::VEC;
-  constexpr int TM = 2, TN = 2, NCH = BK / kKC;
-  constexpr int TILE = 128 * BK;  // floats per operand tile
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / MT, TN = WN / MT, NCH = BK / kKC;
+  constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // floats per operand tile
   constexpr int NST = kDmaStages;
-  __shared__ __attribute__((aligned(1024))) float lds[NST * 2 * TILE];
+  __shared__ __attribute__((aligned(1024))) float lds[NST * (TILE_A + TILE_B)];
 
   int tm, tn;
   tile_coords(a, tm, tn);
@@ -595,7 +606,7 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
-  const int wm0 = (wave >> 1) * 64, wn0 = (wave & 1) * 64;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
 
   MFT::acc_t acc[TM][TN];
 #pragma unroll
@@ -605,24 +616,26 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
 
   const int64_t ntiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   const int64_t nfull = kend > kbeg ? (kend - kbeg) / BK : 0;
-  DmaSrc<AKC> sa;
-  DmaSrc<BKC> sb;
-  dma_init<AKC>(sa, A, a.lda, m0, a.M, kbeg, wave, lane);
-  dma_init<BKC>(sb, B, a.ldb, n0, a.N, kbeg, wave, lane);
-  auto tileA = [&](int st) { return lds + st * 2 * TILE; };
-  auto tileB = [&](int st) { return lds + st * 2 * TILE + TILE; };
+  DmaSrc<AKC, BM> sa;
+  DmaSrc<BKC, BN> sb;
+  dma_init<AKC, BM>(sa, A, a.lda, m0, a.M, kbeg, wave, lane);
+  dma_init<BKC, BN>(sb, B, a.ldb, n0, a.N, kbeg, wave, lane);
+  auto tileA = [&](int st) { return lds + st * (TILE_A + TILE_B); };
+  auto tileB = [&](int st) { return lds + st * (TILE_A + TILE_B) + TILE_A; };
 
   // Per-lane fragment offsets within a tile: KC fragment (rows base + c,
   // k-vector 2 ch + g); MNC fragment element s (k-row 8 ch + 4 g + s,
   // column base + c).
-  auto frag = [&](const float* __restrict__ t, bool kcontig, int base, int ch) {
+  auto frag = [&](const float* __restrict__ t, bool kcontig, int bmn, int base, int ch) {
     MFT::vec_t v;
     if (kcontig) {
       v = *reinterpret_cast<const MFT::vec_t*>(t + kc_off(base + c, 2 * ch + g));
     } else {
       const int n = base + c;
 #pragma unroll
-      for (int s = 0; s < VEC; ++s) v[s] = t[mnc_off(8 * ch + 4 * g + s, n >> 2) + (n & 3)];
+      for (int s = 0; s < VEC; ++s)
+        v[s] = t[(bmn == 256 ? mnc_off<256>(8 * ch + 4 * g + s, n >> 2) : mnc_off<128>(8 * ch + 4 * g + s, n >> 2)) +
+                 (n & 3)];
     }
     return v;
   };
@@ -635,9 +648,9 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
     for (int ch = 0; ch < NCH; ++ch) {
       MFT::vec_t fa[TM], fb[TN];
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[i] = frag(As, AKC, wm0 + i * MT, ch);
+      for (int i = 0; i < TM; ++i) fa[i] = frag(As, AKC, BM, wm0 + i * MT, ch);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) fb[j] = frag(Bs, BKC, wn0 + j * MT, ch);
+      for (int j = 0; j < TN; ++j) fb[j] = frag(Bs, BKC, BN, wn0 + j * MT, ch);
 #pragma unroll
       for (int s = 0; s < VEC; ++s)
 #pragma unroll
@@ -652,7 +665,7 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
       float t = 0.f;
 #pragma unroll
       for (int k = 0; k < BK; ++k)
-        t = t + (BKC ? Bs[kc_off(n, k >> 2) + (k & 3)] : Bs[mnc_off(k, n >> 2) + (n & 3)]);
+        t = t + (BKC ? Bs[kc_off(n, k >> 2) + (k & 3)] : Bs[mnc_off<BN>(k, n >> 2) + (n & 3)]);
       csum += (double)t;
     }
   };
@@ -661,8 +674,8 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
 #pragma unroll
   for (int t = 0; t < NST - 1; ++t) {
     if (t < nfull) {
-      dma_issue<AKC>(sa, tileA(t), wave);
-      dma_issue<BKC>(sb, tileB(t), wave);
+      dma_issue<AKC, BM>(sa, tileA(t), wave);
+      dma_issue<BKC, BN>(sb, tileB(t), wave);
     }
   }
   int st = 0;
@@ -680,25 +693,25 @@ __global__ void __launch_bounds__(256, 2) gemm_dma_kernel(GemmArgs a) {
     asm volatile("s_barrier" ::: "memory");
     if (kt + NST - 1 < nfull) {
       const int sn = st == 0 ? NST - 1 : st - 1;  // (kt + NST - 1) % NST
-      dma_issue<AKC>(sa, tileA(sn), wave);
-      dma_issue<BKC>(sb, tileB(sn), wave);
+      dma_issue<AKC, BM>(sa, tileA(sn), wave);
+      dma_issue<BKC, BN>(sb, tileB(sn), wave);
     }
     compute(st);
     st = st == NST - 1 ? 0 : st + 1;
   }
   if (ntiles > nfull) {  // the partial last k-tile, through registers
     const int64_t k0 = kbeg + nfull * BK;
-    TilePtr<float, AKC, 128> pa;
-    TilePtr<float, BKC, 128> pb;
-    TileRegs<float, AKC, 128> ra;
-    TileRegs<float, BKC, 128> rb;
-    init_ptr<float, AKC, 128>(pa, A, a.lda, m0, a.M, k0);
-    init_ptr<float, BKC, 128>(pb, B, a.ldb, n0, a.N, k0);
-    load_tail<float, AKC, 128>(ra, pa, a.lda, k0, kend);
-    load_tail<float, BKC, 128>(rb, pb, a.ldb, k0, kend);
+    TilePtr<float, AKC, BM> pa;
+    TilePtr<float, BKC, BN> pb;
+    TileRegs<float, AKC, BM> ra;
+    TileRegs<float, BKC, BN> rb;
+    init_ptr<float, AKC, BM>(pa, A, a.lda, m0, a.M, k0);
+    init_ptr<float, BKC, BN>(pb, B, a.ldb, n0, a.N, k0);
+    load_tail<float, AKC, BM>(ra, pa, a.lda, k0, kend);
+    load_tail<float, BKC, BN>(rb, pb, a.ldb, k0, kend);
     __syncthreads();  // every wave is done with the stage being refilled
-    dma_tail_store<AKC>(tileA(st), ra, k0, kend);
-    dma_tail_store<BKC>(tileB(st), rb, k0, kend);
+    dma_tail_store<AKC, BM>(tileA(st), ra, k0, kend);
+    dma_tail_store<BKC, BN>(tileB(st), rb, k0, kend);
     __syncthreads();
     compute(st);
   }
@@ -774,12 +787,13 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
 
 template <typename T, int BM, int BN, bool AKC, bool BKC>
 static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb) {
-  if constexpr (std::is_same<T, float>::value && BM == 128 && BN == 128) {
+  if constexpr (std::is_same<T, float>::value) {
     if (veca && vecb) {
-      gemm_dma_kernel<AKC, BKC><<<grid, 256, 0, stream()>>>(a);
+      gemm_dma_kernel<BM, BN, AKC, BKC><<<grid, 256, 0, stream()>>>(a);
       return;
     }
   }
+  if constexpr (BM != 128 || BN != 128) return;  // larger tiles: aligned float32 only (see gemm_impl)
   if (veca && vecb)
     gemm_kernel<T, BM, BN, AKC, BKC, true, true><<<grid, 256, 0, stream()>>>(a);
   else if (veca)
@@ -810,6 +824,38 @@ struct EpiArgs {
   int colsum_accumulate = 0;
 };
 
+// K splits. A grid of b blocks on C CUs runs ceil(b / C) rounds, so its
+// useful fraction is b / (C * ceil(b / C)); take the fewest splits (each
+// keeping >= 256 of K) that reach 90 % of rounds, else the best found.
+static int choose_splits(int64_t tiles, int64_t batch, int64_t K, int64_t cus) {
+  int splits = 1;
+  double e_best = 0.0;
+  for (int sp = 1; sp <= 16; ++sp) {
+    if (sp > 1 && K / sp < 256) break;
+    const int64_t blocks = tiles * batch * sp;
+    const double eff = (double)blocks / (double)(cus * cdiv(blocks, cus));
+    if (eff > e_best + 1e-9) {
+      e_best = eff;
+      splits = sp;
+    }
+    if (eff >= 0.9) break;
+  }
+  return splits;
+}
+
+// Block tile of the aligned float32 kernel: 256 x 128 when every block still
+// gets a long k range (>= 1024) and the grid covers the CUs, else 128 x 128.
+// The larger tile moves 25 % fewer bytes per MFMA through the loads and LDS
+// but has half the blocks; on the GPT-2 shapes it wins for the long-K
+// products (dW, the vocabulary head's dX and dW) and loses on K = 768.
+static void pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t cus, int& bm, int& bn) {
+  bm = bn = 128;
+  if (M < 256) return;
+  const int64_t tiles = cdiv(M, 256) * cdiv(N, 128);
+  const int sp = choose_splits(tiles, batch, K, cus);
+  if (tiles * batch * sp >= cus && K / sp >= 1024) bm = 256;
+}
+
 template <typename T>
 static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda, int64_t sA,
                      const void* B, int64_t ldb, int64_t sB, void* C, int64_t ldc, int64_t sC, int64_t batch,
@@ -835,28 +881,13 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   a.aux = ep.aux;
   a.colsum = ep.colsum;
   a.colsum_accumulate = ep.colsum_accumulate;
-  // K splits. A grid of b blocks on C CUs runs ceil(b / C) rounds, so its
-  // useful fraction is b / (C * ceil(b / C)); take the fewest splits (each
-  // keeping >= 256 of K) that reach 90 % of rounds, else the best found.
   const int64_t cus = num_cus() > 0 ? num_cus() : 256;
-  constexpr int bm = 128, bn = 128;
+  const bool veca = aligned(A, 16) && lda % VEC == 0 && (batch == 1 || sA % VEC == 0) && (akc ? K % VEC == 0 : M % VEC == 0);
+  const bool vecb = aligned(B, 16) && ldb % VEC == 0 && (batch == 1 || sB % VEC == 0) && (bkc ? K % VEC == 0 : N % VEC == 0);
+  int bm = 128, bn = 128;
+  if (std::is_same<T, float>::value && veca && vecb) pick_tile(M, N, K, batch, cus, bm, bn);
   const int64_t tmn = cdiv(M, bm) * cdiv(N, bn);
-  int splits = 1;
-  if (force_splits > 0) {
-    splits = force_splits;
-  } else {
-    double e_best = 0.0;
-    for (int sp = 1; sp <= 16; ++sp) {
-      if (sp > 1 && K / sp < 256) break;
-      const int64_t blocks = tmn * batch * sp;
-      const double eff = (double)blocks / (double)(cus * cdiv(blocks, cus));
-      if (eff > e_best + 1e-9) {
-        e_best = eff;
-        splits = sp;
-      }
-      if (eff >= 0.9) break;
-    }
-  }
+  int splits = force_splits > 0 ? force_splits : choose_splits(tmn, batch, K, cus);
   a.tiles_m = (int)cdiv(M, bm);
   a.tiles_n = (int)cdiv(N, bn);
   const int64_t tiles = (int64_t)a.tiles_m * a.tiles_n;
@@ -867,8 +898,6 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   splits = (int)cdiv(K > 0 ? K : 1, kps);
   a.k_per_split = kps;
   const size_t es = sizeof(T);
-  bool veca = aligned(A, 16) && lda % VEC == 0 && (batch == 1 || sA % VEC == 0) && (akc ? K % VEC == 0 : M % VEC == 0);
-  bool vecb = aligned(B, 16) && ldb % VEC == 0 && (batch == 1 || sB % VEC == 0) && (bkc ? K % VEC == 0 : N % VEC == 0);
   void* ws = nullptr;
   if (splits > 1) {
     const size_t main_bytes = (size_t)splits * batch * M * N * es;
@@ -881,7 +910,18 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
   {
     TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
-    launch_layout<T, bm, bn>(a, grid, akc, bkc, veca, vecb);
+    if constexpr (std::is_same<T, float>::value) {
+      if (bm == 256 && bn == 256)
+        launch_layout<T, 256, 256>(a, grid, akc, bkc, veca, vecb);
+      else if (bm == 256)
+        launch_layout<T, 256, 128>(a, grid, akc, bkc, veca, vecb);
+      else if (bn == 256)
+        launch_layout<T, 128, 256>(a, grid, akc, bkc, veca, vecb);
+      else
+        launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb);
+    } else {
+      launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb);
+    }
     if (splits > 1) {
       int64_t total = batch * M * N;
       int rg = (int)(cdiv(total, 256 * 4) < 8192 ? cdiv(total, 256 * 4) : 8192);

@@ -144,6 +144,24 @@ def test_gemm_split_k_with_partial_last_tile(dev, dt, akc, bkc):
     assert bits_equal(outs[1], outs[2])
 
 
+@pytest.mark.parametrize("akc,bkc", [(True, False), (True, True), (False, False), (False, True)])
+def test_gemm_large_tile_ragged_edges_and_k_tail(dev, akc, bkc):
+    """float32 shapes whose k range per block is long enough for the 256 x 128
+    block tile: M, N not multiples of the tile, K = 2052 over 2 splits (the
+    second ends in a partial k-tile); split results bit-identical run to run."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(21)
+    M, N, K = 2000, 2040, 2052
+    a = rng.standard_normal((M, K) if akc else (K, M)).astype(np.float32)
+    b = rng.standard_normal((N, K) if bkc else (K, N)).astype(np.float32)
+    ref = _gemm_ref(a.astype(np.float64), b.astype(np.float64), akc, bkc)
+    da, db = D.from_numpy(a), D.from_numpy(b)
+    outs = [K_.gemm(da, db, a_kcontig=akc, b_kcontig=bkc, splits=s).numpy() for s in (0, 0, 1)]
+    for o in outs:
+        assert rel_err(o, ref) <= TOL[np.float32]
+    assert bits_equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
 def test_batched_gemm(dev, dt):
     D, K_ = _dev()
@@ -186,7 +204,8 @@ def test_linear_forward_backward_at_layernorm_linear_workload(dev, dt):
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
-@pytest.mark.parametrize("M,K,N", [(1024, 256, 512), (256, 4096, 96), (300, 68, 132)])
+@pytest.mark.parametrize("M,K,N", [(1024, 256, 512), (256, 4096, 96), (300, 68, 132), (2048, 2048, 2048),
+                                   (4096, 1024, 2048)])
 def test_fused_linear_epilogues_equal_the_unfused_ops(dev, dt, M, K, N):
     """Residual add, GELU and GELU backward in the GEMM epilogue give the same
     bits as the separate kernels (with and without split-K)."""
