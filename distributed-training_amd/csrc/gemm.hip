@@ -514,12 +514,17 @@ __device__ __forceinline__ int mnc_off(int k, int u) {
 }
 
 // The BMN / 64 load instructions (1 KB each) of each wave per operand tile:
-// per-lane source pointers, set up once and advanced one k-tile per issue.
+// a wave-uniform base address (the current k-tile's origin, advanced by
+// scalar adds) and fixed per-lane 32-bit byte offsets, so issuing a tile
+// takes no vector instructions. Offsets are >= 0: clamped rows / columns
+// stay at or after the tile origin (the origin is inside the matrix, and
+// MN - 4 >= mn0 because MN and mn0 are multiples of 4).
 template <bool KCONTIG, int BMN>
 struct DmaSrc {
   static constexpr int NQ = BMN / 64;
-  const float* p[NQ];
-  int64_t step;
+  const float* base;
+  unsigned off[NQ];
+  int64_t step;  // elements per k-tile
 };
 
 template <bool KCONTIG, int BMN>
@@ -527,6 +532,7 @@ __device__ __forceinline__ void dma_init(DmaSrc<KCONTIG, BMN>& s, const float* _
                                          int64_t mn0, int64_t MN, int64_t kbeg, int wave, int lane) {
   constexpr int NQ = DmaSrc<KCONTIG, BMN>::NQ;
   constexpr int RV = BMN / 4;  // mn-vectors per k-row (MNC)
+  s.base = KCONTIG ? P + mn0 * ld + kbeg : P + kbeg * ld + mn0;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const int j = wave * NQ + q;  // 1 KB chunk of the tile
@@ -535,28 +541,42 @@ __device__ __forceinline__ void dma_init(DmaSrc<KCONTIG, BMN>& s, const float* _
       int64_t mn = mn0 + 16 * j + r;
       mn = mn < MN ? mn : MN - 1;
       const int v = (lane & 3) ^ kc_swz(r);
-      s.p[q] = P + mn * ld + kbeg + 4 * v;
+      s.off[q] = (unsigned)(((mn - mn0) * ld + 4 * v) * 4);
     } else {
       const int k = j * (64 / RV) + lane / RV;
       const int u = (lane % RV) ^ mnc_swz(k);
       int64_t mn = mn0 + 4 * u;
       mn = mn < MN ? mn : MN - 4;
-      s.p[q] = P + (kbeg + k) * ld + mn;
+      s.off[q] = (unsigned)((k * ld + (mn - mn0)) * 4);
     }
   }
   s.step = KCONTIG ? 16 : 16 * ld;
 }
 
-template <bool KCONTIG, int BMN>
-__device__ __forceinline__ void dma_issue(DmaSrc<KCONTIG, BMN>& s, float* __restrict__ tile, int wave) {
+// Issue one operand tile: chunk q of this wave lands at LDS byte address
+// lds_wave + LDS_OFF + 1024 q (lds_wave: wave-uniform, this wave's first
+// chunk of stage 0). m0 takes the LDS address one wait state before the load.
+template <int LDS_OFF, bool KCONTIG, int BMN>
+__device__ __forceinline__ void dma_issue(DmaSrc<KCONTIG, BMN>& s, unsigned lds_wave) {
   constexpr int NQ = DmaSrc<KCONTIG, BMN>::NQ;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)s.p[q],
-                                     (__attribute__((address_space(3))) void*)(tile + (wave * NQ + q) * 256), 16, 0, 0);
-    s.p[q] += s.step;
-  }
+  for (int q = 0; q < NQ; ++q)
+    asm volatile("s_add_u32 m0, %2, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(s.off[q]), "s"(s.base),
+                 "s"(lds_wave), "n"(LDS_OFF + 1024 * q)
+                 : "memory", "m0");
+  s.base += s.step;
 }
+
+// This wave's loads except the newest N have landed, then every wave's have.
+template <int N>
+__device__ __forceinline__ void dma_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <int V>
+struct IC {
+  static constexpr int value = V;
+};
 
 // The partial last k-tile through registers, stored in the same layouts
 // (k at or past kend as zeros).
@@ -614,14 +634,21 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
 #pragma unroll
     for (int j = 0; j < TN; ++j) acc[i][j] = MFT::acc_t(0);
 
-  const int64_t ntiles = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-  const int64_t nfull = kend > kbeg ? (kend - kbeg) / BK : 0;
+  const int ntiles = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
+  const int nfull = kend > kbeg ? (int)((kend - kbeg) / BK) : 0;
   DmaSrc<AKC, BM> sa;
   DmaSrc<BKC, BN> sb;
   dma_init<AKC, BM>(sa, A, a.lda, m0, a.M, kbeg, wave, lane);
   dma_init<BKC, BN>(sb, B, a.ldb, n0, a.N, kbeg, wave, lane);
   auto tileA = [&](int st) { return lds + st * (TILE_A + TILE_B); };
   auto tileB = [&](int st) { return lds + st * (TILE_A + TILE_B) + TILE_A; };
+  // LDS byte address of this wave's first A chunk and first B chunk in stage
+  // 0 (the low 32 bits of a generic LDS address are the LDS offset)
+  const unsigned lds0 = (unsigned)(uintptr_t)lds;
+  const unsigned ldsA = __builtin_amdgcn_readfirstlane(lds0 + wave * DmaSrc<AKC, BM>::NQ * 1024u);
+  const unsigned ldsB = __builtin_amdgcn_readfirstlane(lds0 + TILE_A * 4 + wave * DmaSrc<BKC, BN>::NQ * 1024u);
+  constexpr int STAGE_BYTES = (TILE_A + TILE_B) * 4;
+  constexpr int NQT = DmaSrc<AKC, BM>::NQ + DmaSrc<BKC, BN>::NQ;  // loads per wave per k-tile
 
   // Per-lane fragment offsets within a tile: KC fragment (rows base + c,
   // k-vector 2 ch + g); MNC fragment element s (k-row 8 ch + 4 g + s,
@@ -643,7 +670,7 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
   double csum = 0.0;
   auto compute = [&](int st) {
     const float* As = tileA(st);
-    const float* Bs = tileB(st);
+    const float* Bs = tileB(st);  // st is a constant in the main loop: immediate LDS offsets
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
       MFT::vec_t fa[TM], fb[TN];
@@ -670,37 +697,38 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
     }
   };
 
-  // Prologue: tiles 0 .. NST-2 in flight.
-#pragma unroll
-  for (int t = 0; t < NST - 1; ++t) {
-    if (t < nfull) {
-      dma_issue<AKC, BM>(sa, tileA(t), wave);
-      dma_issue<BKC, BN>(sb, tileB(t), wave);
-    }
-  }
-  int st = 0;
-  for (int64_t kt = 0; kt < nfull; ++kt) {
-    // this wave's loads of tile kt have landed (the next tile's 4 may still
-    // be in flight), then every wave's have, and every wave is done with
-    // the stage about to be refilled
+  static_assert(NST == 3, "the main loop is unrolled over three stages");
+  auto issue = [&](auto stc) {
+    constexpr int st = decltype(stc)::value;
+    dma_issue<st * STAGE_BYTES>(sa, ldsA);
+    dma_issue<st * STAGE_BYTES>(sb, ldsB);
+  };
+  // One k-tile: this wave's loads of tile kt have landed (the next tile's
+  // may still be in flight), then every wave's have, and every wave is done
+  // with the stage about to be refilled (that of tile kt - 1); then the
+  // loads of tile kt + 2 and the MFMAs of tile kt.
+  auto step = [&](auto stc, int kt) {
+    constexpr int st = decltype(stc)::value;
     if (kt + 1 < nfull)
-      __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+      dma_wait_barrier<NQT>();
     else
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    // a bare s_barrier: the workgroup fence of __syncthreads would wait for
-    // every load in flight, the next tile's too (memory clobber: no LDS
-    // access moves across it)
-    asm volatile("s_barrier" ::: "memory");
-    if (kt + NST - 1 < nfull) {
-      const int sn = st == 0 ? NST - 1 : st - 1;  // (kt + NST - 1) % NST
-      dma_issue<AKC, BM>(sa, tileA(sn), wave);
-      dma_issue<BKC, BN>(sb, tileB(sn), wave);
-    }
+      dma_wait_barrier<0>();
+    if (kt + 2 < nfull) issue(IC<(st + 2) % 3>());
     compute(st);
-    st = st == NST - 1 ? 0 : st + 1;
+  };
+  if (nfull > 0) issue(IC<0>());
+  if (nfull > 1) issue(IC<1>());
+  int kt = 0;
+  for (; kt + 3 <= nfull; kt += 3) {
+    step(IC<0>(), kt);
+    step(IC<1>(), kt + 1);
+    step(IC<2>(), kt + 2);
   }
+  if (kt < nfull) step(IC<0>(), kt);
+  if (kt + 1 < nfull) step(IC<1>(), kt + 1);
+  const int st = nfull % 3;  // stage of the partial tile, if any
   if (ntiles > nfull) {  // the partial last k-tile, through registers
-    const int64_t k0 = kbeg + nfull * BK;
+    const int64_t k0 = kbeg + (int64_t)nfull * BK;
     TilePtr<float, AKC, BM> pa;
     TilePtr<float, BKC, BN> pb;
     TileRegs<float, AKC, BM> ra;
