@@ -814,9 +814,9 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
 }
 
 template <typename T, int BM, int BN, bool AKC, bool BKC>
-static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb) {
+static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb, bool dma) {
   if constexpr (std::is_same<T, float>::value) {
-    if (veca && vecb) {
+    if (dma) {
       gemm_dma_kernel<BM, BN, AKC, BKC><<<grid, 256, 0, stream()>>>(a);
       return;
     }
@@ -833,15 +833,15 @@ static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb) {
 }
 
 template <typename T, int BM, int BN>
-static void launch_layout(const GemmArgs& a, dim3 grid, int akc, int bkc, bool veca, bool vecb) {
+static void launch_layout(const GemmArgs& a, dim3 grid, int akc, int bkc, bool veca, bool vecb, bool dma) {
   if (akc && bkc)
-    launch_variant<T, BM, BN, true, true>(a, grid, veca, vecb);
+    launch_variant<T, BM, BN, true, true>(a, grid, veca, vecb, dma);
   else if (akc)
-    launch_variant<T, BM, BN, true, false>(a, grid, veca, vecb);
+    launch_variant<T, BM, BN, true, false>(a, grid, veca, vecb, dma);
   else if (bkc)
-    launch_variant<T, BM, BN, false, true>(a, grid, veca, vecb);
+    launch_variant<T, BM, BN, false, true>(a, grid, veca, vecb, dma);
   else
-    launch_variant<T, BM, BN, false, false>(a, grid, veca, vecb);
+    launch_variant<T, BM, BN, false, false>(a, grid, veca, vecb, dma);
 }
 
 struct EpiArgs {
@@ -912,8 +912,11 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   const int64_t cus = num_cus() > 0 ? num_cus() : 256;
   const bool veca = aligned(A, 16) && lda % VEC == 0 && (batch == 1 || sA % VEC == 0) && (akc ? K % VEC == 0 : M % VEC == 0);
   const bool vecb = aligned(B, 16) && ldb % VEC == 0 && (batch == 1 || sB % VEC == 0) && (bkc ? K % VEC == 0 : N % VEC == 0);
+  // The direct-to-LDS kernel addresses a tile with 32-bit byte offsets from
+  // its origin: leading dimensions below 2^22 elements keep them in range.
+  const bool dma = std::is_same<T, float>::value && veca && vecb && lda < (1 << 22) && ldb < (1 << 22);
   int bm = 128, bn = 128;
-  if (std::is_same<T, float>::value && veca && vecb) pick_tile(M, N, K, batch, cus, bm, bn);
+  if (dma) pick_tile(M, N, K, batch, cus, bm, bn);
   const int64_t tmn = cdiv(M, bm) * cdiv(N, bn);
   int splits = force_splits > 0 ? force_splits : choose_splits(tmn, batch, K, cus);
   a.tiles_m = (int)cdiv(M, bm);
@@ -940,15 +943,15 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
     TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
     if constexpr (std::is_same<T, float>::value) {
       if (bm == 256 && bn == 256)
-        launch_layout<T, 256, 256>(a, grid, akc, bkc, veca, vecb);
+        launch_layout<T, 256, 256>(a, grid, akc, bkc, veca, vecb, dma);
       else if (bm == 256)
-        launch_layout<T, 256, 128>(a, grid, akc, bkc, veca, vecb);
+        launch_layout<T, 256, 128>(a, grid, akc, bkc, veca, vecb, dma);
       else if (bn == 256)
-        launch_layout<T, 128, 256>(a, grid, akc, bkc, veca, vecb);
+        launch_layout<T, 128, 256>(a, grid, akc, bkc, veca, vecb, dma);
       else
-        launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb);
+        launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb, dma);
     } else {
-      launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb);
+      launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb, dma);
     }
     if (splits > 1) {
       int64_t total = batch * M * N;
