@@ -184,9 +184,10 @@ __device__ __forceinline__ int tswz(int row) { return ((row >> 4) & 3) << 2; }
 // vectors, 256 threads), stored to LDS [NR][DP + PAD] after the current tile's
 // MFMAs. Rows >= Tn and columns >= D are zero.
 //
-// FAST (16-byte access allowed, D == DP and T a multiple of 64, so every tile
-// lies inside [0, T)): every thread issues the same loads from persistent
-// pointers with no branch. Otherwise each element is bounds-checked.
+// FAST (16-byte access allowed, D == DP and T a multiple of 128, so every
+// tile and every block lies inside [0, T)): every thread issues the same
+// loads from persistent pointers with no branch. Otherwise each element is
+// bounds-checked.
 template <typename T, int NR, int DP, bool FAST>
 struct TileFetch {
   typedef typename AM<T>::vec_t V;
@@ -371,6 +372,11 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
 
   typename M::vec_t qf[DP / 8];
   load_frag_rows<T, DP>(qf, Q, a.sq.t, qr, Tn, D, g, vec);
+  if constexpr (FAST && sizeof(T) == 4) {
+    // scores straight in base-2 units: q * scale * log2(e) once, not per score
+#pragma unroll
+    for (int ch = 0; ch < DP / 8; ++ch) qf[ch] *= sl2;
+  }
   typename M::acc_t oacc[DP / MT];
 #pragma unroll
   for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] = typename M::acc_t(0);
@@ -408,7 +414,7 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
       for (int jt = 0; jt < KB / MT; ++jt)
 #pragma unroll
         for (int i = 0; i < NACC; ++i) {
-          T s = sacc[jt][i] * sl2;
+          T s = FAST && sizeof(T) == 4 ? sacc[jt][i] : sacc[jt][i] * sl2;
           if (mask) {
             const int j = k0 + jt * MT + M::row(i, g);
             s = (j <= qr && j < Tn) ? s : ninf;
@@ -432,8 +438,12 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
       psum = group_sum(psum);
       lrow = lrow * alpha + psum;
       mrow = mnew;
+      // rescale the output only when some lane's max moved (alpha == 1
+      // leaves it unchanged bit for bit)
+      if (__any(alpha != T(1))) {
 #pragma unroll
-      for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
+        for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
+      }
 #pragma unroll
       for (int jt = 0; jt < KB / MT; ++jt) mma_lds_t_regs<T, DP>(oacc, Vs, jt * MT, sacc[jt], g, c);
     }
@@ -484,7 +494,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   constexpr int STAGE = 2 * TILE + 2 * TILE_T;  // Q, dO (+ their transposes)
   constexpr int LDS_N = 2 * STAGE > KBB * LD ? 2 * STAGE : KBB * LD;
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
-  __shared__ __attribute__((aligned(16))) T stats[2][3][QT];  // row max (base 2), 1 / row sum, rowsum(dO * O)
+  // per query row: max (base 2), 1 / sum, rowsum(dO * O), max + log2(sum)
+  __shared__ __attribute__((aligned(16))) T stats[2][4][QT];
 
   int bx, bh;
   xcd_block(bx, bh);
@@ -505,6 +516,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   T* DS = a.ds ? (T*)a.ds + (int64_t)bh * Tn * Tn : nullptr;
   const T sl2 = (T)(a.scale * 1.4426950408889634);
   const bool vec = a.vec != 0;
+  // this lane's dS byte offset from a tile's first row: row 4g, column kj
+  const unsigned ds_lane = (unsigned)(4 * g * Tn + kj) * (unsigned)sizeof(T);
 
   typename M::vec_t kf[DP / 8], vf[DP / 8];
   load_frag_rows<T, DP>(kf, K, a.sk.t, kj, Tn, D, g, vec);
@@ -549,6 +562,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
       stats[stage][0][threadIdx.x] = st0;
       stats[stage][1][threadIdx.x] = T(1) / st1;
       stats[stage][2][threadIdx.x] = st2;
+      stats[stage][3][threadIdx.x] = st0 + log2(st1);
     }
   };
   if (nqt > 0) {
@@ -593,15 +607,41 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
         }
       };
       if constexpr (F32) {
-        // rows 8a + 4g + 0..3 of MFMA steps 4a .. 4a+3: one 16-byte read per statistic
+        if constexpr (FAST) {
+          // Every row of the tile and every key of the block lie inside
+          // [0, T): no bounds tests. P = 2^(s sl2 - (m + log2 sum)): one
+          // fma and one exp. dS rows are addressed from a wave-uniform row
+          // pointer plus this lane's fixed offset, so the stores take no
+          // vector address arithmetic.
+          const int lim = kj - qs - 4 * g;  // row qs + 4g + x sees key kj iff x >= lim
+          T* dsb = DS ? DS + (int64_t)qs * Tn : nullptr;
 #pragma unroll
-        for (int a4 = 0; a4 < NACC / 4; ++a4) {
-          const int r0 = 8 * a4 + 4 * g;
-          const typename M::vec_t m4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][0][r0]);
-          const typename M::vec_t l4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][1][r0]);
-          const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
+          for (int a4 = 0; a4 < NACC / 4; ++a4) {
+            const int r0 = 8 * a4 + 4 * g;
+            const typename M::vec_t ml4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][3][r0]);
+            const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) prob(4 * a4 + e, m4[e], l4[e], d4[e]);
+            for (int e = 0; e < 4; ++e) {
+              const int i = 4 * a4 + e;
+              T p = ex2(__builtin_fmaf(s[i], sl2, -ml4[e]));
+              if (mask) p = 8 * a4 + e >= lim ? p : T(0);
+              s[i] = p;
+              const T v = p * (dp[i] - d4[e]);
+              dp[i] = v;
+              if (DS) *(T*)((char*)(dsb + (int64_t)(8 * a4 + e) * Tn) + ds_lane) = v;
+            }
+          }
+        } else {
+          // rows 8a + 4g + 0..3 of MFMA steps 4a .. 4a+3: one 16-byte read per statistic
+#pragma unroll
+          for (int a4 = 0; a4 < NACC / 4; ++a4) {
+            const int r0 = 8 * a4 + 4 * g;
+            const typename M::vec_t m4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][0][r0]);
+            const typename M::vec_t l4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][1][r0]);
+            const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) prob(4 * a4 + e, m4[e], l4[e], d4[e]);
+          }
         }
         // dV^T += dO^T P ; dK^T += Q^T dS (transposed tiles: vector reads)
         mma_ldsT_regs<DP, LDT>(dv, Qs + 2 * TILE + TILE_T, 0, s, g, c);
@@ -841,7 +881,7 @@ static int pick_dp(int64_t D) {
   }
 // FAST tile loads when 16-byte access is allowed and the head dimension fills the padded tile
 #define DP_SWITCH(dp, KERNEL, T, grid)                                              \
-  if (a.vec && a.D == (dp == 16 && sizeof(T) == 4 ? 32 : dp) && a.T % 64 == 0) { \
+  if (a.vec && a.D == (dp == 16 && sizeof(T) == 4 ? 32 : dp) && a.T % 128 == 0) { \
     DP_SWITCH_F(dp, KERNEL, T, grid, true)              \
   } else {                                               \
     DP_SWITCH_F(dp, KERNEL, T, grid, false)             \
