@@ -359,7 +359,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index in a scalar register: conditions on it are wave-uniform branches
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / MT, c = lane % MT;
   const int wq0 = q0 + wave * MT;
   const int qr = wq0 + c;  // this lane's query (column)
@@ -410,21 +411,31 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
       // causal mask only where a key of the tile can exceed a query of the wave
       const bool mask = (k0 + KB - 1 > wq0) || (k0 + KB > Tn);
       T bmax = ninf;
+      // the mask test hoisted out of the per-score loop (two copies of it)
+      auto scores = [&](auto maskc) {
+        constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
-      for (int jt = 0; jt < KB / MT; ++jt)
+        for (int jt = 0; jt < KB / MT; ++jt)
 #pragma unroll
-        for (int i = 0; i < NACC; ++i) {
-          T s = FAST && sizeof(T) == 4 ? sacc[jt][i] : sacc[jt][i] * sl2;
-          if (mask) {
-            const int j = k0 + jt * MT + M::row(i, g);
-            s = (j <= qr && j < Tn) ? s : ninf;
+          for (int i = 0; i < NACC; ++i) {
+            T s = FAST && sizeof(T) == 4 ? sacc[jt][i] : sacc[jt][i] * sl2;
+            if constexpr (MASK) {
+              const int j = k0 + jt * MT + M::row(i, g);
+              s = (j <= qr && j < Tn) ? s : ninf;
+            }
+            sacc[jt][i] = s;
+            bmax = fmax(bmax, s);
           }
-          sacc[jt][i] = s;
-          bmax = fmax(bmax, s);
-        }
+      };
+      if (mask)
+        scores(std::true_type());
+      else
+        scores(std::false_type());
       bmax = group_max(bmax);
       const T mnew = fmax(mrow, bmax);
-      const bool live = mnew != ninf;
+      // aligned path: every query sees key 0 in the first tile, so the max is
+      // finite from then on
+      const bool live = FAST || mnew != ninf;
       const T alpha = live ? ex2(mrow - mnew) : T(1);
       T psum = T(0);
 #pragma unroll
@@ -502,7 +513,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int k0 = bx * KBB;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index in a scalar register: conditions on it are wave-uniform branches
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / MT, c = lane % MT;
   const int wk0 = k0 + wave * MT;
   const int kj = wk0 + c;  // this lane's key (column)
@@ -614,23 +626,31 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
           // pointer plus this lane's fixed offset, so the stores take no
           // vector address arithmetic.
           const int lim = kj - qs - 4 * g;  // row qs + 4g + x sees key kj iff x >= lim
-          T* dsb = DS ? DS + (int64_t)qs * Tn : nullptr;
+          T* dsb = DS + (int64_t)qs * Tn;  // the aligned path always runs with the dS workspace
+          // the mask test hoisted out of the per-score loop
+          auto probs = [&](auto maskc) {
+            constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
-          for (int a4 = 0; a4 < NACC / 4; ++a4) {
-            const int r0 = 8 * a4 + 4 * g;
-            const typename M::vec_t ml4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][3][r0]);
-            const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
+            for (int a4 = 0; a4 < NACC / 4; ++a4) {
+              const int r0 = 8 * a4 + 4 * g;
+              const typename M::vec_t ml4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][3][r0]);
+              const typename M::vec_t d4 = *reinterpret_cast<const typename M::vec_t*>(&stats[cur][2][r0]);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int i = 4 * a4 + e;
-              T p = ex2(__builtin_fmaf(s[i], sl2, -ml4[e]));
-              if (mask) p = 8 * a4 + e >= lim ? p : T(0);
-              s[i] = p;
-              const T v = p * (dp[i] - d4[e]);
-              dp[i] = v;
-              if (DS) *(T*)((char*)(dsb + (int64_t)(8 * a4 + e) * Tn) + ds_lane) = v;
+              for (int e = 0; e < 4; ++e) {
+                const int i = 4 * a4 + e;
+                T p = ex2(__builtin_fmaf(s[i], sl2, -ml4[e]));
+                if constexpr (MASK) p = 8 * a4 + e >= lim ? p : T(0);
+                s[i] = p;
+                const T v = p * (dp[i] - d4[e]);
+                dp[i] = v;
+                *(T*)((char*)(dsb + (int64_t)(8 * a4 + e) * Tn) + ds_lane) = v;
+              }
             }
-          }
+          };
+          if (mask)
+            probs(std::true_type());
+          else
+            probs(std::false_type());
         } else {
           // rows 8a + 4g + 0..3 of MFMA steps 4a .. 4a+3: one 16-byte read per statistic
 #pragma unroll
@@ -689,7 +709,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index in a scalar register: conditions on it are wave-uniform branches
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / MT, c = lane % MT;
   const int wq0 = q0 + wave * MT;
   const int qr = wq0 + c;
@@ -790,7 +811,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index in a scalar register: conditions on it are wave-uniform branches
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane / MT, c = lane % MT;
   const int wq0 = q0 + wave * MT;
   const int qr = wq0 + c;
@@ -928,7 +950,11 @@ static int attn_bwd_impl(AttnArgs& a) {
     TimedLaunch tl(DTMI_FAM_ATTN_BWD, 5.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
     attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
     dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
-    DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
+    if (a.ds) {
+      DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
+    } else {  // the aligned key-block pass writes dS unconditionally
+      DP_SWITCH_F(dp, attn_bwd_kv_kernel, T, grid, false)
+    }
     if (a.ds) {
       DP_SWITCH(dp, attn_bwd_q_ds_kernel, T, grid)
     } else {

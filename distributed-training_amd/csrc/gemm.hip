@@ -942,9 +942,7 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   {
     TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
     if constexpr (std::is_same<T, float>::value) {
-      if (bm == 256 && bn == 256)
-        launch_layout<T, 256, 256>(a, grid, akc, bkc, veca, vecb, dma);
-      else if (bm == 256)
+      if (bm == 256)
         launch_layout<T, 256, 128>(a, grid, akc, bkc, veca, vecb, dma);
       else if (bn == 256)
         launch_layout<T, 128, 256>(a, grid, akc, bkc, veca, vecb, dma);
