@@ -556,14 +556,19 @@ __device__ __forceinline__ void dma_init(DmaSrc<KCONTIG, BMN>& s, const float* _
 // Issue one operand tile: chunk q of this wave lands at LDS byte address
 // lds_wave + LDS_OFF + 1024 q (lds_wave: wave-uniform, this wave's first
 // chunk of stage 0). m0 takes the LDS address one wait state before the load.
+// The asm writes no SCC (an s_add here would clobber the carry of a 64-bit
+// scalar add the compiler may have split around it): the address is summed
+// outside and moved in with s_mov_b32.
 template <int LDS_OFF, bool KCONTIG, int BMN>
 __device__ __forceinline__ void dma_issue(DmaSrc<KCONTIG, BMN>& s, unsigned lds_wave) {
   constexpr int NQ = DmaSrc<KCONTIG, BMN>::NQ;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q)
-    asm volatile("s_add_u32 m0, %2, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(s.off[q]), "s"(s.base),
-                 "s"(lds_wave), "n"(LDS_OFF + 1024 * q)
+  for (int q = 0; q < NQ; ++q) {
+    const unsigned dst = lds_wave + (unsigned)(LDS_OFF + 1024 * q);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(s.off[q]), "s"(s.base),
+                 "s"(dst)
                  : "memory", "m0");
+  }
   s.base += s.step;
 }
 

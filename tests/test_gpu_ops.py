@@ -162,6 +162,34 @@ def test_gemm_large_tile_ragged_edges_and_k_tail(dev, akc, bkc):
     assert bits_equal(outs[0], outs[1])
 
 
+@pytest.mark.parametrize("akc,bkc,which", [(True, False, "A"), (False, False, "A"), (True, False, "B"),
+                                           (True, True, "B")])
+def test_gemm_operand_crossing_a_4gib_address_boundary(dev, akc, bkc, which):
+    """float32 operands placed so that the per-k-tile advance of the loads'
+    64-bit base address carries into its high dword (a 4 GiB boundary is
+    crossed inside the k loop); the result must match the reference."""
+    D, K_ = _dev()
+    M, N, K = 512, 384, 2048
+    rng = np.random.default_rng(31)
+    a = rng.standard_normal((M, K) if akc else (K, M)).astype(np.float32)
+    b = rng.standard_normal((N, K) if bkc else (K, N)).astype(np.float32)
+    big = D.empty(((4 << 30) // 4 + (64 << 20) // 4,), np.float32)
+    boundary = -(-big.ptr // (1 << 32)) * (1 << 32)
+    assert boundary + (32 << 20) <= big.ptr + big.nbytes
+    # the operand starts a few k-tiles (or k-rows) before the boundary
+    x = a if which == "A" else b
+    lead = 5 * 64 if (akc if which == "A" else bkc) else 3 * 64 * x.shape[1]
+    e0 = (boundary - big.ptr - lead) // 4
+    view = big[e0:e0 + x.size].reshape(*x.shape)
+    view.assign(x)
+    other = D.from_numpy(b if which == "A" else a)
+    da, db = (view, other) if which == "A" else (other, view)
+    ref = _gemm_ref(a.astype(np.float64), b.astype(np.float64), akc, bkc)
+    for splits in (1, 0):
+        got = K_.gemm(da, db, a_kcontig=akc, b_kcontig=bkc, splits=splits).numpy()
+        assert rel_err(got, ref) <= TOL[np.float32]
+
+
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
 def test_batched_gemm(dev, dt):
     D, K_ = _dev()
