@@ -330,18 +330,18 @@ __device__ __forceinline__ void store_result(T* __restrict__ lds, const typename
 
 // ----------------------------------------------------------------- forward
 // rowmax is kept in base-2 units: m = log2(e) * max_j (q . k_j * scale).
-// Blocks are dealt to the 8 XCDs round-robin by linear block id, and every
-// query (or key) block of one (batch, head) reads the same K/V (or Q/dO)
-// rows. Remap the linear id so each XCD gets a contiguous range of
-// (batch, head) pairs with all of their blocks: those rows are fetched once
-// per XCD's L2 instead of once per XCD.
-__device__ __forceinline__ void xcd_block(int& bx, int& by) {
-  const int gx = (int)gridDim.x;
-  const int total = gx * (int)gridDim.y;
-  int L = (int)blockIdx.x + gx * (int)blockIdx.y;
-  if ((total & 7) == 0) L = (L & 7) * (total >> 3) + (L >> 3);
-  bx = L % gx;
-  by = L / gx;
+// Blocks start in linear-id order and are dealt to the 8 XCDs round-robin.
+// Causal blocks differ in length (the last query block visits every key
+// tile, the first one a single tile), and a long block that starts late
+// leaves most of the chip idle while it finishes. So the linear id is split
+// as rank * (B*H) + bh: all (batch, head) pairs' longest blocks (rank 0)
+// start first, then rank 1, ... With B*H a multiple of 8 every block of one
+// (batch, head) also lands on the same XCD, so its K/V (or Q/dO) rows are
+// fetched into one L2.
+__device__ __forceinline__ void causal_block(int& rank, int& bh) {
+  const int L = (int)blockIdx.x + (int)gridDim.x * (int)blockIdx.y;
+  rank = L / (int)gridDim.y;
+  bh = L % (int)gridDim.y;
 }
 
 template <typename T, int DP, bool FAST>
@@ -354,8 +354,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
   constexpr int LDS_N = 2 * STAGE > QB * LD ? 2 * STAGE : QB * LD;
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
 
-  int bx, bh;
-  xcd_block(bx, bh);
+  int bx, bh;  // bx: length rank (0 = longest)
+  causal_block(bx, bh);
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
@@ -508,8 +508,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   // per query row: max (base 2), 1 / sum, rowsum(dO * O), max + log2(sum)
   __shared__ __attribute__((aligned(16))) T stats[2][4][QT];
 
-  int bx, bh;
-  xcd_block(bx, bh);
+  int bx, bh;  // bx: length rank (0 = longest)
+  causal_block(bx, bh);
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int k0 = bx * KBB;
@@ -704,8 +704,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   constexpr int LDS_N = 2 * TILE > QB * LD ? 2 * TILE : QB * LD;
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
 
-  int bx, bh;
-  xcd_block(bx, bh);
+  int bx, bh;  // bx: length rank (0 = longest)
+  causal_block(bx, bh);
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
@@ -806,8 +806,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   constexpr int LDS_N = 2 * STAGE > QB * LD ? 2 * STAGE : QB * LD;
   __shared__ __attribute__((aligned(16))) T lds[LDS_N];
 
-  int bx, bh;
-  xcd_block(bx, bh);
+  int bx, bh;  // bx: length rank (0 = longest)
+  causal_block(bx, bh);
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, D = (int)a.D;
   const int q0 = (int)(gridDim.x - 1 - bx) * QB;  // longest causal rows first
