@@ -38,6 +38,7 @@ import numpy as np  # noqa: E402
 
 METRIC = "fwd+bwd+AdamW tokens/sec at GPT-2-small shape; % MFMA / % HBM roofline"
 PEAK_FP32_MFMA = 157.3e12
+PEAK_BF16_MFMA = 2.5e15  # dense bf16 MFMA (no sparsity)
 PEAK_HBM = 8.0e12
 CFG = dict(vocab=50304, ctx=1024, dim=768, heads=12, layers=12, dtype="float32")
 BATCH, WORLD = 8, 4
@@ -136,6 +137,9 @@ def main(argv=None):
                     help="gpt2: the headline training step; the others are the per-path microbenchmarks")
     ap.add_argument("--dtype", default="float32", choices=["float32", "float64"],
                     help="compute dtype of the microbenchmarks (the gpt2 step is float32)")
+    ap.add_argument("--gemm-math", default="f32", choices=["f32", "bf16x6"],
+                    help="arithmetic of the float32 GEMMs: float32 MFMA, or operands split exactly into three "
+                         "bf16 parts with the six largest partial products on the bf16 MFMA")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the data-parallel exchange is simulated on-device over {WORLD} replicas "
@@ -149,6 +153,8 @@ def main(argv=None):
     from dtmi import _lib
     from dtmi import ddp as P, nn as N, optim as O, replicas as R, train as S
     from dtmi.autograd import Indices
+
+    _lib.set_gemm_math(a.gemm_math)
 
     info = _lib.device_info()
     print(f"[bench] device {info['name']} ({info['num_cus']} CUs); building GPT-2-small weights", file=sys.stderr,
@@ -182,11 +188,22 @@ def main(argv=None):
     ms_step = 1e3 * dt / a.steps
     n, ms, work = fams["gemm"]
     gemm_tflops = work / (ms * 1e-3) / 1e12 if ms else 0.0
-    roofline = {"bound": "mfma", "kernel": "gemm_dma_kernel (MFMA f32 32x32x2, Linear fwd/dX/dW)",
-                "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
-                "frac": round(gemm_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": _profiled_traffic(),
-                "launches": n, "avg_launch_ms": round(ms / max(n, 1), 4),
-                "flop_per_step": gemm_flops_per_step(CFG, BATCH, WORLD)}
+    if a.gemm_math == "f32":
+        roofline = {"bound": "mfma", "kernel": "gemm_dma_kernel (MFMA f32 32x32x2, Linear fwd/dX/dW)",
+                    "achieved": round(gemm_tflops, 2), "peak": PEAK_FP32_MFMA / 1e12, "unit": "TFLOP/s",
+                    "frac": round(gemm_tflops * 1e12 / PEAK_FP32_MFMA, 4), "traffic": _profiled_traffic(),
+                    "launches": n, "avg_launch_ms": round(ms / max(n, 1), 4),
+                    "flop_per_step": gemm_flops_per_step(CFG, BATCH, WORLD)}
+    else:
+        # six bf16 MFMA products per float32 product: the matrix cores run 6x
+        # the float32-equivalent FLOP, against the dense bf16 peak
+        roofline = {"bound": "mfma", "kernel": ("gemm_x6_kernel (MFMA bf16 32x32x16, float32 operands split "
+                                                "exactly into 3 bf16 parts, 6 partial products, Linear fwd/dX/dW)"),
+                    "achieved": round(6 * gemm_tflops, 2), "peak": PEAK_BF16_MFMA / 1e12, "unit": "TFLOP/s",
+                    "frac": round(6 * gemm_tflops * 1e12 / PEAK_BF16_MFMA, 4), "traffic": None,
+                    "fp32_equivalent_TFLOP/s": round(gemm_tflops, 2),
+                    "launches": n, "avg_launch_ms": round(ms / max(n, 1), 4),
+                    "flop_per_step": gemm_flops_per_step(CFG, BATCH, WORLD)}
     kernels = {}
     for f, (cnt, fms, fwork) in fams.items():
         if not cnt:
@@ -208,7 +225,7 @@ def main(argv=None):
                                    "buckets, fixed-order average, clip 1.0, AdamW"),
                       "global_batch": WORLD * BATCH, "seq_len": CFG["ctx"], "parallelism": "dp4-simulated",
                       "params": sum(int(np.prod(s)) for _, s in param_spec(CFG))},
-           "roofline": roofline, "kernels": kernels, "loss": round(loss, 5)}
+           "roofline": roofline, "kernels": kernels, "loss": round(loss, 5), "gemm_math": a.gemm_math}
     if not a.no_cpu_baseline:
         print("[bench] CPU baseline (oracle) ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(weights, xs, ys, a.cpu_seq)

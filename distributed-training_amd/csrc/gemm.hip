@@ -752,6 +752,279 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
   write_acc<float, TM, TN>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
 }
 
+// ---------------------------------------------------------------------------
+// float32 products on the bf16 matrix cores (v_mfma_f32_32x32x16_bf16).
+//
+// A float32 x is the exact sum of three bf16 values: x0 = bf16(x), x1 =
+// bf16(x - x0), x2 = x - x0 - x1 (round-to-nearest-even each time; x has 24
+// significant bits and each step takes the leading 8, so x2 is left with at
+// most 8 and bf16 holds it exactly). Then a*b = sum of the 9 products a_i b_j,
+// each exact in float32 (8-bit by 8-bit significands). The kernel adds the 6
+// with i + j <= 2 into float32 MFMA accumulators, smallest first, and drops
+// a1 b2, a2 b1 and a2 b2: |a1| <= 2^-8 |a| and |a2| <= 2^-16 |a|, so what is
+// dropped is below 2^-23 |a b| (about one float32 rounding of the product).
+// The bf16 MFMA runs 16x the float32 MFMA's rate, so the 6 products take
+// 3/8 of the matrix-core time of one float32 MFMA product.
+//
+// Data path: global float32 -> registers (16-byte vectors along k, or 8-byte
+// vectors along m/n for m/n-contiguous operands, 4 k-rows at a time) ->
+// split (v_cvt_pk_bf16_f32, two values per instruction) -> LDS as three bf16
+// planes per operand, each [row][16 k] with the two 16-byte k-halves of a row
+// swapped on every other group of 8 rows, so the MFMA fragment reads
+// (ds_read_b128: lane (g, c) reads row c, k 8g..8g+7) hit distinct banks.
+// k-tile 16 (one MFMA k-step), two LDS stages, one barrier per k-tile.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+constexpr int kX6BK = 16;
+
+// x and y as three packed bf16 pairs (low half = x): p0 + p1 + p2 == (x, y) exactly.
+// One v_cvt_pk_bf16_f32 per level; the two halves are widened back to float32
+// by bit operations on the packed result (<< 16, & 0xffff0000).
+// (as an asm statement: written as two __bf16 conversions, the compiler
+// rebuilds the low half from a separate one-value conversion)
+__device__ __forceinline__ unsigned cvt_pk_bf16(float x, float y) {
+  unsigned r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+  return r;
+}
+__device__ __forceinline__ void split3(float x, float y, unsigned& p0, unsigned& p1, unsigned& p2) {
+  p0 = cvt_pk_bf16(x, y);
+  const float rx = x - __uint_as_float(p0 << 16), ry = y - __uint_as_float(p0 & 0xffff0000u);
+  p1 = cvt_pk_bf16(rx, ry);
+  p2 = cvt_pk_bf16(rx - __uint_as_float(p1 << 16), ry - __uint_as_float(p1 & 0xffff0000u));
+}
+
+// byte offset of k-quad kq (k = 4kq..4kq+3) of `row` in one bf16 plane
+__device__ __forceinline__ int x6_quad_off(int row, int kq) {
+  return row * 32 + 16 * ((kq >> 1) ^ ((row >> 3) & 1)) + 8 * (kq & 1);
+}
+// byte offset of lane group g's 8 k-values (k = 8g..8g+7) of `row`
+__device__ __forceinline__ int x6_frag_off(int row, int g) { return row * 32 + 16 * (g ^ ((row >> 3) & 1)); }
+
+// Splits the 4 consecutive-k values v of `row` (k-quad kq) into the 3 planes.
+template <int PLANE>
+__device__ __forceinline__ void x6_store_quad(char* __restrict__ lds, int row, int kq, float v0, float v1, float v2,
+                                              float v3) {
+  unsigned a0, a1, a2, b0, b1, b2;
+  split3(v0, v1, a0, a1, a2);
+  split3(v2, v3, b0, b1, b2);
+  typedef unsigned u2 __attribute__((ext_vector_type(2)));
+  const int o = x6_quad_off(row, kq);
+  *reinterpret_cast<u2*>(lds + o) = u2{a0, b0};
+  *reinterpret_cast<u2*>(lds + PLANE + o) = u2{a1, b1};
+  *reinterpret_cast<u2*>(lds + 2 * PLANE + o) = u2{a2, b2};
+}
+
+// One operand's BMN x 16 float32 tile. KCONTIG: NV = BMN/64 16-byte vectors
+// per thread (row f/4, k-quad f%4). Otherwise NV = BMN/128 groups per thread
+// of 4 k-rows x 2 adjacent columns (8-byte vectors; columns 2*(f % (BMN/2)),
+// k-quad f / (BMN/2)). Addresses are a wave-uniform base (advanced one k-tile
+// per load, in scalar registers) plus per-thread 32-bit byte offsets fixed for
+// the whole k loop; rows or columns past the matrix edge are clamped onto the
+// last ones (they feed only outputs that are never stored). The host keeps
+// every offset below 2^32 (leading dimension < 2^22 elements).
+template <bool KCONTIG, int BMN>
+struct X6Src {
+  static constexpr int NV = KCONTIG ? BMN / 64 : BMN / 128;
+  static constexpr int NF = KCONTIG ? 1 : 4;  // loads per vector slot
+  typedef typename std::conditional<KCONTIG, MF<float>::vec_t, f32x2_t>::type ld_t;
+  const char* base;
+  unsigned off[NV][NF];
+  int64_t step;  // bytes per k-tile
+  ld_t v[NV][NF];
+
+  __device__ __forceinline__ void init(const float* __restrict__ P, int64_t ld, int64_t mn0, int64_t MN,
+                                       int64_t kbeg) {
+    base = reinterpret_cast<const char*>(KCONTIG ? P + mn0 * ld + kbeg : P + kbeg * ld + mn0);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      if (KCONTIG) {
+        int64_t mn = mn0 + f / 4;
+        mn = mn < MN ? mn : MN - 1;
+        off[i][0] = (unsigned)(((mn - mn0) * ld + 4 * (f % 4)) * 4);
+      } else {
+        int64_t mn = mn0 + 2 * (f % (BMN / 2));
+        mn = mn < MN ? mn : MN - 2;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) off[i][j] = (unsigned)(((4 * (f / (BMN / 2)) + j) * ld + (mn - mn0)) * 4);
+      }
+    }
+    step = (KCONTIG ? (int64_t)kX6BK : (int64_t)kX6BK * ld) * 4;
+  }
+  // a k-tile wholly inside [kbeg, kend)
+  __device__ __forceinline__ void load() {
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int j = 0; j < NF; ++j) v[i][j] = *reinterpret_cast<const ld_t*>(base + off[i][j]);
+    base += step;
+  }
+  // the last k-tile, k0 + 16 > kend (k0 = its first k, kend - k0 a multiple
+  // of 4): addresses clamped to the last k-quad (or k-row kend - 1), values
+  // at k >= kend zeroed
+  __device__ __forceinline__ void load_tail(int64_t k0, int64_t kend, int64_t ld) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      if (KCONTIG) {
+        const int64_t k = k0 + 4 * (f % 4);
+        const int64_t back = k < kend ? 0 : (k - (kend - 4)) * 4;
+        const ld_t x = *reinterpret_cast<const ld_t*>(base + off[i][0] - back);
+        v[i][0] = k < kend ? x : ld_t(0);
+      } else {
+        const int64_t kq0 = k0 + 4 * (f / (BMN / 2));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int64_t k = kq0 + j;
+          const int64_t back = k < kend ? 0 : (k - (kend - 1)) * ld * 4;
+          const ld_t x = *reinterpret_cast<const ld_t*>(base + off[i][j] - back);
+          v[i][j] = k < kend ? x : ld_t(0);
+        }
+      }
+    }
+  }
+  // split the registers into the three planes of the LDS tile
+  __device__ __forceinline__ void store(char* __restrict__ lds) const {
+    constexpr int PLANE = BMN * 32;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      if (KCONTIG) {
+        x6_store_quad<PLANE>(lds, f / 4, f % 4, v[i][0][0], v[i][0][1], v[i][0][2], v[i][0][3]);
+      } else {
+        const int r = 2 * (f % (BMN / 2)), kq = f / (BMN / 2);
+        x6_store_quad<PLANE>(lds, r, kq, v[i][0][0], v[i][1][0], v[i][2][0], v[i][3][0]);
+        x6_store_quad<PLANE>(lds, r + 1, kq, v[i][0][1], v[i][1][1], v[i][2][1], v[i][3][1]);
+      }
+    }
+  }
+  // column sums of an n-contiguous B tile: this thread's two columns over its
+  // 4 k-rows, in k order, into the running float64 sums
+  __device__ __forceinline__ void colsum(double (&cs)[2]) const {
+    static_assert(!KCONTIG && NV == 1, "column sums: n-contiguous B, 128 columns");
+    cs[0] += (double)(((v[0][0][0] + v[0][1][0]) + v[0][2][0]) + v[0][3][0]);
+    cs[1] += (double)(((v[0][0][1] + v[0][1][1]) + v[0][2][1]) + v[0][3][1]);
+  }
+};
+
+// Block tile BM x BN = 128 x 128, 4 waves in a 2 x 2 grid of 64 x 64 wave tiles.
+template <int BM, int BN, bool AKC, bool BKC>
+__global__ void __launch_bounds__(256, 3) gemm_x6_kernel(GemmArgs a) {
+  static_assert(BM == 128 && BN == 128, "gemm_x6_kernel: 128 x 128 tiles");
+  using MFT = MF<float>;
+  constexpr int MT = 32, WM = BM / 2, WN = BN / 2, TM = WM / MT, TN = WN / MT;
+  constexpr int A_BYTES = 3 * BM * 32, B_BYTES = 3 * BN * 32, STAGE = A_BYTES + B_BYTES;
+  __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+
+  int tm, tn;
+  tile_coords(a, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int split = blockIdx.y;
+  const int64_t batch = blockIdx.z;
+  const int64_t kbeg = (int64_t)split * a.k_per_split;
+  const int64_t kend = kbeg + a.k_per_split < a.K ? kbeg + a.k_per_split : a.K;
+  const float* A = (const float*)a.A + batch * a.sA;
+  const float* B = (const float*)a.B + batch * a.sB;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane / MT, c = lane % MT;
+  const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+
+  MFT::acc_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = MFT::acc_t(0);
+
+  const int64_t ntiles = kend > kbeg ? (kend - kbeg + kX6BK - 1) / kX6BK : 0;
+  const int64_t nfull = kend > kbeg ? (kend - kbeg) / kX6BK : 0;
+  X6Src<AKC, BM> sa;
+  X6Src<BKC, BN> sb;
+  sa.init(A, a.lda, m0, a.M, kbeg);
+  sb.init(B, a.ldb, n0, a.N, kbeg);
+  bool take_colsum = false;
+  if constexpr (!BKC) take_colsum = a.colsum != nullptr && tm == 0;
+  double cs[2] = {0.0, 0.0};
+  auto store = [&](int stage) {
+    sa.store(lds + stage * STAGE);
+    sb.store(lds + stage * STAGE + A_BYTES);
+    if constexpr (!BKC)
+      if (take_colsum) sb.colsum(cs);
+  };
+  auto load_tail = [&](int64_t kt) {
+    const int64_t k0 = kbeg + kt * kX6BK;
+    sa.load_tail(k0, kend, a.lda);
+    sb.load_tail(k0, kend, a.ldb);
+  };
+  auto compute = [&](int stage) {
+    const char* As = lds + stage * STAGE;
+    const char* Bs = As + A_BYTES;
+    bf16x8_t fa[TM][3], fb[TN][3];
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        fa[i][p] = *reinterpret_cast<const bf16x8_t*>(As + p * (BM * 32) + x6_frag_off(wm0 + i * MT + c, g));
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        fb[j][p] = *reinterpret_cast<const bf16x8_t*>(Bs + p * (BN * 32) + x6_frag_off(wn0 + j * MT + c, g));
+    }
+    // partial products smallest first: (2,0) (1,1) (0,2) (1,0) (0,1) (0,0)
+    constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
+#pragma unroll
+    for (int t = 0; t < 6; ++t)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][PA[t]], fb[j][PB[t]], acc[i][j], 0, 0, 0);
+  };
+  if (ntiles > 0) {
+    if (nfull > 0) {
+      sa.load();
+      sb.load();
+    } else {
+      load_tail(0);
+    }
+    store(0);
+  }
+  __syncthreads();
+  // full k-tiles: the next tile is full too (no bounds work in this loop)
+  int64_t kt = 0;
+  for (; kt + 1 < nfull; ++kt) {
+    sa.load();
+    sb.load();
+    compute((int)(kt & 1));
+    store((int)(kt & 1) ^ 1);
+    __syncthreads();
+  }
+  // the last full tile (its successor, if any, is the partial tail) and the tail
+  for (; kt < ntiles; ++kt) {
+    const bool more = kt + 1 < ntiles;
+    if (more) load_tail(kt + 1);
+    compute((int)(kt & 1));
+    if (more) store((int)(kt & 1) ^ 1);
+    __syncthreads();
+  }
+  if constexpr (!BKC) {
+    if (take_colsum) {
+      // the 4 threads that share a column pair (k-quads 0..3) add in k-quad order
+      double* red = reinterpret_cast<double*>(lds);
+      const int f = threadIdx.x, col = 2 * (f % (BN / 2)), kq = f / (BN / 2);
+      red[kq * BN + col] = cs[0];
+      red[kq * BN + col + 1] = cs[1];
+      __syncthreads();
+      if ((int)threadIdx.x < BN) {
+        const int n = threadIdx.x;
+        const double s = ((red[n] + red[BN + n]) + red[2 * BN + n]) + red[3 * BN + n];
+        finish_colsum<float>(a, s, n0 + n, split);
+      }
+    }
+  }
+  write_acc<float, TM, TN>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
+}
+
 // Sum of the split-K partials in split order 0, 1, ..., S-1, then the
 // epilogue. PLAIN (bias only): VEC consecutive columns per thread.
 template <typename T, bool PLAIN, int VEC>
@@ -837,6 +1110,21 @@ static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb, b
     gemm_kernel<T, BM, BN, AKC, BKC, false, false><<<grid, 256, 0, stream()>>>(a);
 }
 
+static void launch_x6(const GemmArgs& a, dim3 grid, int akc, int bkc) {
+  if (akc && bkc)
+    gemm_x6_kernel<128, 128, true, true><<<grid, 256, 0, stream()>>>(a);
+  else if (akc)
+    gemm_x6_kernel<128, 128, true, false><<<grid, 256, 0, stream()>>>(a);
+  else if (bkc)
+    gemm_x6_kernel<128, 128, false, true><<<grid, 256, 0, stream()>>>(a);
+  else
+    gemm_x6_kernel<128, 128, false, false><<<grid, 256, 0, stream()>>>(a);
+}
+
+// float32 GEMM arithmetic: DTMI_GEMM_MATH_F32 (float32 MFMA) or
+// DTMI_GEMM_MATH_BF16X6 (exact 3-way bf16 split, 6 bf16 MFMA products).
+static int g_gemm_math = DTMI_GEMM_MATH_F32;
+
 template <typename T, int BM, int BN>
 static void launch_layout(const GemmArgs& a, dim3 grid, int akc, int bkc, bool veca, bool vecb, bool dma) {
   if (akc && bkc)
@@ -920,8 +1208,12 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   // The direct-to-LDS kernel addresses a tile with 32-bit byte offsets from
   // its origin: leading dimensions below 2^22 elements keep them in range.
   const bool dma = std::is_same<T, float>::value && veca && vecb && lda < (1 << 22) && ldb < (1 << 22);
+  // split-bf16 products: aligned float32 operands (its column sums need an
+  // n-contiguous B)
+  const bool x6 = std::is_same<T, float>::value && veca && vecb && g_gemm_math == DTMI_GEMM_MATH_BF16X6 &&
+                  !(a.colsum && bkc) && lda < (1 << 22) && ldb < (1 << 22);
   int bm = 128, bn = 128;
-  if (dma) pick_tile(M, N, K, batch, cus, bm, bn);
+  if (dma && !x6) pick_tile(M, N, K, batch, cus, bm, bn);
   const int64_t tmn = cdiv(M, bm) * cdiv(N, bn);
   int splits = force_splits > 0 ? force_splits : choose_splits(tmn, batch, K, cus);
   a.tiles_m = (int)cdiv(M, bm);
@@ -947,7 +1239,9 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   {
     TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
     if constexpr (std::is_same<T, float>::value) {
-      if (bm == 256)
+      if (x6)
+        launch_x6(a, grid, akc, bkc);
+      else if (bm == 256)
         launch_layout<T, 256, 128>(a, grid, akc, bkc, veca, vecb, dma);
       else if (bn == 256)
         launch_layout<T, 128, 256>(a, grid, akc, bkc, veca, vecb, dma);
@@ -1006,6 +1300,23 @@ static int gemm_dispatch(int dtype, int akc, int bkc, int64_t M, int64_t N, int6
 }  // namespace dtmi
 
 using namespace dtmi;
+
+DTMI_EXPORT int dtmi_set_gemm_math(int math) {
+  DTMI_BODY_BEGIN
+  DTMI_CHECK(math == DTMI_GEMM_MATH_F32 || math == DTMI_GEMM_MATH_BF16X6, "dtmi_set_gemm_math: unknown mode %d",
+             math);
+  g_gemm_math = math;
+  return DTMI_OK;
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_get_gemm_math(int* math) {
+  DTMI_BODY_BEGIN
+  DTMI_CHECK(math != nullptr, "dtmi_get_gemm_math: NULL pointer");
+  *math = g_gemm_math;
+  return DTMI_OK;
+  DTMI_BODY_END
+}
 
 DTMI_EXPORT int dtmi_gemm(int dtype, int a_kcontig, int b_kcontig, int64_t M, int64_t N, int64_t K, const void* A,
                           int64_t lda, int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C,

@@ -161,6 +161,40 @@ def timing_read(family: str):
     return n.value, ms.value, work.value
 
 
+GEMM_MATH = {"f32": 0, "bf16x6": 1}
+
+
+def set_gemm_math(mode: str):
+    """Arithmetic of the float32 GEMMs: "f32" (float32 MFMA, the default) or
+    "bf16x6" (each operand split exactly into three bf16 parts, the six
+    largest partial products on the bf16 MFMA, float32 accumulation)."""
+    if mode not in GEMM_MATH:
+        raise ValueError(f"unknown GEMM math {mode!r}; expected one of {sorted(GEMM_MATH)}")
+    call("dtmi_set_gemm_math", GEMM_MATH[mode])
+
+
+def gemm_math() -> str:
+    m = C.c_int()
+    call("dtmi_get_gemm_math", C.byref(m))
+    return {v: k for k, v in GEMM_MATH.items()}[m.value]
+
+
+class use_gemm_math:
+    """with use_gemm_math("bf16x6"): ... -- the previous mode is restored on exit."""
+
+    def __init__(self, mode: str):
+        self.mode = mode
+
+    def __enter__(self):
+        self.prev = gemm_math()
+        set_gemm_math(self.mode)
+        return self
+
+    def __exit__(self, *exc):
+        set_gemm_math(self.prev)
+        return False
+
+
 def memory_stats():
     a, b, c = C.c_size_t(), C.c_size_t(), C.c_size_t()
     call("dtmi_memory_stats", C.byref(a), C.byref(b), C.byref(c))

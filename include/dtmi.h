@@ -237,6 +237,22 @@ int dtmi_gemm(int dtype, int a_kcontig, int b_kcontig, int64_t M, int64_t N, int
               int64_t strideA, const void* B, int64_t ldb, int64_t strideB, void* C, int64_t ldc, int64_t strideC,
               int64_t batch, const void* bias, int accumulate, int splits);
 
+/* Arithmetic of the float32 GEMMs (every dtmi_gemm / dtmi_linear_* call with
+ * DTMI_F32; float64 is unaffected). No dtrain counterpart: dtrain's float32
+ * matmul is NumPy's (dtrain/autograd.py:102-109).
+ *  - DTMI_GEMM_MATH_F32 (default): float32 MFMA (v_mfma_f32_32x32x2_f32).
+ *  - DTMI_GEMM_MATH_BF16X6: each float32 operand split exactly into three
+ *    bf16 parts (a = a0 + a1 + a2, round-to-nearest-even at each step); the
+ *    six partial products a_i b_j with i + j <= 2 run on the bf16 MFMA
+ *    (v_mfma_f32_32x32x16_bf16, exact products, float32 accumulation). The
+ *    dropped terms are below 2^-23 |a b| per product, about one float32
+ *    rounding. Used for 16-byte aligned operands; others take the float32 MFMA.
+ *    Inputs of magnitude above 3.38e38 (bf16 overflow) are out of its range. */
+#define DTMI_GEMM_MATH_F32 0
+#define DTMI_GEMM_MATH_BF16X6 1
+int dtmi_set_gemm_math(int math);
+int dtmi_get_gemm_math(int* math);
+
 /* Linear layer y = x @ w + b (dtrain/nn.py:63-65) with X [M,K], W [K,N]:
  * forward Y = X W + b (bias fused in the epilogue, may be NULL);
  * dX = dY W^T (autograd.py:106); dW = X^T dY (autograd.py:107, the batch sum
