@@ -138,8 +138,10 @@ def main(argv=None):
     ap.add_argument("--dtype", default="float32", choices=["float32", "float64"],
                     help="compute dtype of the microbenchmarks (the gpt2 step is float32)")
     ap.add_argument("--gemm-math", default="f32", choices=["f32", "bf16x6"],
-                    help="arithmetic of the float32 GEMMs: float32 MFMA, or operands split exactly into three "
-                         "bf16 parts with the six largest partial products on the bf16 MFMA")
+                    help="arithmetic of the float32 GEMMs for the headline value: float32 MFMA, or operands split "
+                         "exactly into three bf16 parts with the six largest partial products on the bf16 MFMA")
+    ap.add_argument("--no-alt-gemm-math", action="store_true",
+                    help="skip timing the same step with the other GEMM arithmetic")
     a = ap.parse_args(argv)
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the data-parallel exchange is simulated on-device over {WORLD} replicas "
@@ -172,17 +174,40 @@ def main(argv=None):
     for i in range(a.warmup):
         res = S.step_ddp(model, ddp, opt, batches, clip=CLIP)
         print(f"[bench] warmup step {i + 1}/{a.warmup} loss {res.loss:.4f}", file=sys.stderr, flush=True)
-    _lib.sync()
-    _lib.timing_enable(True)
-    t0 = time.perf_counter()
-    for _ in range(a.steps):
-        res = S.step_ddp(model, ddp, opt, batches, clip=CLIP)
-    _lib.sync()
-    dt = time.perf_counter() - t0
-    fams = {f: _lib.timing_read(f) for f in _lib.FAM}
-    _lib.timing_enable(False)
+
+    def timed():
+        _lib.sync()
+        _lib.timing_enable(True)
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            r = S.step_ddp(model, ddp, opt, batches, clip=CLIP)
+        _lib.sync()
+        el = time.perf_counter() - t0
+        fm = {f: _lib.timing_read(f) for f in _lib.FAM}
+        _lib.timing_enable(False)
+        return el, fm, r
+
+    dt, fams, res = timed()
     loss = res.loss
-    print(f"[bench] {a.steps} steps in {dt:.3f} s, loss {loss:.4f}", file=sys.stderr, flush=True)
+    print(f"[bench] {a.steps} steps in {dt:.3f} s, loss {loss:.4f} (GEMM math {a.gemm_math})", file=sys.stderr,
+          flush=True)
+    alt = None
+    if not a.no_alt_gemm_math:
+        # the same step with the other GEMM arithmetic, continuing the same run
+        other = "bf16x6" if a.gemm_math == "f32" else "f32"
+        _lib.set_gemm_math(other)
+        S.step_ddp(model, ddp, opt, batches, clip=CLIP)  # one untimed step in the new mode
+        adt, afams, ares = timed()
+        _lib.set_gemm_math(a.gemm_math)
+        an, ams, awork = afams["gemm"]
+        ag = awork / (ams * 1e-3) / 1e12 if ams else 0.0
+        print(f"[bench] {a.steps} steps in {adt:.3f} s, loss {ares.loss:.4f} (GEMM math {other})", file=sys.stderr,
+              flush=True)
+        alt = {"gemm_math": other, "value": round(WORLD * BATCH * CFG["ctx"] / (adt / a.steps), 1),
+               "unit": "tokens/s", "ms_per_step": round(1e3 * adt / a.steps, 3), "loss": round(ares.loss, 5),
+               "gemm_ms_per_step": round(ams / a.steps, 3), "gemm_fp32_equivalent_TFLOP/s": round(ag, 2)}
+        if other == "bf16x6":
+            alt["gemm_mfma_frac_of_bf16_peak"] = round(6 * ag * 1e12 / PEAK_BF16_MFMA, 4)
 
     tokens = WORLD * BATCH * CFG["ctx"]
     ms_step = 1e3 * dt / a.steps
@@ -225,7 +250,12 @@ def main(argv=None):
                                    "buckets, fixed-order average, clip 1.0, AdamW"),
                       "global_batch": WORLD * BATCH, "seq_len": CFG["ctx"], "parallelism": "dp4-simulated",
                       "params": sum(int(np.prod(s)) for _, s in param_spec(CFG))},
-           "roofline": roofline, "kernels": kernels, "loss": round(loss, 5), "gemm_math": a.gemm_math}
+           "roofline": roofline, "kernels": kernels, "loss": round(loss, 5), "gemm_math": a.gemm_math,
+           "gemm_math_note": ("f32: float32 MFMA (v_mfma_f32_32x32x2_f32). bf16x6: each float32 operand split "
+                              "exactly into three bf16 parts, the six partial products a_i*b_j with i+j<=2 on the "
+                              "bf16 MFMA (exact products, float32 accumulation; dropped terms < 2^-23 |ab|); both "
+                              "pass the same float32 parity bar (rel err <= 1e-5 vs the float64 oracle)"),
+           "alt_gemm_math": alt}
     if not a.no_cpu_baseline:
         print("[bench] CPU baseline (oracle) ...", file=sys.stderr, flush=True)
         out["cpu_baseline"] = cpu_baseline(weights, xs, ys, a.cpu_seq)

@@ -297,9 +297,8 @@ __device__ __forceinline__ typename MF<T>::vec_t read_frag(const T* __restrict__
   return v;
 }
 
-__device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords_of(const GemmArgs& a, int t, int& tm, int& tn) {
   const int nt = a.tiles_m * a.tiles_n;
-  int t = blockIdx.x;
   if ((nt & 7) == 0) t = (t & 7) * (nt >> 3) + (t >> 3);  // contiguous tile range per XCD
   constexpr int GROUP = 8;
   const int per_group = GROUP * a.tiles_n;
@@ -309,6 +308,9 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn)
   const int r = t - group * per_group;
   tm = first_m + r % gsz;
   tn = r / gsz;
+}
+__device__ __forceinline__ void tile_coords(const GemmArgs& a, int& tm, int& tn) {
+  tile_coords_of(a, (int)blockIdx.x, tm, tn);
 }
 
 // The column sum of one B column over this block's k range: to colsum (or
@@ -770,8 +772,8 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
 // vectors along m/n for m/n-contiguous operands, 4 k-rows at a time) ->
 // split (v_cvt_pk_bf16_f32, two values per instruction) -> LDS as three bf16
 // planes per operand, each [row][16 k] with the two 16-byte k-halves of a row
-// swapped on every other group of 8 rows, so the MFMA fragment reads
-// (ds_read_b128: lane (g, c) reads row c, k 8g..8g+7) hit distinct banks.
+// swapped by a row swizzle, so the MFMA fragment reads (ds_read_b128: lane
+// (g, c) reads row c, k 8g..8g+7) hit distinct banks.
 // k-tile 16 (one MFMA k-step), two LDS stages, one barrier per k-tile.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -794,12 +796,17 @@ __device__ __forceinline__ void split3(float x, float y, unsigned& p0, unsigned&
   p2 = cvt_pk_bf16(rx - __uint_as_float(p1 << 16), ry - __uint_as_float(p1 & 0xffff0000u));
 }
 
+// The two 16-byte k-halves of a plane row are swapped when bit 2 xor bit 3
+// of the row is set: 8 consecutive rows (and 16) then cover distinct 16-byte
+// bank groups, so 16-byte accesses by consecutive rows are conflict-free
+// whether the LDS serves them 8 or 16 lanes at a time.
+__device__ __forceinline__ int x6_swz(int row) { return ((row >> 2) ^ (row >> 3)) & 1; }
 // byte offset of k-quad kq (k = 4kq..4kq+3) of `row` in one bf16 plane
 __device__ __forceinline__ int x6_quad_off(int row, int kq) {
-  return row * 32 + 16 * ((kq >> 1) ^ ((row >> 3) & 1)) + 8 * (kq & 1);
+  return row * 32 + 16 * ((kq >> 1) ^ x6_swz(row)) + 8 * (kq & 1);
 }
 // byte offset of lane group g's 8 k-values (k = 8g..8g+7) of `row`
-__device__ __forceinline__ int x6_frag_off(int row, int g) { return row * 32 + 16 * (g ^ ((row >> 3) & 1)); }
+__device__ __forceinline__ int x6_frag_off(int row, int g) { return row * 32 + 16 * (g ^ x6_swz(row)); }
 
 // Splits the 4 consecutive-k values v of `row` (k-quad kq) into the 3 planes.
 template <int PLANE>
@@ -815,39 +822,62 @@ __device__ __forceinline__ void x6_store_quad(char* __restrict__ lds, int row, i
   *reinterpret_cast<u2*>(lds + 2 * PLANE + o) = u2{a2, b2};
 }
 
+// Splits the 8 consecutive-k values x of `row` (k-half h: k = 8h..8h+7) into
+// the 3 planes: one 16-byte store per plane.
+template <int PLANE>
+__device__ __forceinline__ void x6_store_oct(char* __restrict__ lds, int row, int h, const float (&x)[8]) {
+  typedef unsigned u4 __attribute__((ext_vector_type(4)));
+  u4 p0, p1, p2;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    unsigned a0, a1, a2;
+    split3(x[2 * e], x[2 * e + 1], a0, a1, a2);
+    p0[e] = a0;
+    p1[e] = a1;
+    p2[e] = a2;
+  }
+  const int o = x6_frag_off(row, h);
+  *reinterpret_cast<u4*>(lds + o) = p0;
+  *reinterpret_cast<u4*>(lds + PLANE + o) = p1;
+  *reinterpret_cast<u4*>(lds + 2 * PLANE + o) = p2;
+}
+
 // One operand's BMN x 16 float32 tile. KCONTIG: NV = BMN/64 16-byte vectors
-// per thread (row f/4, k-quad f%4). Otherwise NV = BMN/128 groups per thread
-// of 4 k-rows x 2 adjacent columns (8-byte vectors; columns 2*(f % (BMN/2)),
-// k-quad f / (BMN/2)). Addresses are a wave-uniform base (advanced one k-tile
-// per load, in scalar registers) plus per-thread 32-bit byte offsets fixed for
-// the whole k loop; rows or columns past the matrix edge are clamped onto the
-// last ones (they feed only outputs that are never stored). The host keeps
-// every offset below 2^32 (leading dimension < 2^22 elements).
+// per thread (row f/4, k-quad f%4). Otherwise NV = BMN/128 slots per thread of
+// one column (f % BMN) x 8 k-rows (k-half f / BMN), 4-byte loads (a wave
+// reads 64 consecutive columns of a k-row) and one 16-byte LDS store per
+// plane (a wave writes 64 consecutive rows: conflict-free). Addresses are a
+// wave-uniform base (advanced one k-tile per load, in scalar registers) plus
+// per-thread 32-bit byte offsets fixed for the whole k loop; rows or columns
+// past the matrix edge are clamped onto the last ones (they feed only
+// outputs that are never stored). The host keeps every offset below 2^32
+// (leading dimension < 2^22 elements).
 template <bool KCONTIG, int BMN>
 struct X6Src {
   static constexpr int NV = KCONTIG ? BMN / 64 : BMN / 128;
-  static constexpr int NF = KCONTIG ? 1 : 4;  // loads per vector slot
-  typedef typename std::conditional<KCONTIG, MF<float>::vec_t, f32x2_t>::type ld_t;
+  static constexpr int NF = KCONTIG ? 1 : 8;  // loads per vector slot
+  typedef typename std::conditional<KCONTIG, MF<float>::vec_t, float>::type ld_t;
   const char* base;
-  unsigned off[NV][NF];
+  unsigned off[NV];
+  int64_t ldb;   // bytes between k-rows (n-contiguous operands)
   int64_t step;  // bytes per k-tile
   ld_t v[NV][NF];
 
   __device__ __forceinline__ void init(const float* __restrict__ P, int64_t ld, int64_t mn0, int64_t MN,
                                        int64_t kbeg) {
     base = reinterpret_cast<const char*>(KCONTIG ? P + mn0 * ld + kbeg : P + kbeg * ld + mn0);
+    ldb = ld * 4;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int f = threadIdx.x + 256 * i;
-      if (KCONTIG) {
+      if constexpr (KCONTIG) {
         int64_t mn = mn0 + f / 4;
         mn = mn < MN ? mn : MN - 1;
-        off[i][0] = (unsigned)(((mn - mn0) * ld + 4 * (f % 4)) * 4);
+        off[i] = (unsigned)(((mn - mn0) * ld + 4 * (f % 4)) * 4);
       } else {
-        int64_t mn = mn0 + 2 * (f % (BMN / 2));
-        mn = mn < MN ? mn : MN - 2;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) off[i][j] = (unsigned)(((4 * (f / (BMN / 2)) + j) * ld + (mn - mn0)) * 4);
+        int64_t mn = mn0 + f % BMN;
+        mn = mn < MN ? mn : MN - 1;
+        off[i] = (unsigned)((8 * (f / BMN) * ld + (mn - mn0)) * 4);
       }
     }
     step = (KCONTIG ? (int64_t)kX6BK : (int64_t)kX6BK * ld) * 4;
@@ -857,28 +887,29 @@ struct X6Src {
 #pragma unroll
     for (int i = 0; i < NV; ++i)
 #pragma unroll
-      for (int j = 0; j < NF; ++j) v[i][j] = *reinterpret_cast<const ld_t*>(base + off[i][j]);
+      for (int j = 0; j < NF; ++j) v[i][j] = *reinterpret_cast<const ld_t*>(base + j * ldb + off[i]);
     base += step;
   }
   // the last k-tile, k0 + 16 > kend (k0 = its first k, kend - k0 a multiple
   // of 4): addresses clamped to the last k-quad (or k-row kend - 1), values
   // at k >= kend zeroed
-  __device__ __forceinline__ void load_tail(int64_t k0, int64_t kend, int64_t ld) {
+  __device__ __forceinline__ void load_tail(int64_t k0, int64_t kend) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int f = threadIdx.x + 256 * i;
-      if (KCONTIG) {
+      if constexpr (KCONTIG) {
         const int64_t k = k0 + 4 * (f % 4);
         const int64_t back = k < kend ? 0 : (k - (kend - 4)) * 4;
-        const ld_t x = *reinterpret_cast<const ld_t*>(base + off[i][0] - back);
+        const ld_t x = *reinterpret_cast<const ld_t*>(base + off[i] - back);
         v[i][0] = k < kend ? x : ld_t(0);
       } else {
-        const int64_t kq0 = k0 + 4 * (f / (BMN / 2));
+        const int h = f / BMN;
+        const int64_t col_off = (int64_t)off[i] - 8 * h * ldb;  // the column's byte offset in a k-row
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int64_t k = kq0 + j;
-          const int64_t back = k < kend ? 0 : (k - (kend - 1)) * ld * 4;
-          const ld_t x = *reinterpret_cast<const ld_t*>(base + off[i][j] - back);
+        for (int j = 0; j < 8; ++j) {
+          const int64_t k = k0 + 8 * h + j;
+          const int64_t kr = (k < kend ? k : kend - 1) - k0;  // k-row within the tile, clamped
+          const ld_t x = *reinterpret_cast<const ld_t*>(base + kr * ldb + col_off);
           v[i][j] = k < kend ? x : ld_t(0);
         }
       }
@@ -890,21 +921,24 @@ struct X6Src {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int f = threadIdx.x + 256 * i;
-      if (KCONTIG) {
+      if constexpr (KCONTIG) {
         x6_store_quad<PLANE>(lds, f / 4, f % 4, v[i][0][0], v[i][0][1], v[i][0][2], v[i][0][3]);
       } else {
-        const int r = 2 * (f % (BMN / 2)), kq = f / (BMN / 2);
-        x6_store_quad<PLANE>(lds, r, kq, v[i][0][0], v[i][1][0], v[i][2][0], v[i][3][0]);
-        x6_store_quad<PLANE>(lds, r + 1, kq, v[i][0][1], v[i][1][1], v[i][2][1], v[i][3][1]);
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = v[i][j];
+        x6_store_oct<PLANE>(lds, f % BMN, f / BMN, x);
       }
     }
   }
-  // column sums of an n-contiguous B tile: this thread's two columns over its
-  // 4 k-rows, in k order, into the running float64 sums
-  __device__ __forceinline__ void colsum(double (&cs)[2]) const {
+  // column sums of an n-contiguous B tile: this thread's column over its 8
+  // k-rows, in k order, into the running float64 sum
+  __device__ __forceinline__ void colsum(double& cs) const {
     static_assert(!KCONTIG && NV == 1, "column sums: n-contiguous B, 128 columns");
-    cs[0] += (double)(((v[0][0][0] + v[0][1][0]) + v[0][2][0]) + v[0][3][0]);
-    cs[1] += (double)(((v[0][0][1] + v[0][1][1]) + v[0][2][1]) + v[0][3][1]);
+    float t = v[0][0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) t = t + v[0][j];
+    cs += (double)t;
   }
 };
 
@@ -945,7 +979,7 @@ __global__ void __launch_bounds__(256, 3) gemm_x6_kernel(GemmArgs a) {
   sb.init(B, a.ldb, n0, a.N, kbeg);
   bool take_colsum = false;
   if constexpr (!BKC) take_colsum = a.colsum != nullptr && tm == 0;
-  double cs[2] = {0.0, 0.0};
+  double cs = 0.0;
   auto store = [&](int stage) {
     sa.store(lds + stage * STAGE);
     sb.store(lds + stage * STAGE + A_BYTES);
@@ -954,8 +988,8 @@ __global__ void __launch_bounds__(256, 3) gemm_x6_kernel(GemmArgs a) {
   };
   auto load_tail = [&](int64_t kt) {
     const int64_t k0 = kbeg + kt * kX6BK;
-    sa.load_tail(k0, kend, a.lda);
-    sb.load_tail(k0, kend, a.ldb);
+    sa.load_tail(k0, kend);
+    sb.load_tail(k0, kend);
   };
   auto compute = [&](int stage) {
     const char* As = lds + stage * STAGE;
@@ -1009,16 +1043,13 @@ __global__ void __launch_bounds__(256, 3) gemm_x6_kernel(GemmArgs a) {
   }
   if constexpr (!BKC) {
     if (take_colsum) {
-      // the 4 threads that share a column pair (k-quads 0..3) add in k-quad order
+      // the 2 threads of a column (k-halves 0, 1) add in k order
       double* red = reinterpret_cast<double*>(lds);
-      const int f = threadIdx.x, col = 2 * (f % (BN / 2)), kq = f / (BN / 2);
-      red[kq * BN + col] = cs[0];
-      red[kq * BN + col + 1] = cs[1];
+      red[threadIdx.x] = cs;
       __syncthreads();
       if ((int)threadIdx.x < BN) {
         const int n = threadIdx.x;
-        const double s = ((red[n] + red[BN + n]) + red[2 * BN + n]) + red[3 * BN + n];
-        finish_colsum<float>(a, s, n0 + n, split);
+        finish_colsum<float>(a, red[n] + red[BN + n], n0 + n, split);
       }
     }
   }
