@@ -116,7 +116,7 @@ __global__ void __launch_bounds__(256) ln_fwd_kernel(T* __restrict__ y, T* __res
 static int ln_bwd_blocks(int64_t rows) {
   int64_t b = cdiv(rows, 4 * 2);  // two rows per wave
   if (b < 1) b = 1;
-  return (int)(b < 1024 ? b : 1024);
+  return (int)(b < 512 ? b : 512);
 }
 
 template <typename T, int NV, int VW>
