@@ -193,21 +193,26 @@ def main(argv=None):
           flush=True)
     alt = None
     if not a.no_alt_gemm_math:
-        # the same step with the other GEMM arithmetic, continuing the same run
+        # the same step with the other GEMM arithmetic, continuing the same run;
+        # a library error here is reported in the line instead of losing it
         other = "bf16x6" if a.gemm_math == "f32" else "f32"
-        _lib.set_gemm_math(other)
-        S.step_ddp(model, ddp, opt, batches, clip=CLIP)  # one untimed step in the new mode
-        adt, afams, ares = timed()
-        _lib.set_gemm_math(a.gemm_math)
-        an, ams, awork = afams["gemm"]
-        ag = awork / (ams * 1e-3) / 1e12 if ams else 0.0
-        print(f"[bench] {a.steps} steps in {adt:.3f} s, loss {ares.loss:.4f} (GEMM math {other})", file=sys.stderr,
-              flush=True)
-        alt = {"gemm_math": other, "value": round(WORLD * BATCH * CFG["ctx"] / (adt / a.steps), 1),
-               "unit": "tokens/s", "ms_per_step": round(1e3 * adt / a.steps, 3), "loss": round(ares.loss, 5),
-               "gemm_ms_per_step": round(ams / a.steps, 3), "gemm_fp32_equivalent_TFLOP/s": round(ag, 2)}
-        if other == "bf16x6":
-            alt["gemm_mfma_frac_of_bf16_peak"] = round(6 * ag * 1e12 / PEAK_BF16_MFMA, 4)
+        try:
+            _lib.set_gemm_math(other)
+            S.step_ddp(model, ddp, opt, batches, clip=CLIP)  # one untimed step in the new mode
+            adt, afams, ares = timed()
+            an, ams, awork = afams["gemm"]
+            ag = awork / (ams * 1e-3) / 1e12 if ams else 0.0
+            print(f"[bench] {a.steps} steps in {adt:.3f} s, loss {ares.loss:.4f} (GEMM math {other})",
+                  file=sys.stderr, flush=True)
+            alt = {"gemm_math": other, "value": round(WORLD * BATCH * CFG["ctx"] / (adt / a.steps), 1),
+                   "unit": "tokens/s", "ms_per_step": round(1e3 * adt / a.steps, 3), "loss": round(ares.loss, 5),
+                   "gemm_ms_per_step": round(ams / a.steps, 3), "gemm_fp32_equivalent_TFLOP/s": round(ag, 2)}
+            if other == "bf16x6":
+                alt["gemm_mfma_frac_of_bf16_peak"] = round(6 * ag * 1e12 / PEAK_BF16_MFMA, 4)
+        except RuntimeError as e:
+            alt = {"gemm_math": other, "error": str(e)}
+        finally:
+            _lib.set_gemm_math(a.gemm_math)
 
     tokens = WORLD * BATCH * CFG["ctx"]
     ms_step = 1e3 * dt / a.steps

@@ -21,6 +21,10 @@
 //     stages, in swizzled layouts that keep the fragment reads conflict-free.
 //   gemm_kernel (float64, and float32 with unaligned operands): registers ->
 //     LDS, double-buffered.
+//   gemm_x6_kernel (float32 when dtmi_set_gemm_math selects the split-bf16
+//     arithmetic, aligned operands): each operand split exactly into three
+//     bf16 parts on the way into LDS, six partial products on the bf16 MFMA
+//     (its own section below).
 // (256x128 and 128x256 tiles, 32-wide k-tiles, a two-tile register prefetch
 // and AGPR accumulators measured no faster on the GPT-2 shapes.)
 //
