@@ -175,22 +175,27 @@ def main(argv=None):
         res = S.step_ddp(model, ddp, opt, batches, clip=CLIP)
         print(f"[bench] warmup step {i + 1}/{a.warmup} loss {res.loss:.4f}", file=sys.stderr, flush=True)
 
-    def timed():
+    def timed(events):
+        """K steps between barriers; with events, the library also brackets
+        every kernel launch with HIP events on its stream (per-family time)."""
         _lib.sync()
-        _lib.timing_enable(True)
+        _lib.timing_enable(events)
         t0 = time.perf_counter()
         for _ in range(a.steps):
             r = S.step_ddp(model, ddp, opt, batches, clip=CLIP)
         _lib.sync()
         el = time.perf_counter() - t0
-        fm = {f: _lib.timing_read(f) for f in _lib.FAM}
+        fm = {f: _lib.timing_read(f) for f in _lib.FAM} if events else None
         _lib.timing_enable(False)
         return el, fm, r
 
-    dt, fams, res = timed()
+    # value / ms_per_step: K uninstrumented steps; roofline / kernels: the next
+    # K steps with per-launch HIP events (which add ~10 us between launches)
+    dt, _, res = timed(False)
+    dt_ev, fams, res_ev = timed(True)
     loss = res.loss
-    print(f"[bench] {a.steps} steps in {dt:.3f} s, loss {loss:.4f} (GEMM math {a.gemm_math})", file=sys.stderr,
-          flush=True)
+    print(f"[bench] {a.steps} steps in {dt:.3f} s, loss {loss:.4f} (GEMM math {a.gemm_math}); {a.steps} more with "
+          f"per-launch events in {dt_ev:.3f} s", file=sys.stderr, flush=True)
     alt = None
     if not a.no_alt_gemm_math:
         # the same step with the other GEMM arithmetic, continuing the same run;
@@ -199,7 +204,8 @@ def main(argv=None):
         try:
             _lib.set_gemm_math(other)
             S.step_ddp(model, ddp, opt, batches, clip=CLIP)  # one untimed step in the new mode
-            adt, afams, ares = timed()
+            adt, _, ares = timed(False)
+            _, afams, _ = timed(True)
             an, ams, awork = afams["gemm"]
             ag = awork / (ams * 1e-3) / 1e12 if ams else 0.0
             print(f"[bench] {a.steps} steps in {adt:.3f} s, loss {ares.loss:.4f} (GEMM math {other})",
@@ -238,7 +244,7 @@ def main(argv=None):
     for f, (cnt, fms, fwork) in fams.items():
         if not cnt:
             continue
-        entry = {"launches": cnt, "ms_per_step": round(fms / a.steps, 3)}
+        entry = {"launches": cnt, "ms_per_step": round(fms / a.steps, 3)}  # from the evented steps
         if f in ("gemm", "attn_fwd", "attn_bwd"):
             entry["TFLOP/s"] = round(fwork / (fms * 1e-3) / 1e12, 2)
         else:
@@ -256,6 +262,9 @@ def main(argv=None):
                       "global_batch": WORLD * BATCH, "seq_len": CFG["ctx"], "parallelism": "dp4-simulated",
                       "params": sum(int(np.prod(s)) for _, s in param_spec(CFG))},
            "roofline": roofline, "kernels": kernels, "loss": round(loss, 5), "gemm_math": a.gemm_math,
+           "timing_note": (f"value and ms_per_step: {a.steps} steps with no instrumentation; roofline and kernels: "
+                           f"the next {a.steps} steps with HIP events around every launch "
+                           f"({1e3 * dt_ev / a.steps:.1f} ms per step with the events)"),
            "gemm_math_note": ("f32: float32 MFMA (v_mfma_f32_32x32x2_f32). bf16x6: each float32 operand split "
                               "exactly into three bf16 parts, the six partial products a_i*b_j with i+j<=2 on the "
                               "bf16 MFMA (exact products, float32 accumulation; dropped terms < 2^-23 |ab|); both "
@@ -286,16 +295,21 @@ def _threads():
 
 
 def _timed(a, fn, families):
+    """Wall time of `steps` uninstrumented calls, then per-family kernel time
+    from `steps` more calls with HIP events around every launch."""
     from dtmi import _lib
     for _ in range(a.warmup):
         fn()
     _lib.sync()
-    _lib.timing_enable(True)
     t0 = time.perf_counter()
     for _ in range(a.steps):
         fn()
     _lib.sync()
     dt = time.perf_counter() - t0
+    _lib.timing_enable(True)
+    for _ in range(a.steps):
+        fn()
+    _lib.sync()
     fams = {f: _lib.timing_read(f) for f in families}
     _lib.timing_enable(False)
     return dt, fams
