@@ -203,7 +203,8 @@ def main(argv=None):
         other = "bf16x6" if a.gemm_math == "f32" else "f32"
         try:
             _lib.set_gemm_math(other)
-            S.step_ddp(model, ddp, opt, batches, clip=CLIP)  # one untimed step in the new mode
+            for _ in range(max(a.warmup, 1)):  # untimed steps in the new mode, as for the first
+                S.step_ddp(model, ddp, opt, batches, clip=CLIP)
             adt, _, ares = timed(False)
             _, afams, _ = timed(True)
             an, ams, awork = afams["gemm"]
