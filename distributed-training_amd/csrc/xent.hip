@@ -150,6 +150,88 @@ __global__ void __launch_bounds__(256) xent_bwd_kernel(T* __restrict__ dz, const
   }
 }
 
+// Forward and gradient in one pass (float32, rows of up to 65536 logits):
+// one 1024-thread block per row holds the row in registers (NV 16-byte
+// vectors per thread), so the logits are read once and dlogits written once
+// (the two-kernel form reads them twice). dlogits = (exp(z - max) / sum -
+// onehot) * (1 / n): the gradient for an upstream gradient of 1, which
+// xent_grad_scale_kernel rescales in place when the upstream gradient is not
+// 1. Max and sum are combined in a fixed order: a butterfly per wave, then
+// the 16 wave results in wave order.
+template <int NV>
+__global__ void __launch_bounds__(1024) xent_fused_kernel(float* __restrict__ dz, float* __restrict__ rowmax,
+                                                           float* __restrict__ rowsum, float* __restrict__ logp_t,
+                                                           const float* __restrict__ z,
+                                                           const int64_t* __restrict__ targets, int64_t V,
+                                                           float inv_n) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const f4* zr = reinterpret_cast<const f4*>(z + row * V);
+  f4* dr = reinterpret_cast<f4*>(dz + row * V);
+  const int nv = (int)(V / 4);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  f4 v[NV];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = tid + 1024 * j;
+    v[j] = i < nv ? zr[i] : f4(-INFINITY);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m = fmaxf(m, v[j][e]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  float M = red[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+  float sl = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sl += (tid + 1024 * j < nv) ? expf(v[j][e] - M) : 0.f;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sl += __shfl_xor(sl, off, 64);
+  if (lane == 0) red[wave] = sl;
+  __syncthreads();
+  float S = red[0];
+#pragma unroll
+  for (int w = 1; w < 16; ++w) S += red[w];
+  const int64_t t = targets[row];
+  if (tid == 0) {
+    rowmax[row] = M;
+    rowsum[row] = S;
+    // (z - zmax) - log(s), dtrain/autograd.py:255
+    logp_t[row] = (t >= 0 && t < V) ? (z[row * V + t] - M) - logf(S) : NAN;
+  }
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = tid + 1024 * j;
+    if (i < nv) {
+      f4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float p = expf(v[j][e] - M) / S;
+        if ((int64_t)(4 * i + e) == t) p = p - 1.f;
+        o[e] = p * inv_n;
+      }
+      dr[i] = o;
+    }
+  }
+}
+
+// x *= g[0] unless g[0] == 1 (then x is already the gradient).
+template <typename T>
+__global__ void __launch_bounds__(256) xent_grad_scale_kernel(T* __restrict__ x, const T* __restrict__ g, int64_t n) {
+  const T gv = *g;
+  if (gv == T(1)) return;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] = x[i] * gv;
+}
+
 // dS = P * (dP - rowsum(dP * P)); one wave per row.
 template <typename T>
 __global__ void __launch_bounds__(256) softmax_bwd_kernel(T* __restrict__ ds, const T* __restrict__ p,
@@ -223,6 +305,71 @@ DTMI_EXPORT int dtmi_xent_bwd(int dtype, void* dlogits, const void* logits, cons
         (double*)dlogits, (const double*)logits, (const double*)rowmax, (const double*)rowsum, targets,
         (const double*)g_dev, g_host, rows, vocab, vec ? 1 : 0);
   LAUNCH_CHECK("xent_bwd_kernel");
+  return DTMI_OK;
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_xent_fused(int dtype, void* loss, void* dlogits, void* rowmax, void* rowsum, const void* logits,
+                                const int64_t* targets, int64_t rows, int64_t vocab) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(rows > 0 && vocab > 0 && rows < (1LL << 31), "dtmi_xent_fused: bad shape [%lld, %lld]",
+             (long long)rows, (long long)vocab);
+  DTMI_CHECK(loss && dlogits && rowmax && rowsum && logits && targets, "dtmi_xent_fused: NULL pointer");
+  const int64_t nv = vocab / 4;
+  const bool fused = dtype == DTMI_F32 && vocab % 4 == 0 && nv <= 16 * 1024 && aligned(logits, 16) &&
+                     aligned(dlogits, 16);
+  if (!fused) {  // the two-kernel form: forward, then the gradient for an upstream gradient of 1
+    int rc = dtmi_xent_fwd(dtype, loss, rowmax, rowsum, logits, targets, rows, vocab);
+    if (rc) return rc;
+    return dtmi_xent_bwd(dtype, dlogits, logits, rowmax, rowsum, targets, nullptr, 1.0, rows, vocab);
+  }
+  float* logp = nullptr;
+  int rc = pool_alloc((void**)&logp, (size_t)rows * sizeof(float));
+  if (rc) return rc;
+  {
+    TimedLaunch tl(DTMI_FAM_XENT, 2.0 * (double)rows * vocab * 4);
+    const float inv_n = 1.f / (float)rows;
+    auto go = [&](auto nvc) {
+      constexpr int NV = decltype(nvc)::value;
+      xent_fused_kernel<NV><<<(unsigned)rows, 1024, 0, stream()>>>((float*)dlogits, (float*)rowmax, (float*)rowsum,
+                                                                   logp, (const float*)logits, targets, vocab, inv_n);
+    };
+    const int need = (int)cdiv(nv, 1024);
+    if (need <= 1)
+      go(std::integral_constant<int, 1>());
+    else if (need <= 2)
+      go(std::integral_constant<int, 2>());
+    else if (need <= 4)
+      go(std::integral_constant<int, 4>());
+    else if (need <= 8)
+      go(std::integral_constant<int, 8>());
+    else if (need <= 13)
+      go(std::integral_constant<int, 13>());
+    else
+      go(std::integral_constant<int, 16>());
+    xent_loss_kernel<float><<<1, 256, 0, stream()>>>((float*)loss, logp, rows);
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(logp);
+  if (le != hipSuccess) return fail_hip(le, "xent_fused kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_xent_grad_scale(int dtype, void* dlogits, const void* g_dev, int64_t n) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(dlogits && g_dev && n >= 0, "dtmi_xent_grad_scale: bad arguments");
+  if (n == 0) return DTMI_OK;
+  const int grid = (int)(cdiv(n, 256 * 8) < 4096 ? cdiv(n, 256 * 8) : 4096);
+  if (dtype == DTMI_F32)
+    xent_grad_scale_kernel<float><<<grid, 256, 0, stream()>>>((float*)dlogits, (const float*)g_dev, n);
+  else
+    xent_grad_scale_kernel<double><<<grid, 256, 0, stream()>>>((double*)dlogits, (const double*)g_dev, n);
+  LAUNCH_CHECK("xent_grad_scale_kernel");
   return DTMI_OK;
   DTMI_BODY_END
 }

@@ -63,6 +63,8 @@ SIGNATURES: dict[str, list] = {
     "dtmi_layernorm_bwd": [i32, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
     "dtmi_xent_fwd": [i32, vp, vp, vp, vp, vp, i64, i64],
     "dtmi_xent_bwd": [i32, vp, vp, vp, vp, vp, vp, f64, i64, i64],
+    "dtmi_xent_fused": [i32, vp, vp, vp, vp, vp, vp, i64, i64],
+    "dtmi_xent_grad_scale": [i32, vp, vp, i64],
     "dtmi_softmax_bwd": [i32, vp, vp, vp, i64, i64],
     "dtmi_embedding_fwd": [i32, vp, vp, vp, i64, i64, i64],
     "dtmi_embedding_bwd": [i32, vp, vp, vp, vp, vp, i32, i64, i64, i32],

@@ -367,8 +367,19 @@ def cross_entropy(logits: Tensor, targets) -> Tensor:
     V = z.shape[-1]
     t = as_indices(targets)
     t.check(V, "target", allow_negative=False)
-    loss, rmax, rsum = K.xent_fwd(z, t.dev)
+    if not (_grad_enabled and logits.requires_grad):
+        loss, rmax, rsum = K.xent_fwd(z, t.dev)
+        return Tensor._make(loss, (logits,), None)
+    # training: the gradient for an upstream gradient of 1 comes out of the
+    # forward pass (one read of the logits); the backward rescales it in place
+    # when the upstream gradient differs, and a second backward through this
+    # node recomputes it from the logits and the saved row statistics
+    loss, rmax, rsum, dz = K.xent_fused(z, t.dev)
+    pending = [dz]
 
     def bw(g):
-        return (K.xent_bwd(z, t.dev, rmax, rsum, g=_contig(g).reshape(1)),)
+        g1 = _contig(g).reshape(1)
+        if pending:
+            return (K.xent_grad_scale(pending.pop(), g1),)
+        return (K.xent_bwd(z, t.dev, rmax, rsum, g=g1),)
     return Tensor._make(loss, (logits,), bw)

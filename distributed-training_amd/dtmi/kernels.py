@@ -327,6 +327,32 @@ def xent_bwd(logits: DeviceArray, targets: DeviceArray, rmax: DeviceArray, rsum:
     return dz
 
 
+def xent_fused(logits: DeviceArray, targets: DeviceArray):
+    """Forward plus the gradient for an upstream gradient of 1, in one pass
+    over the logits where the shape allows. Returns (loss, rowmax, rowsum,
+    dlogits)."""
+    _contig(logits, targets)
+    V = logits.shape[-1]
+    rows = logits.size // V
+    if targets.dtype != np.int64 or targets.size != rows:
+        raise ValueError("xent: targets must be int64 with one entry per row")
+    loss = empty((), logits.dtype)
+    rmax = empty((rows,), logits.dtype)
+    rsum = empty((rows,), logits.dtype)
+    dz = empty(logits.shape, logits.dtype)
+    _c("dtmi_xent_fused", _dt(logits), loss.ptr, dz.ptr, rmax.ptr, rsum.ptr, logits.ptr, targets.ptr, rows, V)
+    return loss, rmax, rsum, dz
+
+
+def xent_grad_scale(dz: DeviceArray, g: DeviceArray) -> DeviceArray:
+    """dz *= g[0] in place unless g[0] == 1; returns dz."""
+    _contig(dz, g)
+    if g.size != 1 or g.dtype != dz.dtype:
+        raise TypeError("xent: upstream gradient must be a 1-element array of the logits dtype")
+    _c("dtmi_xent_grad_scale", _dt(dz), dz.ptr, g.ptr, dz.size)
+    return dz
+
+
 def softmax_bwd(p: DeviceArray, dp: DeviceArray) -> DeviceArray:
     _contig(p, dp)
     if p.shape != dp.shape:

@@ -209,6 +209,15 @@ int dtmi_xent_fwd(int dtype, void* loss, void* rowmax, void* rowsum, const void*
                   int64_t rows, int64_t vocab);
 int dtmi_xent_bwd(int dtype, void* dlogits, const void* logits, const void* rowmax, const void* rowsum,
                   const int64_t* targets, const void* g_dev, double g_host, int64_t rows, int64_t vocab);
+/* Forward and gradient together, for a training step: the dtmi_xent_fwd outputs
+ * plus dlogits for an upstream gradient of 1, i.e. (exp(z - max) / sum -
+ * onehot(t)) / rows (dtrain/autograd.py:262-265 with g = 1). float32 rows of
+ * up to 65536 logits are read once and dlogits written once; other shapes run
+ * the two kernels above. dtmi_xent_grad_scale then multiplies dlogits (n
+ * elements) in place by the device scalar *g_dev unless it is exactly 1. */
+int dtmi_xent_fused(int dtype, void* loss, void* dlogits, void* rowmax, void* rowsum, const void* logits,
+                    const int64_t* targets, int64_t rows, int64_t vocab);
+int dtmi_xent_grad_scale(int dtype, void* dlogits, const void* g_dev, int64_t n);
 
 /* Row-wise softmax backward dS = P * (dP - rowsum(dP * P)), the core of
  * dtrain/autograd.py:242 (without the 1/sqrt(d) factor). */

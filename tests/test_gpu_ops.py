@@ -62,6 +62,32 @@ def test_cross_entropy_forward_backward(dev, dt, rows, V):
     assert rel_err(ggrad.numpy(), gz) <= TOL[dt]
 
 
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("rows,V", [(64, 50304), (8, 65536), (16, 4), (33, 1003), (8, 65540), (256, 65)])
+def test_cross_entropy_single_pass_forward_and_gradient(dev, dt, rows, V):
+    """dtmi_xent_fused (one read of the logits for float32 rows of up to 65536,
+    the two-kernel form otherwise) against the oracle, then the in-place
+    rescale for upstream gradients 1 (no change) and 0.25."""
+    D, K = _dev()
+    rng = np.random.default_rng(rows * 3 + V)
+    z = (rng.standard_normal((rows, V)) * 3).astype(dt)
+    t = rng.integers(0, V, rows)
+    loss, cache = ops.cross_entropy_fwd(z, t)
+    dz, dtgt = D.from_numpy(z), D.from_numpy(t.astype(np.int64))
+    dloss, rmax, rsum, dl = K.xent_fused(dz, dtgt)
+    assert rel_err(dloss.numpy(), loss) <= TOL[dt]
+    g1 = ops.cross_entropy_bwd(np.asarray(1.0, dtype=dt), z, t, cache)
+    assert rel_err(dl.numpy(), g1) <= TOL[dt]
+    before = dl.numpy()
+    K.xent_grad_scale(dl, D.from_numpy(np.ones(1, dt)))
+    assert bits_equal(dl.numpy(), before)
+    gq = ops.cross_entropy_bwd(np.asarray(0.25, dtype=dt), z, t, cache)
+    K.xent_grad_scale(dl, D.from_numpy(np.full(1, 0.25, dt)))
+    assert rel_err(dl.numpy(), gq) <= TOL[dt]
+    # the saved row statistics serve the two-kernel backward as well
+    assert rel_err(K.xent_bwd(dz, dtgt, rmax, rsum, g_host=1.0).numpy(), g1) <= TOL[dt]
+
+
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
 def test_softmax_backward(dev, dt):
     D, K = _dev()
