@@ -6,7 +6,7 @@ function cites the dtrain file:line it follows and performs the same NumPy
 operations in the same order with the same dtype promotion (NumPy 2 rules), so
 that on identical inputs it produces what dtrain produces. Only tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg import it, and only as
-the checker or the timed CPU baseline -- never as part of the product path
+the reference results to compare against or the timed CPU baseline -- never as part of the product path
 (the dtmi package never imports it).
 
 Pinning (what stops a plausible mistake here from going unnoticed):

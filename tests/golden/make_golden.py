@@ -1,5 +1,5 @@
 """Write golden vectors from dtrain itself (run in a container that has the dtrain
-source tree; the fixtures are committed and the GPU box never needs dtrain).
+source tree; the fixtures are committed, so the GPU tests never need dtrain).
 
     python tests/golden/make_golden.py [/path/to/DISTRIBUTED-TRAINING]
 

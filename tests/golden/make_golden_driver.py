@@ -1,6 +1,6 @@
 """Write golden fixtures for the training driver's data and checkpoint formats
 from dtrain itself (run where the dtrain source tree exists; the fixtures are
-committed and the GPU box never needs dtrain).
+committed, so the GPU tests never need dtrain).
 
     python tests/golden/make_golden_driver.py [/path/to/DISTRIBUTED-TRAINING]
 
