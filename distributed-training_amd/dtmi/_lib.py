@@ -117,13 +117,20 @@ def load(path: Path | str | None = None):
 
 
 def lib():
-    """The library, initialised on device DTMI_DEVICE (default 0)."""
+    """The library, initialised on device DTMI_DEVICE (default 0), with the
+    float32 GEMM arithmetic DTMI_GEMM_MATH ("f32", the default, or "bf16x6")."""
     global _initialised
     L = load()
     if not _initialised:
         rc = L.dtmi_init(int(os.environ.get("DTMI_DEVICE", "0")))
         if rc != 0:
             raise DtmiError(f"dtmi_init failed ({rc}): {L.dtmi_last_error().decode()}")
+        mode = os.environ.get("DTMI_GEMM_MATH", "f32")
+        if mode not in GEMM_MATH:
+            raise ValueError(f"DTMI_GEMM_MATH={mode!r}; expected one of {sorted(GEMM_MATH)}")
+        rc = L.dtmi_set_gemm_math(GEMM_MATH[mode])
+        if rc != 0:
+            raise DtmiError(f"dtmi_set_gemm_math failed ({rc}): {L.dtmi_last_error().decode()}")
         _initialised = True
     return L
 

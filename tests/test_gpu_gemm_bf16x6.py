@@ -34,11 +34,14 @@ def _ref(a, b, akc, bkc):
 
 
 def test_mode_switch_round_trips(dev):
+    import os
     from dtmi import _lib
-    assert _lib.gemm_math() == "f32"
-    with _lib.use_gemm_math("bf16x6"):
-        assert _lib.gemm_math() == "bf16x6"
-    assert _lib.gemm_math() == "f32"
+    start = _lib.gemm_math()
+    assert start == os.environ.get("DTMI_GEMM_MATH", "f32")
+    for mode in ("bf16x6", "f32"):
+        with _lib.use_gemm_math(mode):
+            assert _lib.gemm_math() == mode
+        assert _lib.gemm_math() == start
     with pytest.raises(ValueError):
         _lib.set_gemm_math("tf32")
 
