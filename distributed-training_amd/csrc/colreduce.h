@@ -1,10 +1,11 @@
 // Deterministic second stage of the column reductions (LayerNorm dgamma/dbeta,
 // bias gradients): out[c] (+)= sum_p parts[p * cols + c].
 //
-// A 256-thread block covers 32 columns with 8 groups of 32 lanes; group g adds
-// the parts p = g, g + 8, g + 16, ... in increasing order (eight independent
-// loads in flight per step), then the eight group sums are added in group
-// order. The grouping depends only on nparts, so results are reproducible.
+// A 1024-thread block covers 32 columns with 32 groups of 32 lanes; group g
+// adds the parts p = g, g + 32, g + 64, ... in increasing order (eight
+// independent loads in flight per step), then the 32 group sums of a column
+// are combined by a fixed butterfly across 32 lanes. The grouping depends only
+// on nparts, so results are reproducible.
 #pragma once
 
 #include "common.h"
@@ -14,43 +15,46 @@ namespace dtmi {
 // blockIdx.y selects one of two (out, parts) pairs, so two reductions of the
 // same shape (LayerNorm's dgamma and dbeta) share one launch.
 template <typename T>
-__global__ void __launch_bounds__(256) colreduce_kernel(T* __restrict__ out, const T* __restrict__ parts, int nparts,
-                                                         int64_t cols, int accumulate, T* __restrict__ out1,
-                                                         const T* __restrict__ parts1) {
+__global__ void __launch_bounds__(1024) colreduce_kernel(T* __restrict__ out, const T* __restrict__ parts, int nparts,
+                                                          int64_t cols, int accumulate, T* __restrict__ out1,
+                                                          const T* __restrict__ parts1) {
   if (blockIdx.y == 1) {
     out = out1;
     parts = parts1;
   }
-  __shared__ T sh[8][32];
+  __shared__ T sh[32][33];
   const int cl = threadIdx.x & 31, grp = threadIdx.x >> 5;
-  const int64_t c = (int64_t)blockIdx.x * 32 + cl;
+  const int64_t c0 = (int64_t)blockIdx.x * 32;
+  const int64_t c = c0 + cl;
   T acc = T(0);
   if (c < cols) {
     int p = grp;
-    for (; p + 8 * 7 < nparts; p += 64) {
+    for (; p + 32 * 7 < nparts; p += 256) {
       T v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = parts[(int64_t)(p + 8 * u) * cols + c];
+      for (int u = 0; u < 8; ++u) v[u] = parts[(int64_t)(p + 32 * u) * cols + c];
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc = acc + v[u];
     }
-    for (; p < nparts; p += 8) acc = acc + parts[(int64_t)p * cols + c];
+    for (; p < nparts; p += 32) acc = acc + parts[(int64_t)p * cols + c];
   }
   sh[grp][cl] = acc;
   __syncthreads();
-  if (grp == 0 && c < cols) {
-    T r = sh[0][cl];
+  // thread t now takes column t / 32 and group t % 32: a wave holds two
+  // columns, and each half-wave sums its 32 groups by a fixed butterfly
+  const int col = threadIdx.x >> 5, g = threadIdx.x & 31;
+  T r = sh[g][col];
 #pragma unroll
-    for (int g = 1; g < 8; ++g) r = r + sh[g][cl];
-    out[c] = accumulate ? out[c] + r : r;
-  }
+  for (int off = 16; off >= 1; off >>= 1) r = r + __shfl_xor(r, off, 64);
+  const int64_t cc = c0 + col;
+  if (g == 0 && cc < cols) out[cc] = accumulate ? out[cc] + r : r;
 }
 
 template <typename T>
 inline void launch_colreduce(T* out, const T* parts, int nparts, int64_t cols, int accumulate, T* out1 = nullptr,
                              const T* parts1 = nullptr) {
   dim3 grid((unsigned)cdiv(cols, 32), out1 ? 2u : 1u);
-  colreduce_kernel<T><<<grid, 256, 0, stream()>>>(out, parts, nparts, cols, accumulate, out1, parts1);
+  colreduce_kernel<T><<<grid, 1024, 0, stream()>>>(out, parts, nparts, cols, accumulate, out1, parts1);
 }
 
 }  // namespace dtmi

@@ -144,20 +144,44 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
     }
   }
   const T n = (T)cols;
-  for (int64_t row = (int64_t)blockIdx.x * 4 + wave; row < rows; row += wstride) {
-    const T mu = mean[row], rs = rstd[row];
+  // Software pipeline: the next row's dy, x, mean and rstd are loaded while
+  // the current row is reduced and stored, so every wave keeps a row of loads
+  // in flight. The arithmetic per row is unchanged.
+  T gn[NV][VW], xn[NV][VW];
+  T mun = T(0), rsn = T(0);
+  int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  auto load_row = [&](int64_t r) {
+    mun = mean[r];
+    rsn = rstd[r];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int c = VW * lane + 64 * VW * j;
+      if (c < cols) {
+        load_vec<T, VW>(gn[j], dy + r * cols + c);
+        load_vec<T, VW>(xn[j], x + r * cols + c);
+      }
+    }
+  };
+  if (row < rows) load_row(row);
+  for (; row < rows; row += wstride) {
+    const T mu = mun, rs = rsn;
     T gv[NV][VW], xh[NV][VW];
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        gv[j][e] = gn[j][e];
+        xh[j][e] = xn[j][e];
+      }
+    if (row + wstride < rows) load_row(row + wstride);
     T s1 = T(0), s2 = T(0);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int c = VW * lane + 64 * VW * j;
       if (c < cols) {
-        T xv[VW];
-        load_vec<T, VW>(gv[j], dy + row * cols + c);
-        load_vec<T, VW>(xv, x + row * cols + c);
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
-          xh[j][e] = (xv[e] - mu) * rs;
+          xh[j][e] = (xh[j][e] - mu) * rs;
           T gxh = gv[j][e] * wv[j][e];
           s1 += gxh;
           s2 += gxh * xh[j][e];

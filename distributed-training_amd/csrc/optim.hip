@@ -15,6 +15,8 @@
 #include <cmath>
 #include <vector>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace dtmi {
@@ -301,7 +303,9 @@ __device__ __forceinline__ double sq64(T x) {
 // ------------------------------------------------- fixed-order average
 // out[i] = (((rep_0[i] + rep_1[i]) + ...) + rep_{W-1}[i]) * inv; with SUMSQ the
 // block's float64 sum of out^2 goes to partials[blockIdx.x] (fixed pattern).
-template <typename T, bool VEC, bool SUMSQ>
+// WC > 0 fixes the replica count at compile time (the vector path then loads
+// all replicas at once); WC = 0 takes it from `world`.
+template <typename T, bool VEC, bool SUMSQ, int WC>
 __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out, const T* __restrict__ rep,
                                                               int world, int64_t n, int64_t stride, T inv,
                                                               double* __restrict__ partials) {
@@ -317,8 +321,20 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
       const int64_t e0 = base + (int64_t)(u * 256 + threadIdx.x) * N;
       if (e0 + N <= n) {
         const int64_t k = e0 / N;
-        VT a = ld_nt(reinterpret_cast<const VT*>(rep) + k);
-        for (int r = 1; r < world; ++r) a = a + ld_nt(reinterpret_cast<const VT*>(rep + (int64_t)r * stride) + k);
+        VT a;
+        if constexpr (WC > 0) {
+          // WC replicas known at compile time: every load is issued before
+          // the first add, and the adds keep rank order
+          VT v[WC];
+#pragma unroll
+          for (int r = 0; r < WC; ++r) v[r] = ld_nt(reinterpret_cast<const VT*>(rep + (int64_t)r * stride) + k);
+          a = v[0];
+#pragma unroll
+          for (int r = 1; r < WC; ++r) a = a + v[r];
+        } else {
+          a = ld_nt(reinterpret_cast<const VT*>(rep) + k);
+          for (int r = 1; r < world; ++r) a = a + ld_nt(reinterpret_cast<const VT*>(rep + (int64_t)r * stride) + k);
+        }
         a = a * inv;
         if (SUMSQ)
 #pragma unroll
@@ -374,13 +390,28 @@ __global__ void __launch_bounds__(256) sumsq_multi_kernel(const SumsqEntry* __re
     using VT = typename V16<T>::type;
     constexpr int N = V16<T>::N;
     const int64_t nv = (hi - lo) / N;
-    const VT* xv = reinterpret_cast<const VT*>(x + lo);
-    for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
+    // the pointer comes from a table in memory: cast it to the global address
+    // space so the loads are global (not flat) loads that can all be in flight
+    using GVT = const __attribute__((address_space(1))) VT;
+    GVT* xv = (GVT*)(x + lo);
+    // four vectors are loaded ahead; the squares are added in the same
+    // element order as a one-vector loop
+    int64_t i = threadIdx.x;
+    for (; i + 3 * 256 < nv; i += 4 * 256) {
+      VT a[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = xv[i + u * 256];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int el = 0; el < N; ++el) acc += sq64(vget<T>(a[u], el));
+    }
+    for (; i < nv; i += 256) {
       VT a = xv[i];
 #pragma unroll
       for (int el = 0; el < N; ++el) acc += sq64(vget<T>(a, el));
     }
-    for (int64_t k = lo + nv * N + threadIdx.x; k < hi; k += blockDim.x) acc += sq64(x[k]);
+    for (int64_t k = lo + nv * N + threadIdx.x; k < hi; k += 256) acc += sq64(x[k]);
   } else {
     for (int64_t k = lo + threadIdx.x; k < hi; k += blockDim.x) acc += sq64(x[k]);
   }
@@ -531,20 +562,27 @@ static int launch_average(void* out, const void* rep, int world, int64_t n, int6
   int grid = average_grid(n);
   TimedLaunch tl(DTMI_FAM_BUCKET_AVG, (double)(world + 1) * (double)n * sizeof(T));
   T inv = (T)inv_w;
+  T* O = (T*)out;
+  const T* R = (const T*)rep;
   if (vec) {
-    if (partials)
-      bucket_average_kernel<T, true, true><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride, inv,
-                                                                       partials);
-    else
-      bucket_average_kernel<T, true, false><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride,
-                                                                        inv, partials);
+    auto go = [&](auto wc) {
+      constexpr int WC = decltype(wc)::value;
+      if (partials)
+        bucket_average_kernel<T, true, true, WC><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
+      else
+        bucket_average_kernel<T, true, false, WC><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
+    };
+    switch (world) {
+      case 2: go(std::integral_constant<int, 2>{}); break;
+      case 3: go(std::integral_constant<int, 3>{}); break;
+      case 4: go(std::integral_constant<int, 4>{}); break;
+      default: go(std::integral_constant<int, 0>{}); break;
+    }
   } else {
     if (partials)
-      bucket_average_kernel<T, false, true><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride, inv,
-                                                                        partials);
+      bucket_average_kernel<T, false, true, 0><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
     else
-      bucket_average_kernel<T, false, false><<<grid, 256, 0, stream()>>>((T*)out, (const T*)rep, world, n, stride,
-                                                                         inv, partials);
+      bucket_average_kernel<T, false, false, 0><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
   }
   LAUNCH_CHECK("bucket_average_kernel");
   return DTMI_OK;
