@@ -176,6 +176,12 @@ static int launch_adamw_flat(void* p, const void* g, void* m, void* v, int64_t n
 // Multi-tensor table: one entry per tensor; chunk c of the launch belongs to
 // the entry e with e.chunk_begin <= c < next.chunk_begin.
 constexpr int64_t kChunk = 32768;
+// Pointers read from a table in device memory are generic (flat) pointers to
+// the compiler; flat accesses also count on the LDS/scalar counter, so every
+// wait for them is a full wait. Casting them to the global address space
+// gives global loads and stores that can be in flight together.
+template <typename X>
+using global_t = __attribute__((address_space(1))) X;
 
 struct MTAdamEntry {
   void* p;
@@ -218,10 +224,10 @@ __global__ void __launch_bounds__(256) adamw_multi_kernel(const MTAdamEntry* __r
     constexpr int N = V16<T>::N;
     // lo is a multiple of kChunk (a multiple of N); only the last chunk has a tail.
     const int64_t nv = (hi - lo) / N;
-    VT* pv = reinterpret_cast<VT*>(p + lo);
-    const VT* gv = reinterpret_cast<const VT*>(g + lo);
-    VT* mv = reinterpret_cast<VT*>(m + lo);
-    VT* vv = reinterpret_cast<VT*>(v + lo);
+    global_t<VT>* pv = (global_t<VT>*)(p + lo);
+    global_t<const VT>* gv = (global_t<const VT>*)(g + lo);
+    global_t<VT>* mv = (global_t<VT>*)(m + lo);
+    global_t<VT>* vv = (global_t<VT>*)(v + lo);
     for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) {
       VT P = pv[i], G = gv[i], M = mv[i], W = vv[i];
 #pragma unroll
@@ -267,8 +273,17 @@ __global__ void __launch_bounds__(256) flatten_kernel(T* __restrict__ dst, const
     const int64_t nv = (hi - lo) / N;
     VT* ov = reinterpret_cast<VT*>(out + lo);
     if (src) {
-      const VT* sv = reinterpret_cast<const VT*>(src + lo);
-      for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) ov[i] = sv[i];
+      // four vectors in flight per thread
+      global_t<const VT>* sv = (global_t<const VT>*)(src + lo);
+      int64_t i = threadIdx.x;
+      for (; i + 3 * 256 < nv; i += 4 * 256) {
+        VT a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = sv[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ov[i + u * 256] = a[u];
+      }
+      for (; i < nv; i += 256) ov[i] = sv[i];
     } else {
       VT z;
       for (int el = 0; el < N; ++el) vset<T>(z, el, T(0));
@@ -390,10 +405,7 @@ __global__ void __launch_bounds__(256) sumsq_multi_kernel(const SumsqEntry* __re
     using VT = typename V16<T>::type;
     constexpr int N = V16<T>::N;
     const int64_t nv = (hi - lo) / N;
-    // the pointer comes from a table in memory: cast it to the global address
-    // space so the loads are global (not flat) loads that can all be in flight
-    using GVT = const __attribute__((address_space(1))) VT;
-    GVT* xv = (GVT*)(x + lo);
+    global_t<const VT>* xv = (global_t<const VT>*)(x + lo);
     // four vectors are loaded ahead; the squares are added in the same
     // element order as a one-vector loop
     int64_t i = threadIdx.x;

@@ -153,8 +153,8 @@ __global__ void __launch_bounds__(256) xent_bwd_kernel(T* __restrict__ dz, const
 // Forward and gradient in one pass (float32, rows of up to 65536 logits):
 // one 1024-thread block per row holds the row in registers (NV 16-byte
 // vectors per thread), so the logits are read once and dlogits written once
-// (the two-kernel form reads them twice). dlogits = (exp(z - max) / sum -
-// onehot) * (1 / n): the gradient for an upstream gradient of 1, which
+// (the two-kernel form reads them twice). dlogits = (exp(z - max) * (1 / sum)
+// - onehot) * (1 / n): the gradient for an upstream gradient of 1, which
 // xent_grad_scale_kernel rescales in place when the upstream gradient is not
 // 1. Max and sum are combined in a fixed order: a butterfly per wave, then
 // the 16 wave results in wave order.
@@ -188,11 +188,15 @@ __global__ void __launch_bounds__(1024) xent_fused_kernel(float* __restrict__ dz
 #pragma unroll
   for (int w = 1; w < 16; ++w) M = fmaxf(M, red[w]);
   __syncthreads();
+  // v becomes exp(z - max) (0 past the row end), reused by the gradient
   float sl = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sl += (tid + 1024 * j < nv) ? expf(v[j][e] - M) : 0.f;
+    for (int e = 0; e < 4; ++e) {
+      v[j][e] = (tid + 1024 * j < nv) ? expf(v[j][e] - M) : 0.f;
+      sl += v[j][e];
+    }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) sl += __shfl_xor(sl, off, 64);
   if (lane == 0) red[wave] = sl;
@@ -207,6 +211,11 @@ __global__ void __launch_bounds__(1024) xent_fused_kernel(float* __restrict__ dz
     // (z - zmax) - log(s), dtrain/autograd.py:255
     logp_t[row] = (t >= 0 && t < V) ? (z[row * V + t] - M) - logf(S) : NAN;
   }
+  // p = e * (1 / s): within 1.5 ulp of e / s, and one multiply per logit
+  // instead of a division (the block's vector work does not overlap its
+  // loads, one row block fills a CU). V < 2^31 here, so 32-bit indices.
+  const float rS = 1.f / S;
+  const int t32 = (t >= 0 && t < V) ? (int)t : -1;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int i = tid + 1024 * j;
@@ -214,8 +223,8 @@ __global__ void __launch_bounds__(1024) xent_fused_kernel(float* __restrict__ dz
       f4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float p = expf(v[j][e] - M) / S;
-        if ((int64_t)(4 * i + e) == t) p = p - 1.f;
+        float p = v[j][e] * rS;
+        if (4 * i + e == t32) p = p - 1.f;
         o[e] = p * inv_n;
       }
       dr[i] = o;
