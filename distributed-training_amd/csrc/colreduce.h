@@ -1,11 +1,11 @@
 // Deterministic second stage of the column reductions (LayerNorm dgamma/dbeta,
 // bias gradients): out[c] (+)= sum_p parts[p * cols + c].
 //
-// A 1024-thread block covers 32 columns with 32 groups of 32 lanes; group g
-// adds the parts p = g, g + 32, g + 64, ... in increasing order (eight
-// independent loads in flight per step), then the 32 group sums of a column
-// are combined by a fixed butterfly across 32 lanes. The grouping depends only
-// on nparts, so results are reproducible.
+// A 1024-thread block covers 16 columns with 64 groups of 16 lanes; group g
+// adds the parts p = g, g + 64, g + 128, ... in increasing order (eight
+// independent loads in flight per step: one step for 512 parts), then the 64
+// group sums of a column are combined by a fixed butterfly across a wave. The
+// grouping depends only on nparts, so results are reproducible.
 #pragma once
 
 #include "common.h"
@@ -22,30 +22,30 @@ __global__ void __launch_bounds__(1024) colreduce_kernel(T* __restrict__ out, co
     out = out1;
     parts = parts1;
   }
-  __shared__ T sh[32][33];
-  const int cl = threadIdx.x & 31, grp = threadIdx.x >> 5;
-  const int64_t c0 = (int64_t)blockIdx.x * 32;
+  __shared__ T sh[64][17];
+  const int cl = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 16;
   const int64_t c = c0 + cl;
   T acc = T(0);
   if (c < cols) {
     int p = grp;
-    for (; p + 32 * 7 < nparts; p += 256) {
+    for (; p + 64 * 7 < nparts; p += 512) {
       T v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = parts[(int64_t)(p + 32 * u) * cols + c];
+      for (int u = 0; u < 8; ++u) v[u] = parts[(int64_t)(p + 64 * u) * cols + c];
 #pragma unroll
       for (int u = 0; u < 8; ++u) acc = acc + v[u];
     }
-    for (; p < nparts; p += 32) acc = acc + parts[(int64_t)p * cols + c];
+    for (; p < nparts; p += 64) acc = acc + parts[(int64_t)p * cols + c];
   }
   sh[grp][cl] = acc;
   __syncthreads();
-  // thread t now takes column t / 32 and group t % 32: a wave holds two
-  // columns, and each half-wave sums its 32 groups by a fixed butterfly
-  const int col = threadIdx.x >> 5, g = threadIdx.x & 31;
+  // wave w now takes column w and lane g its group g; the 64 group sums are
+  // combined by a fixed butterfly
+  const int col = threadIdx.x >> 6, g = threadIdx.x & 63;
   T r = sh[g][col];
 #pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) r = r + __shfl_xor(r, off, 64);
+  for (int off = 32; off >= 1; off >>= 1) r = r + __shfl_xor(r, off, 64);
   const int64_t cc = c0 + col;
   if (g == 0 && cc < cols) out[cc] = accumulate ? out[cc] + r : r;
 }
@@ -53,7 +53,7 @@ __global__ void __launch_bounds__(1024) colreduce_kernel(T* __restrict__ out, co
 template <typename T>
 inline void launch_colreduce(T* out, const T* parts, int nparts, int64_t cols, int accumulate, T* out1 = nullptr,
                              const T* parts1 = nullptr) {
-  dim3 grid((unsigned)cdiv(cols, 32), out1 ? 2u : 1u);
+  dim3 grid((unsigned)cdiv(cols, 16), out1 ? 2u : 1u);
   colreduce_kernel<T><<<grid, 1024, 0, stream()>>>(out, parts, nparts, cols, accumulate, out1, parts1);
 }
 
