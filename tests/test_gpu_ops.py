@@ -22,7 +22,7 @@ def _dev():
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
-@pytest.mark.parametrize("shape", [(2, 3, 6), (256, 64), (4096, 768), (5, 1000), (3, 17)])
+@pytest.mark.parametrize("shape", [(2, 3, 6), (256, 64), (4096, 768), (5, 1000), (3, 17), (2400, 1000), (5000, 768)])
 def test_layernorm_forward_backward(dev, dt, shape):
     D, K = _dev()
     rng = np.random.default_rng(sum(shape))

@@ -110,7 +110,7 @@ def test_adamw_multi_matches_per_array_loop(dev, dt):
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
-@pytest.mark.parametrize("world", [1, 2, 3, 4])
+@pytest.mark.parametrize("world", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("n", [1, 262_144, 1_000_001])
 def test_bucket_average_fixed_order_bit_exact(dev, dt, world, n):
     D, K = _dev()
@@ -128,6 +128,22 @@ def test_bucket_average_fixed_order_bit_exact(dev, dt, world, n):
     K.sumsq_finish(parts, nb, sq)
     ref_sq = float(np.dot(ref.astype(np.float64), ref.astype(np.float64)))
     assert abs(float(sq.numpy()[0]) - ref_sq) <= 1e-14 * ref_sq
+
+
+def test_flatten_aligned_sources_bit_exact(dev):
+    """16-byte aligned sources and slots take the vector copy (four vectors in
+    flight per thread, then a one-vector loop, then a scalar tail): sizes that
+    fill whole chunks, end mid-chunk and end off a multiple of four."""
+    D, K = _dev()
+    rng = np.random.default_rng(11)
+    counts = [40000, 262144, 12, 70004, 5, 4]
+    host = [rng.standard_normal(n).astype(np.float32) for n in counts]
+    srcs = [D.from_numpy(h) for h in host]
+    srcs[3] = None
+    dst = D.full((sum(counts),), 9.0, np.float32)
+    K.bucket_flatten(dst, srcs, counts)
+    ref = np.concatenate([h if i != 3 else np.zeros(counts[3], np.float32) for i, h in enumerate(host)])
+    assert bits_equal(dst.numpy(), ref)
 
 
 def test_flatten_with_missing_grads(dev):
