@@ -146,7 +146,10 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
   const T n = (T)cols;
   // Software pipeline: the next row's dy, x, mean and rstd are loaded while
   // the current row is reduced and stored, so every wave keeps a row of loads
-  // in flight. The arithmetic per row is unchanged.
+  // in flight. Rows longer than 8 vectors per lane load each vector where it
+  // is used instead (a second row set would spill). The arithmetic per row is
+  // the same.
+  constexpr bool PF = NV <= 8;
   T gn[NV][VW], xn[NV][VW];
   T mun = T(0), rsn = T(0);
   int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -162,23 +165,34 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
       }
     }
   };
-  if (row < rows) load_row(row);
+  if (PF && row < rows) load_row(row);
   for (; row < rows; row += wstride) {
-    const T mu = mun, rs = rsn;
+    T mu, rs;
     T gv[NV][VW], xh[NV][VW];
+    if constexpr (PF) {
+      mu = mun;
+      rs = rsn;
 #pragma unroll
-    for (int j = 0; j < NV; ++j)
+      for (int j = 0; j < NV; ++j)
 #pragma unroll
-      for (int e = 0; e < VW; ++e) {
-        gv[j][e] = gn[j][e];
-        xh[j][e] = xn[j][e];
-      }
-    if (row + wstride < rows) load_row(row + wstride);
+        for (int e = 0; e < VW; ++e) {
+          gv[j][e] = gn[j][e];
+          xh[j][e] = xn[j][e];
+        }
+      if (row + wstride < rows) load_row(row + wstride);
+    } else {
+      mu = mean[row];
+      rs = rstd[row];
+    }
     T s1 = T(0), s2 = T(0);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int c = VW * lane + 64 * VW * j;
       if (c < cols) {
+        if constexpr (!PF) {
+          load_vec<T, VW>(gv[j], dy + row * cols + c);
+          load_vec<T, VW>(xh[j], x + row * cols + c);
+        }
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
           xh[j][e] = (xh[j][e] - mu) * rs;

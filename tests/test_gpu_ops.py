@@ -22,7 +22,8 @@ def _dev():
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
-@pytest.mark.parametrize("shape", [(2, 3, 6), (256, 64), (4096, 768), (5, 1000), (3, 17), (2400, 1000), (5000, 768)])
+@pytest.mark.parametrize("shape", [(2, 3, 6), (256, 64), (4096, 768), (5, 1000), (3, 17), (2400, 1000), (5000, 768),
+                                   (33, 2000), (9, 2048)])
 def test_layernorm_forward_backward(dev, dt, shape):
     D, K = _dev()
     rng = np.random.default_rng(sum(shape))
@@ -42,6 +43,13 @@ def test_layernorm_forward_backward(dev, dt, shape):
     assert rel_err(db.numpy(), gb) <= TOL[dt]
     dx2, dw2, _ = K.layernorm_bwd(D.from_numpy(g), D.from_numpy(x), D.from_numpy(w), mean, rstd)
     assert bits_equal(dx2.numpy(), dx.numpy()) and bits_equal(dw2.numpy(), dw.numpy())
+
+
+@pytest.mark.parametrize("shape", [(40, 3000), (1100, 4096)])
+def test_layernorm_long_float32_rows(dev, shape):
+    """float32 rows of 12 and 16 vectors per lane: the backward loads each
+    vector where it is used instead of prefetching the next row."""
+    test_layernorm_forward_backward(dev, np.float32, shape)
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
