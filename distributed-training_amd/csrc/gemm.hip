@@ -1088,7 +1088,16 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
     if (VEC > 1) {  // 16-byte vectors: every operand is aligned (checked by the host)
       typedef T vt __attribute__((ext_vector_type(VEC)));
       vt v = *reinterpret_cast<const vt*>(ws + idx);
-      for (int s = 1; s < splits; ++s) v = v + *reinterpret_cast<const vt*>(ws + (int64_t)s * total + idx);
+      // four partials loaded at a time, added in split order
+      int s = 1;
+      for (; s + 3 < splits; s += 4) {
+        vt t[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) t[u] = *reinterpret_cast<const vt*>(ws + (int64_t)(s + u) * total + idx);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v = v + t[u];
+      }
+      for (; s < splits; ++s) v = v + *reinterpret_cast<const vt*>(ws + (int64_t)s * total + idx);
       if (bias) v = v + *reinterpret_cast<const vt*>(bias + n);
       const int64_t o = m * a.ldc + n;
       if (!PLAIN) {  // the epilogue_store sequence, VEC elements at a time
