@@ -190,6 +190,33 @@ __global__ void reduce_axes_kernel(T* __restrict__ out, const T* __restrict__ x,
   }
 }
 
+// Sum over leading axes of a contiguous array, viewed as [nred, nout]:
+// out[o] = sum_r x[r * nout + o] with r ascending, the order of
+// reduce_axes_kernel for this case (the same bits), in 16-byte vectors with
+// eight rows of loads in flight per thread.
+template <typename T>
+__global__ void __launch_bounds__(256) reduce_lead_kernel(T* __restrict__ out, const T* __restrict__ x, int64_t nout,
+                                                           int64_t nred) {
+  constexpr int N = 16 / sizeof(T);
+  typedef T vt __attribute__((ext_vector_type(N)));
+  const int64_t nv = nout / N;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += stride) {
+    const T* p = x + i * N;
+    vt acc = (vt)(T(0));
+    int64_t r = 0;
+    for (; r + 8 <= nred; r += 8) {
+      vt v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const vt*>(p + (r + u) * nout);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = acc + v[u];
+    }
+    for (; r < nred; ++r) acc = acc + *reinterpret_cast<const vt*>(p + r * nout);
+    *reinterpret_cast<vt*>(out + i * N) = acc;
+  }
+}
+
 // Column sums of a [rows, cols] row-major matrix, deterministic two-stage:
 // stage 1 block (bx, by) sums rows [by*RB, (by+1)*RB) of columns
 // [bx*256*V, ...) into part[by][col]; stage 2 sums the parts of each column in
@@ -451,6 +478,23 @@ DTMI_EXPORT int dtmi_reduce_sum(int dtype, void* out, const void* x, const int64
   if (nout == 0) return DTMI_OK;
   DTMI_CHECK(out && (x || nred == 0), "dtmi_reduce_sum: NULL pointer");
   TimedLaunch tl(DTMI_FAM_OTHER, (double)(nout * nred + nout) * (dtype == DTMI_F32 ? 4 : 8));
+  // contiguous input reduced over a leading run of axes: [nred, nout]
+  bool lead = nred > 0;
+  for (int k = 0; k < ndim && lead; ++k) {
+    if (strides && shape[k] > 1 && strides[k] != cstr[k]) lead = false;
+    if (k > 0 && reduce_mask[k] && !reduce_mask[k - 1]) lead = false;
+  }
+  const int64_t vn = dtype == DTMI_F32 ? 4 : 2;
+  if (lead && nout % vn == 0 && aligned(x, 16) && aligned(out, 16)) {
+    const int64_t nvec = nout / vn;
+    const int grid = (int)(cdiv(nvec, 256) < 8192 ? cdiv(nvec, 256) : 8192);
+    if (dtype == DTMI_F32)
+      reduce_lead_kernel<float><<<grid, 256, 0, stream()>>>((float*)out, (const float*)x, nout, nred);
+    else
+      reduce_lead_kernel<double><<<grid, 256, 0, stream()>>>((double*)out, (const double*)x, nout, nred);
+    LAUNCH_CHECK("reduce_lead_kernel");
+    return DTMI_OK;
+  }
   if (dtype == DTMI_F32)
     reduce_axes_kernel<float><<<grid_1d(nout, 1), 256, 0, stream()>>>((float*)out, (const float*)x, d, nout, nred);
   else

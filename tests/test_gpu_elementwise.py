@@ -67,6 +67,24 @@ def test_relu_exact(dev):
     assert bits_equal(K.relu_bwd(D.from_numpy(x), D.from_numpy(g)).numpy(), ops.relu_bwd(g, m))
 
 
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("shape,axes", [((8, 1024, 768), [0]), ((19, 6, 20), [0]), ((3, 5, 7, 8), [0, 1]),
+                                        ((10, 7), [0]), ((4, 9, 3), [0])])
+def test_reduce_leading_axes_bit_exact(dev, dt, shape, axes):
+    """Sums over leading axes (the position-embedding gradient's batch sum)
+    add the reduced rows in ascending order, vector path or not: the bits of
+    an explicit row-by-row sum."""
+    D, K = _dev()
+    x = np.random.default_rng(len(shape) * 31 + shape[0]).standard_normal(shape).astype(dt)
+    nred = int(np.prod([shape[a] for a in axes]))
+    rows = x.reshape(nred, -1)
+    ref = np.zeros(rows.shape[1], dt)
+    for r in range(nred):
+        ref = ref + rows[r]
+    got = K.reduce_sum(D.from_numpy(x), axes).numpy()
+    assert bits_equal(got.reshape(-1), ref)
+
+
 @pytest.mark.parametrize("dt,tol", [(np.float64, 1e-13), (np.float32, 1e-5)])
 def test_reductions(dev, dt, tol):
     D, K = _dev()
