@@ -124,7 +124,8 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
                                                       T* __restrict__ part_db, const T* __restrict__ dy,
                                                       const T* __restrict__ x, const T* __restrict__ w,
                                                       const T* __restrict__ mean, const T* __restrict__ rstd,
-                                                      int64_t rows, int cols, int accumulate_dx) {
+                                                      const T* __restrict__ addend, int64_t rows, int cols,
+                                                      int accumulate_dx) {
   extern __shared__ unsigned char lds_raw[];
   T* lds = reinterpret_cast<T*>(lds_raw);  // [4 waves][2][NV*VW*64]
   const int lane = threadIdx.x & 63;
@@ -210,13 +211,17 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
     for (int j = 0; j < NV; ++j) {
       const int c = VW * lane + 64 * VW * j;
       if (c < cols) {
+        // dx (+)= r: onto the existing dx, or a separate addend written to dx
+        // (pending + r: the order of the backward engine's sum)
         T o[VW];
         if (accumulate_dx) load_vec<T, VW>(o, dx + row * cols + c);
+        else if (addend) load_vec<T, VW>(o, addend + row * cols + c);
+        const bool add = accumulate_dx || addend;
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
           T gxh = gv[j][e] * wv[j][e];
           T r = rs * ((gxh - m1) - xh[j][e] * m2);
-          o[e] = accumulate_dx ? o[e] + r : r;
+          o[e] = add ? o[e] + r : r;
         }
         store_vec<T, VW>(dx + row * cols + c, o);
       }
@@ -263,9 +268,9 @@ struct LnDispatch {
   }
   template <int NV>
   static void bwd(int grid, T* dx, T* pdw, T* pdb, const T* dy, const T* x, const T* w, const T* mu, const T* rs,
-                  int64_t rows, int cols, int acc) {
+                  const T* add, int64_t rows, int cols, int acc) {
     size_t lds = (size_t)4 * 2 * NV * VW * 64 * sizeof(T);
-    ln_bwd_kernel<T, NV, VW><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, rows, cols, acc);
+    ln_bwd_kernel<T, NV, VW><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, add, rows, cols, acc);
   }
 };
 
@@ -319,9 +324,10 @@ static int ln_fwd(void* y, void* mean, void* rstd, const void* x, const void* w,
 
 template <typename T>
 static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, const void* w, const void* mean,
-                  const void* rstd, int64_t rows, int64_t cols, int accumulate) {
+                  const void* rstd, const void* addend, int64_t rows, int64_t cols, int accumulate) {
   constexpr int VWV = 16 / sizeof(T);
-  bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(dy, 16) && aligned(dx, 16) && aligned(w, 16);
+  bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(dy, 16) && aligned(dx, 16) && aligned(w, 16) &&
+             aligned(addend, 16);
   int vw = vec ? VWV : 1;
   int nv = pick_nv(cdiv(cols, 64LL * vw));
   DTMI_CHECK(nv > 0, "dtmi_layernorm_bwd: rows of %lld elements exceed the supported %d", (long long)cols, 64 * 16 * vw);
@@ -332,17 +338,20 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
   T* pdw = (T*)parts;
   T* pdb = pdw + (size_t)grid * cols;
   {
-    TimedLaunch tl(DTMI_FAM_LN_BWD, (double)rows * cols * 3 * sizeof(T));
+    // x and dy in, dx out, and the addend (or the existing dx) in when summed
+    const double arrays = (addend || (accumulate & 1)) ? 4.0 : 3.0;
+    TimedLaunch tl(DTMI_FAM_LN_BWD, (double)rows * cols * arrays * sizeof(T));
     T* DX = (T*)dx;
     const T *DY = (const T*)dy, *X = (const T*)x, *W = (const T*)w, *MU = (const T*)mean, *RS = (const T*)rstd;
     int c = (int)cols;
     int acc = (accumulate & 1) ? 1 : 0;
+    const T* ADD = (const T*)addend;
     if (vec) {
-#define CALLV(NV) LnDispatch<T, VWV>::template bwd<NV>(grid, DX, pdw, pdb, DY, X, W, MU, RS, rows, c, acc)
+#define CALLV(NV) LnDispatch<T, VWV>::template bwd<NV>(grid, DX, pdw, pdb, DY, X, W, MU, RS, ADD, rows, c, acc)
       LN_NV_SWITCH(nv, CALLV)
 #undef CALLV
     } else {
-#define CALLS(NV) LnDispatch<T, 1>::template bwd<NV>(grid, DX, pdw, pdb, DY, X, W, MU, RS, rows, c, acc)
+#define CALLS(NV) LnDispatch<T, 1>::template bwd<NV>(grid, DX, pdw, pdb, DY, X, W, MU, RS, ADD, rows, c, acc)
       LN_NV_SWITCH(nv, CALLS)
 #undef CALLS
     }
@@ -387,7 +396,30 @@ DTMI_EXPORT int dtmi_layernorm_bwd(int dtype, void* dx, void* dw, void* db, cons
     return rc ? rc : dtmi_fill(dtype, db, 0.0, cols);
   }
   DTMI_CHECK(dx && dy && x && w && mean && rstd, "dtmi_layernorm_bwd: NULL pointer");
-  if (dtype == DTMI_F32) return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, rows, cols, accumulate);
-  return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, rows, cols, accumulate);
+  if (dtype == DTMI_F32) return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, nullptr, rows, cols, accumulate);
+  return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, nullptr, rows, cols, accumulate);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_layernorm_bwd_add(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x,
+                                       const void* w, const void* mean, const void* rstd, const void* dx_addend,
+                                       int64_t rows, int64_t cols, int accumulate) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(rows >= 0 && cols > 0 && cols < (1 << 30), "dtmi_layernorm_bwd_add: bad shape [%lld, %lld]",
+             (long long)rows, (long long)cols);
+  DTMI_CHECK(dw && db, "dtmi_layernorm_bwd_add: NULL dgamma/dbeta");
+  DTMI_CHECK(!(accumulate & 1), "dtmi_layernorm_bwd_add: dx takes the addend, not accumulate bit 0");
+  if (rows == 0) {
+    if (accumulate & 2) return DTMI_OK;
+    int rc = dtmi_fill(dtype, dw, 0.0, cols);
+    return rc ? rc : dtmi_fill(dtype, db, 0.0, cols);
+  }
+  DTMI_CHECK(dx && dy && x && w && mean && rstd && dx_addend, "dtmi_layernorm_bwd_add: NULL pointer");
+  DTMI_CHECK(dx_addend != dx, "dtmi_layernorm_bwd_add: the addend must not be dx (use accumulate bit 0)");
+  if (dtype == DTMI_F32)
+    return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, dx_addend, rows, cols, accumulate);
+  return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, dx_addend, rows, cols, accumulate);
   DTMI_BODY_END
 }

@@ -262,13 +262,30 @@ class Tensor:
 
     @staticmethod
     def _backprop(node, g, grads):
-        for p, pg in zip(node._parents, node._backward(g)):
+        # A backward function may offer `with_addend = (i, f)`: when parent i
+        # already has a pending gradient P, f(g, P) returns the parents'
+        # gradients with P already added into parent i's (P + its own, the
+        # order of the sum below), or None to decline.
+        outs, summed = None, -1
+        fuse = getattr(node._backward, "with_addend", None)
+        if fuse is not None:
+            i, f = fuse
+            p = node._parents[i]
+            if p.requires_grad and id(p) in grads:
+                outs = f(g, grads[id(p)])
+                summed = i if outs is not None else -1
+        if outs is None:
+            outs = node._backward(g)
+        for j, (p, pg) in enumerate(zip(node._parents, outs)):
             if not p.requires_grad or pg is None:
                 continue
             if tuple(pg.shape) != tuple(p.shape):
                 raise RuntimeError(f"gradient shape {pg.shape} != {p.shape}")
             k = id(p)
-            grads[k] = pg if k not in grads else K.binary("add", grads[k], pg)
+            if j == summed or k not in grads:
+                grads[k] = pg
+            else:
+                grads[k] = K.binary("add", grads[k], pg)
 
 
 def grad_out(t: Tensor):
@@ -341,8 +358,17 @@ def layer_norm(x: Tensor, w: Tensor, b: Tensor, eps=1e-5) -> Tensor:
     xd = _contig(x.data)
     y, mean, rstd = K.layernorm_fwd(xd, _contig(w.data), _contig(b.data), eps)
 
-    def bw(g):
-        return K.layernorm_bwd(_contig(g), xd, _contig(w.data), mean, rstd, dw_out=grad_out(w), db_out=grad_out(b))
+    def bw(g, dx_addend=None):
+        return K.layernorm_bwd(_contig(g), xd, _contig(w.data), mean, rstd, dw_out=grad_out(w), db_out=grad_out(b),
+                               dx_addend=dx_addend)
+
+    def bw_add(g, pending):
+        # x already has a pending gradient (the residual path): the kernel
+        # writes pending + dx, the engine's own sum, in the same pass
+        if not pending.is_contiguous or pending.dtype != xd.dtype or pending.shape != xd.shape:
+            return None
+        return bw(g, dx_addend=pending)
+    bw.with_addend = (0, bw_add)
     return Tensor._make(y, (x, w, b), bw)
 
 

@@ -282,8 +282,10 @@ def _out_or_new(out, shape, dtype, what):
 
 
 def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceArray, rstd: DeviceArray,
-                  dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None):
-    """Returns (dx, dw, db); dw / db are written into dw_out / db_out when given."""
+                  dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None,
+                  dx_addend: DeviceArray | None = None):
+    """Returns (dx, dw, db); dw / db are written into dw_out / db_out when given.
+    With dx_addend, dx = dx_addend + the input gradient (a new array)."""
     _contig(dy, x, w, mean, rstd)
     if dy.shape != x.shape:
         raise ValueError("layernorm_bwd: dy/x shape mismatch")
@@ -294,8 +296,15 @@ def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceA
     dx = empty(x.shape, x.dtype)
     dw = _out_or_new(dw_out, (C_,), x.dtype, "layernorm_bwd")
     db = _out_or_new(db_out, (C_,), x.dtype, "layernorm_bwd")
-    _c("dtmi_layernorm_bwd", _dt(dy, x, w, mean, rstd), dx.ptr, dw.ptr, db.ptr, dy.ptr, x.ptr, w.ptr, mean.ptr,
-       rstd.ptr, rows, C_, 0)
+    if dx_addend is None:
+        _c("dtmi_layernorm_bwd", _dt(dy, x, w, mean, rstd), dx.ptr, dw.ptr, db.ptr, dy.ptr, x.ptr, w.ptr, mean.ptr,
+           rstd.ptr, rows, C_, 0)
+    else:
+        _contig(dx_addend)
+        if dx_addend.shape != x.shape or dx_addend.dtype != x.dtype:
+            raise ValueError("layernorm_bwd: dx_addend must match x in shape and dtype")
+        _c("dtmi_layernorm_bwd_add", _dt(dy, x, w, mean, rstd, dx_addend), dx.ptr, dw.ptr, db.ptr, dy.ptr, x.ptr,
+           w.ptr, mean.ptr, rstd.ptr, dx_addend.ptr, rows, C_, 0)
     return dx, dw, db
 
 

@@ -198,6 +198,14 @@ int dtmi_layernorm_fwd(int dtype, void* y, void* mean, void* rstd, const void* x
                        int64_t rows, int64_t cols, double eps);
 int dtmi_layernorm_bwd(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x, const void* w,
                        const void* mean, const void* rstd, int64_t rows, int64_t cols, int accumulate);
+/* dtmi_layernorm_bwd with dx = dx_addend + (the LayerNorm input gradient): the
+ * backward engine's sum of a second gradient into one already pending for the
+ * same tensor (dtrain/autograd.py:193, grads[k] + pg), done in the LayerNorm
+ * pass instead of a separate add; the same bits. dx_addend is a separate
+ * buffer (not dx); accumulate bit 0 must be clear, bit 1 as above. */
+int dtmi_layernorm_bwd_add(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x, const void* w,
+                           const void* mean, const void* rstd, const void* dx_addend, int64_t rows, int64_t cols,
+                           int accumulate);
 
 /* --------------------------------------------------------- cross entropy
  * dtrain/autograd.py:250-266 over logits [rows, vocab] and int64 targets.

@@ -87,6 +87,42 @@ def test_layer_norm_attention_embedding_ops(dev):
             rng.standard_normal((3, 4)))
 
 
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+def test_residual_gradient_summed_in_layernorm_pass(dev, dt):
+    """z = x + layer_norm(x) @ m: x's residual gradient is pending when the
+    LayerNorm backward runs, which then adds its input gradient onto it in its
+    own pass. Same bits as the engine's separate sum, and the oracle's values."""
+    A = _api()[0]
+    r = np.random.default_rng(21)
+    x0 = r.standard_normal((4, 16, 64)).astype(dt)
+    w0 = (1 + 0.1 * r.standard_normal(64)).astype(dt)
+    b0 = (0.1 * r.standard_normal(64)).astype(dt)
+    m0 = (0.1 * r.standard_normal((64, 64))).astype(dt)
+    c0 = r.standard_normal((4, 16, 64)).astype(dt)
+
+    def run(fuse):
+        x, w, b = (A.Tensor(a, requires_grad=True) for a in (x0, w0, b0))
+        h = A.layer_norm(x, w, b)
+        used = []
+        if fuse:
+            i, f = h._backward.with_addend
+            h._backward.with_addend = (i, lambda g, p: used.append(f(g, p)) or used[-1])
+        else:
+            del h._backward.with_addend
+        z = x + h @ A.Tensor(m0)
+        (z * A.Tensor(c0)).sum().backward()
+        assert len(used) == (1 if fuse else 0) and all(u is not None for u in used)
+        return x.grad.numpy(), w.grad.numpy(), b.grad.numpy()
+    fused, plain = run(True), run(False)
+    for a, p in zip(fused, plain):
+        assert bits_equal(a, p)
+    _, cache = ops.layer_norm_fwd(x0, w0, b0)
+    gx, gw, gb = ops.layer_norm_bwd(c0 @ m0.T, cache, w0)
+    tol = 1e-12 if dt == np.float64 else 1e-5
+    for a, ref in zip(fused, (c0 + gx, gw, gb)):
+        assert rel_err(a, ref) <= tol
+
+
 def test_cross_entropy(dev):
     A = _api()[0]
     t = rng.integers(0, 5, size=(2, 3))

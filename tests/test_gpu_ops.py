@@ -45,6 +45,27 @@ def test_layernorm_forward_backward(dev, dt, shape):
     assert bits_equal(dx2.numpy(), dx.numpy()) and bits_equal(dw2.numpy(), dw.numpy())
 
 
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("shape", [(4096, 768), (33, 1000), (3, 17)])
+def test_layernorm_backward_with_addend_bits(dev, dt, shape):
+    """dtmi_layernorm_bwd_add: dx = addend + the input gradient in the same
+    pass, bit for bit the separate sum addend + dx (the backward engine's
+    order); dgamma and dbeta unchanged."""
+    D, K = _dev()
+    rng = np.random.default_rng(shape[0] + shape[1])
+    C = shape[-1]
+    x = D.from_numpy(rng.standard_normal(shape).astype(dt))
+    w = D.from_numpy((1 + 0.01 * rng.standard_normal(C)).astype(dt))
+    b = D.from_numpy((0.01 * rng.standard_normal(C)).astype(dt))
+    g = D.from_numpy(rng.standard_normal(shape).astype(dt))
+    pend = D.from_numpy(rng.standard_normal(shape).astype(dt))
+    _, mean, rstd = K.layernorm_fwd(x, w, b)
+    dx, dw, db = K.layernorm_bwd(g, x, w, mean, rstd)
+    dxa, dwa, dba = K.layernorm_bwd(g, x, w, mean, rstd, dx_addend=pend)
+    assert bits_equal(dxa.numpy(), K.binary("add", pend, dx).numpy())
+    assert bits_equal(dwa.numpy(), dw.numpy()) and bits_equal(dba.numpy(), db.numpy())
+
+
 @pytest.mark.parametrize("shape", [(40, 3000), (1100, 4096)])
 def test_layernorm_long_float32_rows(dev, shape):
     """float32 rows of 12 and 16 vectors per lane: the backward loads each
