@@ -941,7 +941,10 @@ static int attn_fwd_impl(AttnArgs& a) {
   return DTMI_OK;
 }
 
-constexpr double kMaxDsBytes = 4.0 * (1 << 30);
+// Largest dS workspace (bytes) the backward takes from the pool; above it the
+// dQ pass recomputes S, P and dP itself. 4 GiB by default; settable so that
+// the recompute path can be exercised at any size.
+static int64_t g_max_ds_bytes = (int64_t)4 << 30;
 
 template <typename T>
 static int attn_bwd_impl(AttnArgs& a) {
@@ -953,11 +956,11 @@ static int attn_bwd_impl(AttnArgs& a) {
   int rc = pool_alloc(&drow, (size_t)rows * sizeof(T));
   if (rc) return rc;
   a.drow = drow;
-  // dS for the dQ pass: B*H*T*T elements, up to kMaxDsBytes; beyond that the
-  // dQ pass recomputes S, P and dP itself.
+  // dS for the dQ pass: B*H*T*T elements, up to g_max_ds_bytes; beyond that
+  // the dQ pass recomputes S, P and dP itself.
   a.ds = nullptr;
   const double ds_bytes = (double)a.B * a.H * a.T * a.T * sizeof(T);
-  if (ds_bytes <= kMaxDsBytes) {
+  if (ds_bytes <= (double)g_max_ds_bytes) {
     rc = pool_alloc(&a.ds, (size_t)ds_bytes);
     if (rc) {
       pool_free(drow);
@@ -1081,5 +1084,14 @@ DTMI_EXPORT int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_
               : 0;
   if (dtype == DTMI_F32) return attn_bwd_impl<float>(a);
   return attn_bwd_impl<double>(a);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_attn_set_ds_limit(int64_t bytes, int64_t* previous) {
+  DTMI_BODY_BEGIN
+  DTMI_CHECK(bytes >= 0, "dtmi_attn_set_ds_limit: negative limit");
+  if (previous) *previous = g_max_ds_bytes;
+  g_max_ds_bytes = bytes;
+  return DTMI_OK;
   DTMI_BODY_END
 }

@@ -417,7 +417,14 @@ DTMI_EXPORT int dtmi_layernorm_bwd_add(int dtype, void* dx, void* dw, void* db, 
     return rc ? rc : dtmi_fill(dtype, db, 0.0, cols);
   }
   DTMI_CHECK(dx && dy && x && w && mean && rstd && dx_addend, "dtmi_layernorm_bwd_add: NULL pointer");
-  DTMI_CHECK(dx_addend != dx, "dtmi_layernorm_bwd_add: the addend must not be dx (use accumulate bit 0)");
+  {
+    // dx is written while other waves still read rows of the addend: the two
+    // byte ranges must be disjoint (an exact alias is what accumulate bit 0 does)
+    const size_t bytes = (size_t)rows * (size_t)cols * (dtype == DTMI_F32 ? 4 : 8);
+    const uintptr_t a0 = (uintptr_t)dx_addend, d0 = (uintptr_t)dx;
+    DTMI_CHECK(a0 + bytes <= d0 || d0 + bytes <= a0,
+               "dtmi_layernorm_bwd_add: the addend overlaps dx (for dx += use accumulate bit 0 instead)");
+  }
   if (dtype == DTMI_F32)
     return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, dx_addend, rows, cols, accumulate);
   return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, dx_addend, rows, cols, accumulate);

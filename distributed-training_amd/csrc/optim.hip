@@ -316,18 +316,70 @@ __device__ __forceinline__ double sq64(T x) {
 }
 
 // ------------------------------------------------- fixed-order average
-// out[i] = (((rep_0[i] + rep_1[i]) + ...) + rep_{W-1}[i]) * inv; with SUMSQ the
-// block's float64 sum of out^2 goes to partials[blockIdx.x] (fixed pattern).
-// WC > 0 fixes the replica count at compile time (the vector path then loads
-// all replicas at once); WC = 0 takes it from `world`.
-template <typename T, bool VEC, bool SUMSQ, int WC>
+// out[i] = (((rep_a[i] + rep_b[i]) + ...) + rep_z[i]) * inv, where the ranks
+// a, b, ..., z are first, first + 1, ..., first - 1 (mod W) and `first` is the
+// rank order's start for the segment holding element i: 0 everywhere for
+// dtrain's direct all-reduce (comm.py:374-391); for its ring all-reduce
+// (comm.py:292-303, 342-372) chunk c of a bucket buffer is summed starting at
+// rank c. Segments are contiguous ranges of out given by value (at most
+// kMaxSegs per launch); a block inside one segment reads its replica rows in
+// that segment's rank order, so the vector path is the same for every order.
+// With SUMSQ the block's float64 sum of out^2 goes to partials[blockIdx.x]
+// (fixed pattern). WC > 0 fixes the replica count at compile time (the vector
+// path then loads all replicas at once); WC = 0 takes it from `world`.
+constexpr int kMaxSegs = 32;
+struct RankSegs {
+  int64_t start[kMaxSegs + 1];  // start[0] = 0, start[nseg] = n
+  int first[kMaxSegs];
+  int nseg;
+};
+
+// The first rank of element k's segment (a compare per segment, all indices
+// compile-time constants, so the table stays in scalar kernel-argument loads).
+__device__ __forceinline__ int seg_first(const RankSegs& sg, int64_t k) {
+  int f = sg.first[0];
+#pragma unroll
+  for (int j = 1; j < kMaxSegs; ++j)
+    if (j < sg.nseg && k >= sg.start[j]) f = sg.first[j];
+  return f;
+}
+
+template <typename T, bool VEC, bool SUMSQ, int WC, bool ROT>
 __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out, const T* __restrict__ rep,
                                                               int world, int64_t n, int64_t stride, T inv,
-                                                              double* __restrict__ partials) {
+                                                              double* __restrict__ partials, RankSegs sg) {
   __shared__ double lds[4];
   const int64_t base = (int64_t)blockIdx.x * kBlockElems;
+  // rank order of the block: uniform when the block lies in one segment
+  int bfirst = 0;
+  bool mixed = false;
+  if (ROT) {
+    const int64_t bend = base + kBlockElems < n ? base + kBlockElems : n;
+    bfirst = seg_first(sg, base);
+    mixed = seg_first(sg, bend - 1) != bfirst;
+#pragma unroll
+    for (int j = 1; j < kMaxSegs; ++j)  // a segment boundary strictly inside the block
+      if (j < sg.nseg && sg.start[j] > base && sg.start[j] < bend) mixed = true;
+  }
+  // replica row of position r in the block's order
+  auto row = [&](int r) {
+    int q = bfirst + r;
+    q = q >= world ? q - world : q;
+    return rep + (int64_t)q * stride;
+  };
+  // element k in its own segment's order (blocks that straddle segments)
+  auto elem = [&](int64_t k) {
+    const int f = ROT && mixed ? seg_first(sg, k) : bfirst;
+    T a = rep[(int64_t)f * stride + k];
+    for (int r = 1; r < world; ++r) {
+      int q = f + r;
+      q = q >= world ? q - world : q;
+      a = a + rep[(int64_t)q * stride + k];
+    }
+    return a;
+  };
   double acc = 0.0;
-  if (VEC) {
+  if (VEC && !(ROT && mixed)) {
     using VT = typename V16<T>::type;
     constexpr int N = V16<T>::N;
     constexpr int PER = kBlockElems / 256 / N;
@@ -339,16 +391,16 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
         VT a;
         if constexpr (WC > 0) {
           // WC replicas known at compile time: every load is issued before
-          // the first add, and the adds keep rank order
+          // the first add, and the adds keep the rank order
           VT v[WC];
 #pragma unroll
-          for (int r = 0; r < WC; ++r) v[r] = ld_nt(reinterpret_cast<const VT*>(rep + (int64_t)r * stride) + k);
+          for (int r = 0; r < WC; ++r) v[r] = ld_nt(reinterpret_cast<const VT*>(row(r)) + k);
           a = v[0];
 #pragma unroll
           for (int r = 1; r < WC; ++r) a = a + v[r];
         } else {
-          a = ld_nt(reinterpret_cast<const VT*>(rep) + k);
-          for (int r = 1; r < world; ++r) a = a + ld_nt(reinterpret_cast<const VT*>(rep + (int64_t)r * stride) + k);
+          a = ld_nt(reinterpret_cast<const VT*>(row(0)) + k);
+          for (int r = 1; r < world; ++r) a = a + ld_nt(reinterpret_cast<const VT*>(row(r)) + k);
         }
         a = a * inv;
         if (SUMSQ)
@@ -357,9 +409,7 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
         st_nt(a, reinterpret_cast<VT*>(out) + k);
       } else if (e0 < n) {
         for (int64_t k = e0; k < n; ++k) {  // ragged end
-          T a = rep[k];
-          for (int r = 1; r < world; ++r) a = a + rep[(int64_t)r * stride + k];
-          T o = a * inv;
+          T o = elem(k) * inv;
           out[k] = o;
           if (SUMSQ) acc += sq64(o);
         }
@@ -367,9 +417,7 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
     }
   } else {
     for (int64_t k = base + threadIdx.x; k < base + kBlockElems && k < n; k += 256) {
-      T a = rep[k];
-      for (int r = 1; r < world; ++r) a = a + rep[(int64_t)r * stride + k];
-      T o = a * inv;
+      T o = elem(k) * inv;
       out[k] = o;
       if (SUMSQ) acc += sq64(o);
     }
@@ -567,12 +615,11 @@ DTMI_EXPORT int dtmi_bucket_flatten(int dtype, void* dst, const void* const* src
   DTMI_BODY_END
 }
 
-template <typename T>
-static int launch_average(void* out, const void* rep, int world, int64_t n, int64_t stride, double inv_w,
-                          double* partials) {
+template <typename T, bool ROT>
+static int launch_average_t(void* out, const void* rep, int world, int64_t n, int64_t stride, double inv_w,
+                            double* partials, const RankSegs& sg) {
   bool vec = aligned(out, 16) && aligned(rep, 16) && ((stride * (int64_t)sizeof(T)) % 16 == 0);
   int grid = average_grid(n);
-  TimedLaunch tl(DTMI_FAM_BUCKET_AVG, (double)(world + 1) * (double)n * sizeof(T));
   T inv = (T)inv_w;
   T* O = (T*)out;
   const T* R = (const T*)rep;
@@ -580,9 +627,11 @@ static int launch_average(void* out, const void* rep, int world, int64_t n, int6
     auto go = [&](auto wc) {
       constexpr int WC = decltype(wc)::value;
       if (partials)
-        bucket_average_kernel<T, true, true, WC><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
+        bucket_average_kernel<T, true, true, WC, ROT>
+            <<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials, sg);
       else
-        bucket_average_kernel<T, true, false, WC><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
+        bucket_average_kernel<T, true, false, WC, ROT>
+            <<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials, sg);
     };
     switch (world) {
       case 2: go(std::integral_constant<int, 2>{}); break;
@@ -592,11 +641,56 @@ static int launch_average(void* out, const void* rep, int world, int64_t n, int6
     }
   } else {
     if (partials)
-      bucket_average_kernel<T, false, true, 0><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
+      bucket_average_kernel<T, false, true, 0, ROT><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv,
+                                                                                 partials, sg);
     else
-      bucket_average_kernel<T, false, false, 0><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials);
+      bucket_average_kernel<T, false, false, 0, ROT><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv,
+                                                                                  partials, sg);
   }
   LAUNCH_CHECK("bucket_average_kernel");
+  return DTMI_OK;
+}
+
+// One launch per run of at most kMaxSegs segments, each over its own element
+// range (sum-of-squares partials are taken only with a single launch).
+template <typename T>
+static int launch_average(void* out, const void* rep, int world, int64_t n, int64_t stride, double inv_w,
+                          double* partials, const int64_t* seg_start, const int* seg_first, int nseg) {
+  TimedLaunch tl(DTMI_FAM_BUCKET_AVG, (double)(world + 1) * (double)n * sizeof(T));
+  RankSegs sg{};
+  bool rot = false;
+  for (int s = 0; s < nseg; ++s) rot = rot || seg_first[s] != 0;
+  if (!rot || world <= 2) {  // one order for all (for W <= 2 every order gives the same bits)
+    sg.nseg = 1;
+    sg.start[1] = n;
+    return launch_average_t<T, false>(out, rep, world, n, stride, inv_w, partials, sg);
+  }
+  int s0 = 0;
+  int64_t done_blocks = 0;
+  while (s0 < nseg) {
+    const int cnt = nseg - s0 < kMaxSegs ? nseg - s0 : kMaxSegs;
+    const int64_t lo = seg_start[s0], hi = s0 + cnt < nseg ? seg_start[s0 + cnt] : n;
+    sg.nseg = cnt;
+    for (int j = 0; j < cnt; ++j) {
+      sg.start[j] = seg_start[s0 + j] - lo;
+      sg.first[j] = seg_first[s0 + j];
+    }
+    sg.start[cnt] = hi - lo;
+    int rc = launch_average_t<T, true>((T*)out + lo, (const T*)rep + lo, world, hi - lo, stride, inv_w,
+                                       partials ? partials + done_blocks : nullptr, sg);
+    if (rc) return rc;
+    done_blocks += average_grid(hi - lo);
+    s0 += cnt;
+  }
+  return DTMI_OK;
+}
+
+static int check_average(int world, int64_t n, const void* out, const void* replicas, int64_t replica_stride,
+                         const char* who) {
+  DTMI_CHECK(world >= 1, "%s: world must be >= 1 (got %d)", who, world);
+  DTMI_CHECK(out && replicas, "%s: NULL pointer", who);
+  DTMI_CHECK(world == 1 || replica_stride >= n, "%s: replica_stride %lld < n %lld", who, (long long)replica_stride,
+             (long long)n);
   return DTMI_OK;
 }
 
@@ -609,12 +703,41 @@ DTMI_EXPORT int dtmi_bucket_average(int dtype, void* out, const void* replicas, 
   if (nblocks) *nblocks = n > 0 ? average_grid(n) : 0;
   if (sumsq_partials == nullptr && nblocks != nullptr && out == nullptr) return DTMI_OK;  // size query
   if (n == 0) return DTMI_OK;
-  DTMI_CHECK(world >= 1, "dtmi_bucket_average: world must be >= 1 (got %d)", world);
-  DTMI_CHECK(out && replicas, "dtmi_bucket_average: NULL pointer");
-  DTMI_CHECK(world == 1 || replica_stride >= n, "dtmi_bucket_average: replica_stride %lld < n %lld",
-             (long long)replica_stride, (long long)n);
-  if (dtype == DTMI_F32) return launch_average<float>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials);
-  return launch_average<double>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials);
+  int rc = check_average(world, n, out, replicas, replica_stride, "dtmi_bucket_average");
+  if (rc) return rc;
+  const int64_t s0 = 0;
+  const int f0 = 0;
+  if (dtype == DTMI_F32)
+    return launch_average<float>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials, &s0, &f0, 1);
+  return launch_average<double>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials, &s0, &f0, 1);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_bucket_average_ring(int dtype, void* out, const void* replicas, int world, int64_t n,
+                                         int64_t replica_stride, double inv_w, const int64_t* seg_start,
+                                         const int* seg_first, int nseg, double* sumsq_partials) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(n >= 0, "dtmi_bucket_average_ring: negative size");
+  if (n == 0) return DTMI_OK;
+  int rc = check_average(world, n, out, replicas, replica_stride, "dtmi_bucket_average_ring");
+  if (rc) return rc;
+  DTMI_CHECK(nseg >= 1 && seg_start && seg_first, "dtmi_bucket_average_ring: need at least one segment");
+  DTMI_CHECK(seg_start[0] == 0, "dtmi_bucket_average_ring: the first segment must start at 0");
+  for (int s = 0; s < nseg; ++s) {
+    DTMI_CHECK(seg_first[s] >= 0 && seg_first[s] < world, "dtmi_bucket_average_ring: segment %d starts at rank %d",
+               s, seg_first[s]);
+    DTMI_CHECK((s + 1 < nseg ? seg_start[s + 1] : n) > seg_start[s],
+               "dtmi_bucket_average_ring: segment starts must increase inside [0, n)");
+  }
+  DTMI_CHECK(sumsq_partials == nullptr || nseg <= kMaxSegs,
+             "dtmi_bucket_average_ring: sum-of-squares partials need at most %d segments", kMaxSegs);
+  if (dtype == DTMI_F32)
+    return launch_average<float>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials, seg_start,
+                                 seg_first, nseg);
+  return launch_average<double>(out, replicas, world, n, replica_stride, inv_w, sumsq_partials, seg_start,
+                                seg_first, nseg);
   DTMI_BODY_END
 }
 

@@ -47,6 +47,7 @@ SIGNATURES: dict[str, list] = {
     "dtmi_adamw_multi": [i32, i32, pvp, pvp, pvp, pvp, pi64, f64, f64, f64, f64, f64, f64, f64, f64, f64, f64, vp],
     "dtmi_bucket_flatten": [i32, vp, pvp, pi64, i32],
     "dtmi_bucket_average": [i32, vp, vp, i32, i64, i64, f64, vp, pi64],
+    "dtmi_bucket_average_ring": [i32, vp, vp, i32, i64, i64, f64, pi64, C.POINTER(C.c_int), i32, vp],
     "dtmi_sumsq": [i32, pvp, pi64, i32, vp],
     "dtmi_sumsq_finish": [vp, i64, vp, i32],
     "dtmi_clip_scale": [vp, f64, vp, vp],
@@ -80,6 +81,7 @@ SIGNATURES: dict[str, list] = {
     "dtmi_attn_fwd": [i32, i64, i64, i64, i64, f64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, vp],
     "dtmi_attn_bwd": [i32, i64, i64, i64, i64, f64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, vp,
                       vp, pi64, vp, pi64, vp, pi64],
+    "dtmi_attn_set_ds_limit": [i64, pi64],
 }
 
 _lib = None

@@ -31,11 +31,9 @@ replica r is row r, columns [lo, hi). The averaged gradients go to one [n]
 buffer in the same order, so after `finish()` the `param.grad` views are
 back to back and the optimizer runs as one flat launch. Element order inside
 a bucket differs from dtrain's concatenation order (reverse definition
-order); the reduction is elementwise, so no value changes.
-
-The ring order of dtrain's default `--algo ring` (each chunk starts at a
-different rank, comm.py:342-372) is not reproduced; see the module docstring
-of dtmi.replicas.
+order); the reduction is elementwise, and for the ring order each bucket
+carries where dtrain's chunks fall in this layout (dtmi.replicas.
+ring_segments), so no value changes.
 """
 from __future__ import annotations
 
@@ -47,7 +45,7 @@ import numpy as np
 from . import device as dev
 from . import kernels as K
 from .device import DeviceArray
-from .replicas import ReplicaGrads
+from .replicas import ReplicaGrads, ring_segments
 
 
 def bucket_layout(sizes, itemsize, bucket_mb=1.0):
@@ -67,7 +65,7 @@ def bucket_layout(sizes, itemsize, bucket_mb=1.0):
 
 
 class _Bucket:
-    def __init__(self, idx, grads: ReplicaGrads, avg: DeviceArray):
+    def __init__(self, idx, grads: ReplicaGrads, avg: DeviceArray, algo: str):
         self.idx = idx  # parameter indices, reverse definition order (dtrain's bucket order)
         self.params = [grads.params[i] for i in idx]
         self.lo = grads.offsets[min(idx)]
@@ -76,6 +74,10 @@ class _Bucket:
         self.rows = grads.columns(self.lo, self.hi)  # [W, n]: every replica's gradients of this bucket
         self.out = avg[self.lo:self.hi]  # averaged gradients of this bucket
         world = grads.pg.world
+        # rank orders of the all-reduce over this bucket (None: rank 0 first)
+        self.segments = None
+        if algo == "ring" and world > 2:
+            self.segments = ring_segments([grads.params[i].data.size for i in sorted(idx)], world)
         self.ready = [set() for _ in range(world)]
         self.flushed = [False] * world
         self.reduced = False
@@ -87,7 +89,7 @@ class _Bucket:
 
 
 class DDP:
-    def __init__(self, model, pg, bucket_mb: float = 1.0, overlap: bool = True, algo: str = "direct"):
+    def __init__(self, model, pg, bucket_mb: float = 1.0, overlap: bool = True, algo: str = "ring"):
         if algo not in ("direct", "ring"):
             raise ValueError(f"unknown algo {algo!r}")
         self.model, self.pg, self.overlap, self.algo = model, pg, overlap, algo
@@ -98,7 +100,7 @@ class DDP:
         sizes = [p.data.size for p in self.params]
         self.grads = ReplicaGrads(self.params, pg, dtype)
         self.avg = dev.empty((max(self.grads.n, 1),), dtype)
-        self.buckets = [_Bucket(idx, self.grads, self.avg)
+        self.buckets = [_Bucket(idx, self.grads, self.avg, algo)
                         for idx in bucket_layout(sizes, np.dtype(dtype).itemsize, bucket_mb)]
         self._where = {}
         for bi, b in enumerate(self.buckets):
@@ -130,7 +132,7 @@ class DDP:
         if b.reduced or b.n == 0:
             b.reduced = True
             return
-        self.pg.average(b.out, b.rows)
+        self.pg.average(b.out, b.rows, segments=b.segments)
         b.reduced = True
 
     def _on_grad(self, p):

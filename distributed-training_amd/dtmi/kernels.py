@@ -221,9 +221,12 @@ def average_blocks(n: int) -> int:
 
 
 def bucket_average(out: DeviceArray, replicas: DeviceArray, world: int, inv_w: float,
-                   partials: DeviceArray | None = None):
-    """out[i] = fixed rank-order sum of replicas[r, i] times inv_w; replicas is a
-    [W, n] array or a column slice of one (row stride >= n, unit column stride)."""
+                   partials: DeviceArray | None = None, segments=None):
+    """out[i] = rank-order sum of replicas[r, i] times inv_w; replicas is a
+    [W, n] array or a column slice of one (row stride >= n, unit column
+    stride). The order is rank 0 first (dtrain's direct all-reduce) unless
+    `segments` lists (start, first_rank) pairs: elements from `start` on are
+    then summed starting at `first_rank` (dtrain's ring order)."""
     _contig(out)
     if replicas.ndim != 2 or replicas.shape[0] != world or replicas.shape[1] != out.size:
         raise ValueError("bucket_average: replicas must be [world, n]")
@@ -232,8 +235,14 @@ def bucket_average(out: DeviceArray, replicas: DeviceArray, world: int, inv_w: f
     stride = replicas.strides[0] if world > 1 else replicas.shape[1]
     if partials is not None and (partials.dtype != np.float64 or partials.size < average_blocks(out.size)):
         raise ValueError("bucket_average: partials too small")
-    _c("dtmi_bucket_average", _dt(out, replicas), out.ptr, replicas.ptr, int(world), out.size, int(stride),
-       float(inv_w), partials.ptr if partials is not None else None, None)
+    if segments is None:
+        _c("dtmi_bucket_average", _dt(out, replicas), out.ptr, replicas.ptr, int(world), out.size, int(stride),
+           float(inv_w), partials.ptr if partials is not None else None, None)
+        return
+    starts = _lib.i64_array([int(s) for s, _ in segments])
+    firsts = (C.c_int * len(segments))(*[int(f) for _, f in segments])
+    _c("dtmi_bucket_average_ring", _dt(out, replicas), out.ptr, replicas.ptr, int(world), out.size, int(stride),
+       float(inv_w), starts, firsts, len(segments), partials.ptr if partials is not None else None)
 
 
 def sumsq(arrays, out: DeviceArray):
@@ -548,3 +557,11 @@ def attn_bwd(q, k, v, o, dO, rowmax, rowsum, dq=None, dk=None, dv=None, scale=No
        o.ptr, _bht_strides(o), dO.ptr, _bht_strides(dO), rowmax.ptr, rowsum.ptr, dq.ptr, _bht_strides(dq), dk.ptr,
        _bht_strides(dk), dv.ptr, _bht_strides(dv))
     return dq, dk, dv
+
+
+def attn_set_ds_limit(nbytes: int) -> int:
+    """Bound the attention backward's dS workspace (bytes; 0 makes the dQ pass
+    recompute dS). Returns the previous bound."""
+    prev = C.c_int64()
+    _c("dtmi_attn_set_ds_limit", int(nbytes), C.byref(prev))
+    return prev.value

@@ -5,8 +5,12 @@ dtrain runs one process per rank and sums gradients over TCP
 replica runs its forward/backward in turn on the shared parameters (identical
 on every rank, which is what dtrain's broadcast from rank 0 establishes) and
 leaves its gradient buckets in its own rows of HBM; the all-reduce becomes one
-fixed-order on-device reduction over the rows, in dtrain's direct-algorithm
-order (rank 0 first, then 1, 2, ...; dtrain/comm.py:374-391).
+on-device reduction over the rows in the rank order dtrain's collective would
+use: its direct algorithm sums rank 0 first, then 1, 2, ...
+(dtrain/comm.py:374-391); its ring (comm.py:292-303, 342-372, the default)
+cuts a buffer into partition(n, W) chunks and sums chunk c starting at rank
+c, (x_c + x_{c+1}) + ... + x_{c-1}. `ring_segments` maps those chunks onto
+this build's layout, so either order gives dtrain's bits.
 
 `SimGroup` stands where dtrain's ProcessGroup stands for DDP and ZeroAdamW:
 `.rank` (the replica currently running), `.world`, `broadcast`, `barrier`,
@@ -72,9 +76,41 @@ class SimGroup:
     def barrier(self):
         _lib.sync()
 
-    def average(self, out: DeviceArray, rows: DeviceArray, partials: DeviceArray | None = None):
-        """out = (((rows[0] + rows[1]) + ...) + rows[W-1]) * (1.0 / W)."""
-        K.bucket_average(out, rows, self.world, 1.0 / self.world, partials=partials)
+    def average(self, out: DeviceArray, rows: DeviceArray, partials: DeviceArray | None = None, segments=None):
+        """out = (((rows[0] + rows[1]) + ...) + rows[W-1]) * (1.0 / W), or in
+        the rank orders of `segments` ((start, first_rank) pairs, see
+        ring_segments)."""
+        K.bucket_average(out, rows, self.world, 1.0 / self.world, partials=partials, segments=segments)
+
+
+def ring_segments(sizes, world: int):
+    """Where dtrain's ring chunks fall in this build's bucket layout.
+
+    dtrain concatenates a bucket's parameters in REVERSE definition order
+    (dtrain/ddp.py:27-37, 46-56) and its ring all-reduce sums chunk c of
+    partition(n, W) of that buffer starting at rank c (comm.py:342-372). Here
+    the same parameters sit in forward order. `sizes` are the bucket's
+    parameter sizes in forward order; returns (start, first_rank) pairs in
+    ascending start over the forward-order buffer (consecutive pieces with the
+    same first rank merged): element i is summed starting at the first_rank
+    of the last pair whose start <= i."""
+    n = sum(sizes)
+    bounds = partition(n, world)
+    # offset of each parameter in dtrain's (reversed) buffer
+    dofs, off = [0] * len(sizes), 0
+    for i in reversed(range(len(sizes))):
+        dofs[i] = off
+        off += sizes[i]
+    segs = []
+    o = 0
+    for i, k in enumerate(sizes):
+        a, b = dofs[i], dofs[i] + k
+        for c in range(world):
+            lo, hi = max(a, bounds[c]), min(b, bounds[c + 1])
+            if lo < hi and (not segs or segs[-1][1] != c):
+                segs.append((o + lo - a, c))
+        o += k
+    return segs or [(0, 0)]
 
 
 class ReplicaGrads:

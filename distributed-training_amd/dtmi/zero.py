@@ -6,10 +6,12 @@ partitioned with dtrain's `partition` and rank r owns flat[b[r]:b[r+1]]
 (`.shard`, `.bounds`). Each replica's backward flattens its gradients into its
 own row of a [W, n] buffer in forward order: the backward kernels write
 each gradient straight into its slot (see dtmi.replicas.ReplicaGrads), where
-zero.py:46-53 flattens after backward. `step()` then, for every shard in rank order: the fixed-order sum of
-the replicas' rows times 1/W (the reduce-scatter plus `g *= 1/W` of
-zero.py:54-55, in dtrain's direct order), its float64 sum of squares, summed
-over shards in rank order (the all-reduce of zero.py:56-57); the clip factor
+zero.py:46-53 flattens after backward. `step()` then, for every shard in rank
+order: the sum of the replicas' rows times 1/W (the reduce-scatter plus
+`g *= 1/W` of zero.py:54-55, in the order of dtrain's ring reduce-scatter,
+comm.py:342-363: shard r is summed starting at rank r,
+(x_r + x_{r+1}) + ... + x_{r-1}), its float64 sum of squares, summed over
+shards in rank order (the all-reduce of zero.py:56-57); the clip factor
 (computed on the device); and AdamW on every shard. AdamW is elementwise, so
 one launch over the whole buffer with one m/v buffer gives the same bits as W
 per-shard optimizers; `.opt` exposes the running rank's shard view of it, and
@@ -137,7 +139,7 @@ class ZeroAdamW:
                 rows = DeviceArray(self.gflat.block, (W, hi - lo), self.gflat.dtype, self.gflat.offset + lo * isz,
                                    (self.n, 1))
                 parts = self._partials[:self._nblocks[r]]
-                K.bucket_average(g[lo:hi], rows, W, 1.0 / W, partials=parts)
+                K.bucket_average(g[lo:hi], rows, W, 1.0 / W, partials=parts, segments=[(0, r)])
                 K.sumsq_finish(parts, self._nblocks[r], sq, accumulate=r > 0)
             elif r == 0:
                 sq.zero_()

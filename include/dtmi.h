@@ -128,6 +128,21 @@ int dtmi_bucket_flatten(int dtype, void* dst, const void* const* srcs, const int
 int dtmi_bucket_average(int dtype, void* out, const void* replicas, int world, int64_t n,
                         int64_t replica_stride, double inv_w, double* sumsq_partials, int64_t* nblocks);
 
+/* The same average with the rank order of dtrain's ring collectives: element i
+ * lies in segment s (seg_start[s] <= i < seg_start[s + 1], seg_start[0] = 0,
+ * the last segment ends at n) and is summed starting at rank seg_first[s]:
+ * ((rep[f] + rep[f+1]) + ...) + rep[f-1] (indices mod world), then * inv_w.
+ * Replaces the ring all-reduce of dtrain/comm.py:292-303 + 342-372 (chunk c
+ * of a bucket, partition(n, W) of its buffer, summed starting at rank c;
+ * dtrain/ddp.py's default algo) and the reduce-scatter of dtrain/zero.py:54
+ * (shard r summed starting at rank r). The host computes where the chunks of
+ * dtrain's bucket buffer (reverse parameter order) fall in this layout.
+ * seg_start / seg_first are host arrays of nseg entries. sumsq_partials as
+ * for dtmi_bucket_average (one launch, so at most 32 segments with it). */
+int dtmi_bucket_average_ring(int dtype, void* out, const void* replicas, int world, int64_t n,
+                             int64_t replica_stride, double inv_w, const int64_t* seg_start, const int* seg_first,
+                             int nseg, double* sumsq_partials);
+
 /* Deterministic sum of squares in f64 over `nt` tensors, two-stage (per-block
  * partials in a fixed grid, then one fixed-order pass). Replaces
  * sum(float(np.dot(g64, g64)) for each grad) of dtrain/train.py:155-156 and
@@ -313,6 +328,12 @@ int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double 
                   const int64_t* dO_strides, const void* rowmax, const void* rowsum, void* dq,
                   const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
                   const int64_t* dv_strides);
+/* The backward's dQ pass reads the dS = P * (dP - rowsum(dO * O)) that its key
+ * pass wrote to a pooled [B, H, T, T] workspace when that takes at most
+ * `bytes` (default 4 GiB), and otherwise recomputes S, P and dP itself (the
+ * same products as dtrain/autograd.py:239-246). Sets the bound (0: always
+ * recompute) and returns the previous one in *previous (if not NULL). */
+int dtmi_attn_set_ds_limit(int64_t bytes, int64_t* previous);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,8 @@
 """DDP bucket layout, flatten and fixed-order average; ZeRO partition and step;
 restated from dtrain/ddp.py, dtrain/zero.py and dtrain/comm.py for W simulated
-ranks held in one process. Test infrastructure only."""
+ranks held in one process. Both of dtrain's all-reduce orders are restated:
+"direct" (rank 0 first) and "ring" (chunk c of a buffer summed starting at
+rank c). Test infrastructure only."""
 from __future__ import annotations
 
 import numpy as np
@@ -51,11 +53,42 @@ def fixed_order_sum(parts):
     return out
 
 
-def ddp_average(replica_grads, itemsize, bucket_mb=1.0):
-    """DDP.finish (dtrain/ddp.py:84-110) with the direct all-reduce, for W
-    replicas' gradient lists: flatten each replica into its buckets (hook copy,
-    ddp.py:73-81; missing grads contribute zeros, ddp.py:88-94), sum buckets in
-    rank order, multiply by 1.0/W, slice back. Returns the averaged grads."""
+def ring_order_sum(parts):
+    """dtrain/comm.py:292-303 with 342-372 (ring all-reduce, reduce-scatter
+    without the ownership rotation, then all-gather): the buffer is cut into
+    partition(n, W) chunks; chunk c travels the ring from rank c, and each hop
+    adds the receiving rank's own chunk to what arrived (`flat[ri] += recv`,
+    commutative), so chunk c is ((x_c + x_{c+1}) + ...) + x_{c-1}."""
+    W = len(parts)
+    out = parts[0].copy()
+    b = partition(out.size, W)
+    for c in range(W):
+        lo, hi = b[c], b[c + 1]
+        acc = parts[c][lo:hi].copy()
+        for j in range(1, W):
+            acc += parts[(c + j) % W][lo:hi]
+        out[lo:hi] = acc
+    return out
+
+
+def allreduce_sum(parts, algo):
+    """ProcessGroup.allreduce (dtrain/comm.py:292-308) for W ranks' buffers."""
+    if len(parts) == 1:
+        return parts[0].copy()
+    if algo == "ring":
+        return ring_order_sum(parts)
+    if algo == "direct":
+        return fixed_order_sum(parts)
+    raise ValueError(algo)
+
+
+def ddp_average(replica_grads, itemsize, bucket_mb=1.0, algo="direct"):
+    """DDP.finish (dtrain/ddp.py:84-110) for W replicas' gradient lists: flatten
+    each replica into its buckets (hook copy, ddp.py:73-81; missing grads
+    contribute zeros, ddp.py:88-94), all-reduce each bucket with `algo`
+    ("direct": rank order; "ring": dtrain's default, chunk c of the bucket
+    starting at rank c), multiply by 1.0/W, slice back. Returns the averaged
+    grads."""
     W = len(replica_grads)
     first = replica_grads[0]
     sizes = [g.size for g in first]
@@ -73,7 +106,7 @@ def ddp_average(replica_grads, itemsize, bucket_mb=1.0):
                 if g is not None:
                     buf[off:off + s] = g.reshape(-1)
             bufs.append(buf)
-        red = fixed_order_sum(bufs)
+        red = allreduce_sum(bufs, algo)
         red *= inv
         for i, off, s in entries:
             out[i] = red[off:off + s].reshape(first[i].shape).copy()
@@ -83,9 +116,11 @@ def ddp_average(replica_grads, itemsize, bucket_mb=1.0):
 class ZeroAdamW:
     """dtrain/zero.py:23-62 for W simulated ranks: one flat parameter buffer in
     forward order, shard r = flat[b[r]:b[r+1]], one AdamW per shard. `step`
-    takes every replica's flat gradient; the reduce-scatter is the fixed rank
-    order sum (comm.py direct order) of each shard, then *= 1/W, float64 sum of
-    squares per shard summed in rank order (the sq all-reduce), clip, AdamW."""
+    takes every replica's flat gradient; the reduce-scatter is dtrain's ring
+    (comm.py:310-316, 342-363: after the ownership rotation rank r holds chunk
+    r, which the ring summed starting at rank r), then *= 1/W, float64 sum of
+    squares per shard summed in rank order (the sq all-reduce: a 1-element
+    ring all-reduce is chunk 0, rank order), clip, AdamW."""
 
     def __init__(self, params, world, max_grad_norm=None, **adam):
         self.world = world
@@ -101,7 +136,9 @@ class ZeroAdamW:
         shards = []
         for r in range(W):
             lo, hi = self.bounds[r], self.bounds[r + 1]
-            g = fixed_order_sum([rg[lo:hi] for rg in replica_flat_grads])
+            g = replica_flat_grads[r][lo:hi].copy()
+            for j in range(1, W):
+                g += replica_flat_grads[(r + j) % W][lo:hi]
             g *= 1.0 / W
             shards.append(g)
         sqs = [float(np.dot(g.astype(np.float64), g.astype(np.float64))) for g in shards]

@@ -2,9 +2,10 @@
 
 `single_step` is `--mode single` (emulate_world W: each virtual rank's loss is
 scaled by 1/(accum*W) and leaf gradients accumulate, train.py:130-145).
-`ddp_step` is `--mode ddp --algo direct` for W ranks simulated in turn: each
-replica's loss is scaled by 1/accum, gradients go through DDP's buckets and the
-fixed rank-order average (ddp.py:84-110), then the global-norm clip
+`ddp_step` is `--mode ddp` for W ranks simulated in turn: each replica's loss
+is scaled by 1/accum, gradients go through DDP's buckets and the average in
+the all-reduce order of `algo` (ddp.py:84-110; "ring" is dtrain's default
+--algo, "direct" sums in rank order), then the global-norm clip
 (train.py:155-158) and AdamW on `p.grad * s` (train.py:159).
 Test infrastructure only.
 """
@@ -37,7 +38,7 @@ def single_step(P, c, batches, opt: AdamW, clip=1.0, emulate_world=1):
     return loss_sum, gnorm, glist
 
 
-def ddp_step(P, c, batches, opt: AdamW, clip=1.0, bucket_mb=1.0):
+def ddp_step(P, c, batches, opt: AdamW, clip=1.0, bucket_mb=1.0, algo="direct"):
     """batches: list (one per simulated rank) of (x, y). Returns
     (mean loss, grad_norm, averaged grads)."""
     names = list(P.keys())
@@ -49,7 +50,7 @@ def ddp_step(P, c, batches, opt: AdamW, clip=1.0, bucket_mb=1.0):
         replica_grads.append([g[k] for k in names])
         losses.append(float(loss))
     itemsize = np.dtype(c.dtype).itemsize
-    avg = ddp_average(replica_grads, itemsize, bucket_mb)
+    avg = ddp_average(replica_grads, itemsize, bucket_mb, algo)
     sq = global_sq_norm(avg)
     gnorm = float(np.sqrt(sq))
     s = clip_scale(sq, clip) if clip else 1.0

@@ -253,17 +253,18 @@ def test_char_gpt_workload_step_float64(dev):
 
 
 @pytest.mark.parametrize("dt", ["float64", "float32"])
-def test_ddp_simulated_replicas_match_oracle(dev, dt):
-    """DDP over 4 simulated replicas (buckets, fixed-order average, clip, AdamW),
-    two steps: averaged gradients, norm and loss against the oracle's DDP step;
-    AdamW bit-exact on the averaged gradients."""
+@pytest.mark.parametrize("algo", ["ring", "direct"])
+def test_ddp_simulated_replicas_match_oracle(dev, dt, algo):
+    """DDP over 4 simulated replicas (buckets, ring or direct order average,
+    clip, AdamW), two steps: averaged gradients, norm and loss against the
+    oracle's DDP step; AdamW bit-exact on the averaged gradients."""
     A, N, O, P, Z, R, S_ = _api()
     cfg = dict(vocab=17, ctx=8, dim=32, heads=4, layers=2)
     oc = OM.GPTConfig(dtype=dt, **cfg)
     xs, ys = OM.synthetic_tokens(oc, batch=3, seed=9, replicas=4)
     m = N.GPT(N.GPTConfig(dtype=dt, **cfg), seed=4)
     pg = R.SimGroup(4)
-    ddp = P.DDP(m, pg, bucket_mb=0.01)
+    ddp = P.DDP(m, pg, bucket_mb=0.01, algo=algo)
     assert len(ddp.buckets) > 1
     opt = O.AdamW([p.data for p in m.parameters()], lr=1e-3)
     shadow = ShadowAdam(m, 1e-3)
@@ -272,7 +273,8 @@ def test_ddp_simulated_replicas_match_oracle(dev, dt):
         Pn = {n: p.numpy() for n, p in m.named_parameters()}  # the oracle starts from the device's parameters
         oopt = OO.AdamW([Pn[n] for n in Pn], lr=1e-3)
         res = S_.step_ddp(m, ddp, opt, [[(xs[r], ys[r])] for r in range(4)], clip=0.5)
-        loss, gnorm, avg = OS.ddp_step(Pn, oc, [(xs[r], ys[r]) for r in range(4)], oopt, clip=0.5, bucket_mb=0.01)
+        loss, gnorm, avg = OS.ddp_step(Pn, oc, [(xs[r], ys[r]) for r in range(4)], oopt, clip=0.5, bucket_mb=0.01,
+                                       algo=algo)
         assert abs(res.loss - loss) <= tol * abs(loss)
         assert abs(res.grad_norm - gnorm) <= tol * gnorm
         for i, (n, p) in enumerate(m.named_parameters()):
@@ -281,8 +283,8 @@ def test_ddp_simulated_replicas_match_oracle(dev, dt):
 
 
 def test_bucket_size_and_overlap_do_not_change_bits(dev):
-    """dtrain tests/test_training.py:75-80 asserts <= 1e-12; with a fixed-order
-    elementwise average the results are bit-identical."""
+    """dtrain tests/test_training.py:75-80 asserts <= 1e-12; with the direct
+    order (rank 0 first for every element) the results are bit-identical."""
     A, N, O, P, Z, R, S_ = _api()
     cfg = N.GPTConfig(vocab=17, ctx=8, dim=32, heads=4, layers=2, dtype="float64")
     oc = OM.GPTConfig(vocab=17, ctx=8, dim=32, heads=4, layers=2, dtype="float64")
@@ -291,12 +293,33 @@ def test_bucket_size_and_overlap_do_not_change_bits(dev):
     for mb, overlap in ((0.001, True), (100.0, True), (0.01, False)):
         m = N.GPT(cfg, seed=1)
         pg = R.SimGroup(4)
-        ddp = P.DDP(m, pg, bucket_mb=mb, overlap=overlap)
+        ddp = P.DDP(m, pg, bucket_mb=mb, overlap=overlap, algo="direct")
         opt = O.AdamW([p.data for p in m.parameters()], lr=1e-3)
         for _ in range(2):
             S_.step_ddp(m, ddp, opt, [[(xs[r], ys[r])] for r in range(4)])
         finals.append(m.flat.numpy())
     assert bits_equal(finals[0], finals[1]) and bits_equal(finals[0], finals[2])
+
+
+def test_overlap_bucket_size_and_algorithm_do_not_change_results(dev):
+    """dtrain tests/test_training.py:75-80: ring with overlap, ring without it at
+    another bucket size, and direct, all within 1e-12 after three steps (the
+    ring's chunk edges move with the bucket size, so bits may differ)."""
+    A, N, O, P, Z, R, S_ = _api()
+    cfg = N.GPTConfig(vocab=17, ctx=8, dim=32, heads=4, layers=2, dtype="float64")
+    oc = OM.GPTConfig(vocab=17, ctx=8, dim=32, heads=4, layers=2, dtype="float64")
+    xs, ys = OM.synthetic_tokens(oc, batch=2, seed=3, replicas=3)
+    finals = []
+    for mb, overlap, algo in ((1.0, True, "ring"), (0.001, False, "ring"), (1.0, True, "direct")):
+        m = N.GPT(cfg, seed=1)
+        pg = R.SimGroup(3)
+        ddp = P.DDP(m, pg, bucket_mb=mb, overlap=overlap, algo=algo)
+        opt = O.AdamW([p.data for p in m.parameters()], lr=1e-3)
+        for _ in range(3):
+            S_.step_ddp(m, ddp, opt, [[(xs[r], ys[r])] for r in range(3)])
+        finals.append(m.flat.numpy())
+    assert np.max(np.abs(finals[0] - finals[1])) <= 1e-12
+    assert np.max(np.abs(finals[0] - finals[2])) <= 1e-12
 
 
 def test_ddp_matches_single_process_emulated_world(dev):
@@ -382,3 +405,98 @@ def test_step_is_deterministic(dev):
             S_.step_ddp(m, ddp, opt, [[(xs[r], ys[r])] for r in range(4)])
         outs.append(m.flat.numpy())
     assert bits_equal(outs[0], outs[1])
+
+
+# ------------------------------------------- dtrain's data-parallel orders
+SHAPES_DDP = [(7, 5), (3,), (13, 4), (1,), (33,), (6, 6), (2,), (41,)]
+
+
+class _Params:
+    """A model of bare parameters (dtrain's DDP/ZeroAdamW only call .parameters())."""
+
+    def __init__(self, A, arrays):
+        self.ps = [A.Tensor(a.copy(), requires_grad=True) for a in arrays]
+
+    def parameters(self):
+        return self.ps
+
+
+@pytest.mark.parametrize("world", [3, 4])
+@pytest.mark.parametrize("dt", ["float64", "float32"])
+@pytest.mark.parametrize("algo", ["ring", "direct"])
+def test_ddp_average_matches_dtrain_fixture(dev, golden, world, dt, algo):
+    """dtrain's DDP over its TCP ring / direct all-reduce (3 and 4 ranks, 256-byte
+    buckets, gradients over 16 decades) bit for bit: the simulated replicas'
+    gradients go through the grad-ready hooks and finish()."""
+    A, N, O, P, Z, R, S_ = _api()
+    from dtmi import device as D
+    G = golden("dtrain_ddp_reduce.npz")
+    n = len(SHAPES_DDP)
+    m = _Params(A, [G[f"w{world}/{dt}/p0/{i}"] for i in range(n)])
+    pg = R.SimGroup(world)
+    ddp = P.DDP(m, pg, bucket_mb=256 / (1 << 20), overlap=True, algo=algo)
+    assert len(ddp.buckets) > 2
+    for r in range(world):
+        with pg.replica(r):
+            for i in reversed(range(n)):
+                p = m.ps[i]
+                p.grad = D.from_numpy(G[f"w{world}/{dt}/g{r}/{i}"])
+                ddp._on_grad(p)
+    ddp.finish()
+    for i, p in enumerate(m.ps):
+        assert bits_equal(p.grad.numpy(), G[f"w{world}/{dt}/ddp_{algo}/{i}"]), i
+
+
+@pytest.mark.parametrize("world", [3, 4])
+@pytest.mark.parametrize("dt", ["float64", "float32"])
+def test_zero_matches_dtrain_fixture(dev, golden, world, dt):
+    """dtrain's ZeroAdamW (ring reduce-scatter, shard r summed from rank r):
+    without clip the parameters after one step are bit-identical; with clip
+    1.0 the norm is within 1e-14 and the parameters within the clip factor's
+    last-bit difference."""
+    A, N, O, P, Z, R, S_ = _api()
+    from dtmi import device as D
+    G = golden("dtrain_ddp_reduce.npz")
+    n = len(SHAPES_DDP)
+    for tag, clip in (("zero_noclip", None), ("zero", 1.0)):
+        m = _Params(A, [G[f"w{world}/{dt}/p0/{i}"] for i in range(n)])
+        pg = R.SimGroup(world)
+        z = Z.ZeroAdamW(m, pg, max_grad_norm=clip, lr=1e-2, weight_decay=0.1)
+        for r in range(world):
+            with pg.replica(r):
+                for i in range(n):
+                    p = m.ps[i]
+                    p.grad = D.from_numpy(G[f"w{world}/{dt}/g{r}/{i}"])
+                    z._on_grad(p)
+        z.step()
+        ref = G[f"w{world}/{dt}/{tag}_flat"]
+        norm = float(G[f"w{world}/{dt}/{tag}_norm"])
+        assert abs(z.last_grad_norm - norm) <= 1e-14 * norm
+        if clip is None:
+            assert bits_equal(z.flat.numpy(), ref)
+        else:
+            assert np.max(np.abs(z.flat.numpy() - ref)) <= 1e-6 * np.max(np.abs(ref))
+
+
+def test_ddp_ring_training_steps_match_dtrain_fixture(dev, golden):
+    """Two steps of dtrain's DDP loop (--algo ring, 3 ranks, clip 0.5, float64):
+    losses, norms and averaged gradients within 1e-12, and AdamW bit-exact on
+    the device's averaged gradients."""
+    A, N, O, P, Z, R, S_ = _api()
+    S = golden("dtrain_ddp_step_float64.npz")
+    cfg = N.GPTConfig(vocab=11, ctx=8, dim=16, heads=2, layers=2, dtype="float64")
+    m = N.GPT(cfg, seed=4)
+    pg = R.SimGroup(3)
+    ddp = P.DDP(m, pg, bucket_mb=0.002)  # dtrain's default algo: ring
+    assert ddp.algo == "ring"
+    opt = O.AdamW([p.data for p in m.parameters()], lr=3e-3, weight_decay=0.1)
+    shadow = ShadowAdam(m, 3e-3)
+    for s in range(2):
+        batches = [[(S[f"s{s}/x{r}"], S[f"s{s}/y{r}"])] for r in range(3)]
+        res = S_.step_ddp(m, ddp, opt, batches, clip=0.5)
+        assert abs(res.loss - float(S[f"s{s}/loss"])) <= 1e-12 * abs(float(S[f"s{s}/loss"]))
+        sq = float(S[f"s{s}/sq"])
+        assert abs(res.grad_norm - np.sqrt(sq)) <= 1e-12 * np.sqrt(sq)
+        for n, p in m.named_parameters():
+            assert rel_err(p.grad.numpy(), S[f"s{s}/g/{n}"]) <= 1e-12, (s, n)
+        shadow.check(m, res.clip_scale)

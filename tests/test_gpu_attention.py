@@ -93,7 +93,25 @@ def test_attention_on_fused_qkv_layout(dev, dt):
     assert rel_err(got[:, :, 2].transpose(0, 2, 1, 3), gv) <= TOL[dt]
 
 
-def test_backward_without_the_ds_workspace_matches_with_it():
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("shape", [(1, 2, 4, 3), (2, 2, 5, 4), (2, 3, 100, 64), (1, 1, 257, 33), (16, 12, 256, 64),
+                                   (1, 2, 384, 64)])
+def test_recompute_dq_path_matches_oracle(dev, dt, shape):
+    """With the dS workspace bound set to 0 the dQ pass recomputes S, P and
+    dP from q, k, v, dO and the row statistics (the path taken above 4 GiB of
+    dS): forward and backward against the oracle at the same bar."""
+    D, K = _dev()
+    rng = np.random.default_rng(sum(shape) + 7)
+    q, k, v, g = (rng.standard_normal(shape).astype(dt) for _ in range(4))
+    prev = K.attn_set_ds_limit(0)
+    try:
+        _check(D, K, q, k, v, g, dt)
+    finally:
+        K.attn_set_ds_limit(prev)
+    assert prev == 4 << 30
+
+
+def test_backward_without_the_ds_workspace_matches_with_it(dev):
     """B*H*T*T float32 above 4 GiB: the dQ pass recomputes dS instead of
     reading it from a workspace. Splitting the heads in two keeps each half
     under the limit (dS path); the two paths must agree."""

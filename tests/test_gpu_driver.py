@@ -65,8 +65,9 @@ def test_overlap_bucket_size_and_algorithm_do_not_change_results(dev, tmp_path, 
     a, _ = train(tmp_path, "a", corpus, "ddp", 3, extra=[*STEPS, "--bucket-mb", "0.001"])
     b, _ = train(tmp_path, "b", corpus, "ddp", 3, extra=[*STEPS, "--no-overlap", "--bucket-mb", "100"])
     c, _ = train(tmp_path, "c", corpus, "ddp", 3, extra=[*STEPS, "--algo", "direct"])
-    assert_close(a, b, 0.0)  # dtrain allows 1e-12; the fixed-order average makes them identical
-    assert_close(a, c, 0.0)
+    # dtrain's tolerance: the ring's chunk edges move with the bucket size
+    assert_close(a, b, 1e-12)
+    assert_close(a, c, 1e-12)
 
 
 def test_gradient_accumulation_matches_larger_batch(dev, tmp_path, corpus):

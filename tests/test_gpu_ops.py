@@ -66,6 +66,30 @@ def test_layernorm_backward_with_addend_bits(dev, dt, shape):
     assert bits_equal(dwa.numpy(), dw.numpy()) and bits_equal(dba.numpy(), db.numpy())
 
 
+def test_layernorm_backward_rejects_an_addend_overlapping_dx(dev):
+    """An addend that shares bytes with dx without being dx (a shifted view of
+    one buffer) is refused before any launch; disjoint neighbours are fine."""
+    import ctypes
+    from dtmi import _lib
+    D, K = _dev()
+    rows, C = 8, 64
+    x = D.from_numpy(np.random.default_rng(0).standard_normal((rows, C)).astype(np.float32))
+    w, b = D.full((C,), 1.0, np.float32), D.zeros((C,), np.float32)
+    g = D.full((rows, C), 0.5, np.float32)
+    _, mean, rstd = K.layernorm_fwd(x, w, b)
+    buf = D.zeros((3 * rows * C,), np.float32)
+    dw, db = D.empty((C,), np.float32), D.empty((C,), np.float32)
+
+    def call(dx_off, add_off):
+        return _lib.lib().dtmi_layernorm_bwd_add(
+            _lib.F32, ctypes.c_void_p(buf.ptr + 4 * dx_off), dw.ptr, db.ptr, g.ptr, x.ptr, w.ptr, mean.ptr, rstd.ptr,
+            ctypes.c_void_p(buf.ptr + 4 * add_off), rows, C, 0)
+    for dx_off, add_off in ((0, 1), (C, 0), (0, rows * C - 1), (0, 0)):
+        assert call(dx_off, add_off) == 1, (dx_off, add_off)  # DTMI_ERR_INVALID
+    assert call(0, rows * C) == 0 and call(2 * rows * C, rows * C) == 0
+    _lib.sync()
+
+
 @pytest.mark.parametrize("shape", [(40, 3000), (1100, 4096)])
 def test_layernorm_long_float32_rows(dev, shape):
     """float32 rows of 12 and 16 vectors per lane: the backward loads each

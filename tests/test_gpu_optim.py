@@ -186,41 +186,126 @@ def test_clip_scale_bit_exact_with_dtrain(dev):
         assert n_dev.numpy()[0] == float(np.sqrt(sq))
 
 
-def test_bucket_average_and_adamw_at_124m_params_float32(dev):
-    """The gradient-bucket + optimizer workload at full size (124,439,808 float32
-    elements, 4 replicas, step 101): bit-exact against the oracle."""
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_bucket_average_and_adamw_at_124m_params(dev, dt):
+    """The gradient-bucket + optimizer workload at full size (124,439,808
+    elements, 4 replicas, step 101) in float32 and float64: the fixed-order
+    average, the clip factor and AdamW over the full buffer bit-exact against
+    the oracle, then AdamW on the 1/4 ZeRO shard [0, 31,109,952) (a view at
+    the buffer's start, as rank 0 of dtrain/zero.py:37-39 holds it) from the
+    same starting state, bit-exact as well."""
     D, K = _dev()
     n, W = 124_439_808, 4
     rng = np.random.default_rng(4)
-    p = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.02))
-    reps = rng.standard_normal((W, n), dtype=np.float32) * np.float32(1e-3)
-    m = np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-4))
-    v = np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-4))
+    p = (rng.standard_normal(n, dtype=dt) * dt(0.02))
+    reps = rng.standard_normal((W, n), dtype=dt) * dt(1e-3)
+    m = np.abs(rng.standard_normal(n, dtype=dt) * dt(1e-4))
+    v = np.abs(rng.standard_normal(n, dtype=dt) * dt(1e-4))
+    sh = n // W
+    p_sh, m_sh, v_sh = p[:sh].copy(), m[:sh].copy(), v[:sh].copy()
     dp, dm, dv = D.from_numpy(p), D.from_numpy(m), D.from_numpy(v)
-    dg = D.empty((n,), np.float32)
+    dg = D.empty((n,), dt)
     nb = K.average_blocks(n)
     parts = D.empty((nb,), np.float64)
-    K.bucket_average(dg, D.from_numpy(reps), W, 0.25, partials=parts)
+    drep = D.from_numpy(reps)
+    K.bucket_average(dg, drep, W, 0.25, partials=parts)
+    del drep
     sq = D.empty((1,), np.float64)
     K.sumsq_finish(parts, nb, sq)
     s_dev = D.empty((1,), np.float64)
     K.clip_scale(sq, 1.0, s_dev)
     b1t, b2t = O.bias_corrections(0.9, 0.95, 101)
     K.adamw(dp, dg, dm, dv, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t, gscale_dev=s_dev)
+    # the shard leg: rank 0's slice of a second copy of the starting state
+    sp, sm, sv = D.empty((n,), dt), D.empty((n,), dt), D.empty((n,), dt)
+    for dst, src in ((sp, p_sh), (sm, m_sh), (sv, v_sh)):
+        K.copy_into(dst[:sh], D.from_numpy(src))
+    K.adamw(sp[:sh], dg[:sh], sm[:sh], sv[:sh], 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t, gscale_dev=s_dev)
     g = fixed_order_sum(list(reps))
-    g *= 0.25
+    del reps
+    g *= dt(0.25)
     assert bits_equal(dg.numpy(), g)
     # dtrain's BLAS ddot over 124M terms carries ~1e-13 relative error of its
     # own; judge both against an extended-precision sum of the exact squares.
     g64 = g.astype(np.float64)
     exact = float(np.sum(np.square(g64).astype(np.longdouble)))
     ref_sq = float(np.dot(g64, g64))
+    del g64
     got_sq = float(sq.numpy()[0])
     assert abs(got_sq - exact) <= 1e-14 * exact
     assert abs(got_sq - ref_sq) <= 1e-12 * ref_sq
     s = float(s_dev.numpy()[0])
     assert s == O.clip_scale(got_sq, 1.0)
     assert abs(s - O.clip_scale(ref_sq, 1.0)) <= 1e-12
-    O.adamw_update(p, g * s, m, v, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t)
+    gs = g * s  # dtrain/train.py:159: the Python float is rounded to the array dtype
+    O.adamw_update(p, gs, m, v, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t)
     assert bits_equal(dp.numpy(), p)
+    assert bits_equal(dm.numpy(), m)
     assert bits_equal(dv.numpy(), v)
+    O.adamw_update(p_sh, gs[:sh], m_sh, v_sh, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t)
+    assert bits_equal(sp.numpy()[:sh], p_sh)
+    assert bits_equal(sm.numpy()[:sh], m_sh)
+    assert bits_equal(sv.numpy()[:sh], v_sh)
+    assert bits_equal(p_sh, p[:sh])
+
+
+def _ring_ref(reps, segs, dt):
+    W, n = reps.shape
+    starts = [s for s, _ in segs] + [n]
+    out = np.empty(n, dt)
+    for j, (s, f) in enumerate(segs):
+        acc = reps[f, s:starts[j + 1]].copy()
+        for r in range(1, W):
+            acc += reps[(f + r) % W, s:starts[j + 1]]
+        out[s:starts[j + 1]] = acc
+    out *= dt(1.0 / W)  # dtrain/ddp.py:104-106 (weak Python float)
+    return out
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("world", [3, 4, 5])
+@pytest.mark.parametrize("case", ["one_rotated", "block_edges", "inside_blocks", "many"])
+def test_bucket_average_ring_order_bit_exact(dev, dt, world, case):
+    """Segments with their own starting rank (dtrain's ring order): whole
+    buffer rotated, edges on and inside 1024-element blocks, more than 32
+    segments (several launches), against a NumPy rank-order sum per segment;
+    gradients over 16 decades so that any other order changes bits."""
+    D, K = _dev()
+    rng = np.random.default_rng(world + len(case))
+    n = 70_001
+    reps = (rng.standard_normal((world, n)) * 10.0 ** rng.uniform(-8, 8, (world, n))).astype(dt)
+    if case == "one_rotated":
+        segs = [(0, world - 1)]
+    elif case == "block_edges":
+        segs = [(0, 1), (1024, 2), (4096, 0), (40960, world - 1)]
+    elif case == "inside_blocks":
+        segs = [(0, 2), (5, 1), (1030, 0), (1031, world - 1), (33333, 1), (70_000, 2)]
+    else:
+        cuts = np.sort(rng.choice(np.arange(1, n), 70, replace=False))
+        segs = [(0, 1)] + [(int(c), int(rng.integers(0, world))) for c in cuts]
+    out = D.full((n,), 7.0, dt)
+    K.bucket_average(out, D.from_numpy(reps), world, 1.0 / world, segments=segs)
+    ref = _ring_ref(reps, segs, dt)
+    assert bits_equal(out.numpy(), ref)
+    assert not bits_equal(ref, fixed_order_sum(list(reps)) * dt(1.0 / world))
+    if len(segs) <= 32:  # with sum-of-squares partials (one launch)
+        nb = K.average_blocks(n)
+        parts = D.empty((nb,), np.float64)
+        out2 = D.empty((n,), dt)
+        K.bucket_average(out2, D.from_numpy(reps), world, 1.0 / world, partials=parts, segments=segs)
+        assert bits_equal(out2.numpy(), ref)
+        sq = D.empty((1,), np.float64)
+        K.sumsq_finish(parts, nb, sq)
+        r64 = ref.astype(np.float64)
+        ex = float(np.sum(np.square(r64).astype(np.longdouble)))
+        assert abs(float(sq.numpy()[0]) - ex) <= 1e-14 * ex
+
+
+def test_bucket_average_ring_rejects_bad_segments(dev):
+    D, K = _dev()
+    reps = D.zeros((3, 100), np.float32)
+    out = D.empty((100,), np.float32)
+    from dtmi._lib import DtmiError
+    for segs in ([(1, 0)], [(0, 3)], [(0, 1), (0, 2)], [(0, 1), (100, 2)]):
+        with pytest.raises(DtmiError):
+            K.bucket_average(out, reps, 3, 1.0 / 3, segments=segs)

@@ -66,3 +66,54 @@ def test_model_parameter_order_matches_dtrain_names():
     assert [f.name for f in N.GPTConfig.__dataclass_fields__.values()] == \
         ["vocab", "ctx", "dim", "heads", "layers", "dtype"]
     assert list(N.Block.__init__.__code__.co_names).index("ln1") < list(N.Block.__init__.__code__.co_names).index("qkv")
+
+
+def _segmented_average(rows, segs, W):
+    """What dtmi_bucket_average_ring computes, element by element on the host:
+    element i summed starting at the first rank of its segment."""
+    n = rows.shape[1]
+    starts = [s for s, _ in segs] + [n]
+    out = np.empty(n, rows.dtype)
+    for j, (s, f) in enumerate(segs):
+        for i in range(s, starts[j + 1]):
+            acc = rows[f, i]
+            for r in range(1, W):
+                acc = acc + rows[(f + r) % W, i]
+            out[i] = acc
+    return out * rows.dtype.type(1.0 / W)
+
+
+def test_ring_segments_reproduce_dtrains_ring_buckets(golden):
+    """The segments of every bucket, applied to the forward-order layout, give
+    dtrain's DDP ring average bit for bit (its own fixture: 3 and 4 ranks,
+    256-byte buckets)."""
+    from dtmi.replicas import ring_segments
+    G = golden("dtrain_ddp_reduce.npz")
+    shapes = [(7, 5), (3,), (13, 4), (1,), (33,), (6, 6), (2,), (41,)]
+    sizes = [int(np.prod(s)) for s in shapes]
+    offs = np.cumsum([0] + sizes)
+    for W in (3, 4):
+        for dt in ("float64", "float32"):
+            reps = np.stack([np.concatenate([G[f"w{W}/{dt}/g{r}/{i}"].reshape(-1) for i in range(len(shapes))])
+                             for r in range(W)])
+            for idx in bucket_layout(sizes, np.dtype(dt).itemsize, 256 / (1 << 20)):
+                fwd = sorted(idx)
+                lo, hi = offs[fwd[0]], offs[fwd[-1] + 1]
+                segs = ring_segments([sizes[i] for i in fwd], W)
+                assert [s for s, _ in segs] == sorted(s for s, _ in segs) and segs[0][0] == 0
+                got = _segmented_average(reps[:, lo:hi], segs, W)
+                for i in fwd:
+                    ref = G[f"w{W}/{dt}/ddp_ring/{i}"].reshape(-1)
+                    assert got[offs[i] - lo:offs[i + 1] - lo].tobytes() == ref.tobytes(), (W, dt, i)
+
+
+def test_ring_segments_cover_gpt2_small_buckets():
+    """At the GPT-2-small layout (51 buckets, 4 ranks) every bucket needs at
+    most a few segments, all within one launch (32 per launch)."""
+    from dtmi.replicas import ring_segments
+    cfg = OM.GPTConfig(vocab=50304, ctx=1024, dim=768, heads=12, layers=12, dtype="float32")
+    sizes = [int(np.prod(s)) for _, s in OM.param_spec(cfg)]
+    for idx in bucket_layout(sizes, 4, 1.0):
+        segs = ring_segments([sizes[i] for i in sorted(idx)], 4)
+        assert 1 <= len(segs) <= 32
+        assert {f for _, f in segs} <= {0, 1, 2, 3}

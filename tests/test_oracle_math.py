@@ -10,7 +10,7 @@ import pytest
 
 from helpers import rel_err
 from oracle import model, ops, optim
-from oracle.ddp import ZeroAdamW, bucket_layout, ddp_average, fixed_order_sum, partition
+from oracle.ddp import ZeroAdamW, bucket_layout, ddp_average, fixed_order_sum, partition, ring_order_sum
 
 rng = np.random.default_rng(0)
 
@@ -220,7 +220,7 @@ def test_zero_shards_equal_full_adamw_and_state_bytes():
     assert z.opts[0].state_bytes() == 2 * 8 * -(-n // W)  # dtrain tests/test_training.py:72
     flat_grads = [rng.standard_normal(n) for _ in range(W)]
     z.step(flat_grads)
-    g = fixed_order_sum(flat_grads)
+    g = ring_order_sum(flat_grads)  # the reduce-scatter: shard r summed from rank r
     g *= 1.0 / W
     sq = 0.0
     for r in range(W):
@@ -230,6 +230,31 @@ def test_zero_shards_equal_full_adamw_and_state_bytes():
     opt = optim.AdamW([full], lr=1e-2)
     opt.step([g * optim.clip_scale(sq, 1.0)])
     np.testing.assert_array_equal(z.flat, full)
+
+
+def test_ring_order_sum_brute_force():
+    """Chunk c of partition(n, W) summed over ranks c, c+1, ..., c-1, written
+    as an explicit loop per element."""
+    for W, n in ((3, 10), (4, 7), (4, 2), (5, 23)):
+        parts = [rng.standard_normal(n) * 10.0 ** rng.uniform(-8, 8, n) for _ in range(W)]
+        got = ring_order_sum(parts)
+        b = partition(n, W)
+        for i in range(n):
+            c = max(j for j in range(W) if b[j] <= i and b[j + 1] > i)
+            acc = parts[c][i]
+            for j in range(1, W):
+                acc = acc + parts[(c + j) % W][i]
+            assert got[i] == acc
+        assert np.array_equal(ring_order_sum(parts[:2]), fixed_order_sum(parts[:2]))
+
+
+def test_planted_mistake_in_ring_order_is_caught(golden):
+    """A ring that starts every chunk at rank 0 (the direct order) fails
+    dtrain's ring fixture."""
+    G = golden("dtrain_ddp_reduce.npz")
+    reps = [[G[f"w4/float64/g{r}/{i}"] for i in range(8)] for r in range(4)]
+    got = ddp_average(reps, 8, 256 / (1 << 20), "direct")
+    assert not all(np.array_equal(a, G[f"w4/float64/ddp_ring/{i}"]) for i, a in enumerate(got))
 
 
 def test_partition_closed_form():
