@@ -24,6 +24,11 @@ int fail_hip(hipError_t e, const char* what, const char* file, int line);
 hipStream_t stream();
 bool initialized();
 int num_cus();
+int device_id();  // the device dtmi_init selected (-1 before)
+
+// Set-up of the allocation-free LayerNorm backward's device scratch array on
+// `device` (which must be current); called once per device by dtmi_init.
+int ln_scratch_setup(int device);
 
 // Pooled device allocation (stream-ordered reuse on the single library stream).
 int pool_alloc(void** p, size_t bytes);

@@ -324,7 +324,8 @@ static int ln_fwd(void* y, void* mean, void* rstd, const void* x, const void* w,
 
 template <typename T>
 static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, const void* w, const void* mean,
-                  const void* rstd, const void* addend, int64_t rows, int64_t cols, int accumulate) {
+                  const void* rstd, const void* addend, int64_t rows, int64_t cols, int accumulate,
+                  void* scratch_ptr = nullptr, size_t scratch_bytes = 0) {
   constexpr int VWV = 16 / sizeof(T);
   bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(dy, 16) && aligned(dx, 16) && aligned(w, 16) &&
              aligned(addend, 16);
@@ -332,15 +333,24 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
   int nv = pick_nv(cdiv(cols, 64LL * vw));
   DTMI_CHECK(nv > 0, "dtmi_layernorm_bwd: rows of %lld elements exceed the supported %d", (long long)cols, 64 * 16 * vw);
   const int grid = ln_bwd_blocks(rows);
-  void* parts = nullptr;
-  int rc = pool_alloc(&parts, (size_t)2 * grid * cols * sizeof(T));
-  if (rc) return rc;
+  const size_t part_bytes = (size_t)2 * grid * cols * sizeof(T);
+  void* parts = scratch_ptr;
+  if (scratch_ptr) {
+    DTMI_CHECK(part_bytes <= scratch_bytes,
+               "dtmi_layernorm_bwd_noalloc: [%lld, %lld] needs %zu bytes of column partials, more than the %zu "
+               "of its scratch array (use dtmi_layernorm_bwd)",
+               (long long)rows, (long long)cols, part_bytes, scratch_bytes);
+  } else {
+    int rc = pool_alloc(&parts, part_bytes);
+    if (rc) return rc;
+  }
   T* pdw = (T*)parts;
   T* pdb = pdw + (size_t)grid * cols;
   {
     // x and dy in, dx out, and the addend (or the existing dx) in when summed
     const double arrays = (addend || (accumulate & 1)) ? 4.0 : 3.0;
-    TimedLaunch tl(DTMI_FAM_LN_BWD, (double)rows * cols * arrays * sizeof(T));
+    // the allocation-free form is not timed: timing creates HIP events
+    TimedLaunch tl(scratch_ptr ? -1 : DTMI_FAM_LN_BWD, (double)rows * cols * arrays * sizeof(T));
     T* DX = (T*)dx;
     const T *DY = (const T*)dy, *X = (const T*)x, *W = (const T*)w, *MU = (const T*)mean, *RS = (const T*)rstd;
     int c = (int)cols;
@@ -358,8 +368,31 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
     launch_colreduce<T>((T*)dw, pdw, grid, cols, (accumulate & 2) ? 1 : 0, (T*)db, pdb);
   }
   hipError_t le = hipGetLastError();
-  pool_free(parts);
+  if (!scratch_ptr) pool_free(parts);
   if (le != hipSuccess) return fail_hip(le, "ln_bwd kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+}
+
+// -------------------------------------------- allocation-free entry point
+// The dgamma / dbeta column partials of dtmi_layernorm_bwd_noalloc live in a
+// file-scope device array: every GPU the library runs on holds its own copy
+// until the process ends. In host code `scratch` names only a host-side
+// stand-in, so the address each device's copy has is taken once per device
+// with hipGetSymbolAddress (dtmi_init, with the device current) and only that
+// address is handed to kernels.
+constexpr size_t kLnScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kLnScratchBytes];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+
+int ln_scratch_setup(int device) {
+  DTMI_CHECK(device >= 0 && device < kMaxDevices, "dtmi_init: device %d beyond %d", device, kMaxDevices);
+  if (g_scratch_ptr[device]) return DTMI_OK;
+  void* p = nullptr;
+  hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
+  DTMI_CHECK(p != nullptr, "dtmi_init: no device address for the LayerNorm scratch array");
+  g_scratch_ptr[device] = p;
   return DTMI_OK;
 }
 
@@ -428,5 +461,29 @@ DTMI_EXPORT int dtmi_layernorm_bwd_add(int dtype, void* dx, void* dw, void* db, 
   if (dtype == DTMI_F32)
     return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, dx_addend, rows, cols, accumulate);
   return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, dx_addend, rows, cols, accumulate);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_layernorm_bwd_noalloc(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x,
+                                           const void* w, const void* mean, const void* rstd, int64_t rows,
+                                           int64_t cols, int accumulate) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(rows >= 0 && cols > 0 && cols < (1 << 30), "dtmi_layernorm_bwd_noalloc: bad shape [%lld, %lld]",
+             (long long)rows, (long long)cols);
+  DTMI_CHECK(dw && db, "dtmi_layernorm_bwd_noalloc: NULL dgamma/dbeta");
+  if (rows == 0) {
+    if (accumulate & 2) return DTMI_OK;
+    int rc = dtmi_fill(dtype, dw, 0.0, cols);
+    return rc ? rc : dtmi_fill(dtype, db, 0.0, cols);
+  }
+  DTMI_CHECK(dx && dy && x && w && mean && rstd, "dtmi_layernorm_bwd_noalloc: NULL pointer");
+  const int dev = device_id();
+  void* sp = dev >= 0 && dev < kMaxDevices ? g_scratch_ptr[dev] : nullptr;
+  DTMI_CHECK(sp != nullptr, "dtmi_layernorm_bwd_noalloc: scratch array not set up on device %d", dev);
+  if (dtype == DTMI_F32)
+    return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, nullptr, rows, cols, accumulate, sp, kLnScratchBytes);
+  return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, nullptr, rows, cols, accumulate, sp, kLnScratchBytes);
   DTMI_BODY_END
 }

@@ -42,6 +42,7 @@ int fail_hip(hipError_t e, const char* what, const char* file, int line) {
 hipStream_t stream() { return g_stream; }
 bool initialized() { return g_stream != nullptr; }
 int num_cus() { return g_num_cus; }
+int device_id() { return g_device; }
 
 // ------------------------------------------------------------------ pool
 // Sizes are rounded up (256 B granules below 1 MiB, 64 KiB granules below
@@ -206,7 +207,7 @@ static void drain_pending(bool wait) {
 }
 
 TimedLaunch::TimedLaunch(int fam, double w) : family(fam), work(w), slot(-1) {
-  if (!g_timing) return;
+  if (!g_timing || fam < 0) return;  // family -1: never timed (creates no events)
   if (g_pending.size() > 4096) drain_pending(false);
   PendingTiming t{fam, w, nullptr, nullptr};
   if (hipEventCreate(&t.a) != hipSuccess) return;
@@ -276,6 +277,10 @@ DTMI_EXPORT int dtmi_init(int device) {
   hipDeviceProp_t prop;
   HIP_TRY(hipGetDeviceProperties(&prop, device));
   g_num_cus = prop.multiProcessorCount;
+  {
+    int rc = ln_scratch_setup(device);
+    if (rc) return rc;
+  }
   HIP_TRY(hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking));
   void* stage = nullptr;
   if (hipHostMalloc(&stage, kStageBytes, hipHostMallocDefault) == hipSuccess) {

@@ -63,6 +63,7 @@ SIGNATURES: dict[str, list] = {
     "dtmi_layernorm_fwd": [i32, vp, vp, vp, vp, vp, vp, i64, i64, f64],
     "dtmi_layernorm_bwd": [i32, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
     "dtmi_layernorm_bwd_add": [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
+    "dtmi_layernorm_bwd_noalloc": [i32, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
     "dtmi_xent_fwd": [i32, vp, vp, vp, vp, vp, i64, i64],
     "dtmi_xent_bwd": [i32, vp, vp, vp, vp, vp, vp, f64, i64, i64],
     "dtmi_xent_fused": [i32, vp, vp, vp, vp, vp, vp, i64, i64],

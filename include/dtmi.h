@@ -221,6 +221,19 @@ int dtmi_layernorm_bwd(int dtype, void* dx, void* dw, void* db, const void* dy, 
 int dtmi_layernorm_bwd_add(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x, const void* w,
                            const void* mean, const void* rstd, const void* dx_addend, int64_t rows, int64_t cols,
                            int accumulate);
+/* dtmi_layernorm_bwd that allocates nothing. No counterpart in dtrain: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, kernels and bits as dtmi_layernorm_bwd; its dgamma/dbeta column
+ * partials go to a fixed 8 MiB device array per GPU (held until the process
+ * ends) instead of the pool: 2 * min(512, ceil(rows / 8)) * cols * element
+ * size must fit (float32 up to 2048 columns, float64 up to 1024, at any row
+ * count), larger shapes return DTMI_ERR_INVALID before any launch. Calls that
+ * overlap on one GPU (from other threads or streams) share the array and
+ * race; calls on the library stream are ordered. Not timed by
+ * dtmi_timing_enable (that creates events). */
+int dtmi_layernorm_bwd_noalloc(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x, const void* w,
+                               const void* mean, const void* rstd, int64_t rows, int64_t cols, int accumulate);
 
 /* --------------------------------------------------------- cross entropy
  * dtrain/autograd.py:250-266 over logits [rows, vocab] and int64 targets.
