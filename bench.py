@@ -45,40 +45,6 @@ BATCH, WORLD = 8, 4
 LR, BETAS, EPS, WD, CLIP = 3e-4, (0.9, 0.95), 1e-8, 0.1, 1.0
 
 
-def param_spec(c):
-    C, V = c["dim"], c["vocab"]
-    spec = [("tok", (V, C)), ("pos", (c["ctx"], C))]
-    for i in range(c["layers"]):
-        p = f"blocks.{i}."
-        spec += [(p + "ln1.w", (C,)), (p + "ln1.b", (C,)), (p + "qkv.w", (C, 3 * C)), (p + "qkv.b", (3 * C,)),
-                 (p + "proj.w", (C, C)), (p + "proj.b", (C,)), (p + "ln2.w", (C,)), (p + "ln2.b", (C,)),
-                 (p + "fc.w", (C, 4 * C)), (p + "fc.b", (4 * C,)), (p + "out.w", (4 * C, C)), (p + "out.b", (C,))]
-    return spec + [("ln.w", (C,)), ("ln.b", (C,)), ("head.w", (C, V))]
-
-
-def synthetic_weights(c, seed):
-    """Matrices N(0, 0.02) (float64 draw in parameter order, cast), biases 0, LayerNorm w 1, b 0."""
-    rng = np.random.default_rng(seed)
-    out = {}
-    for name, shape in param_spec(c):
-        if len(shape) == 2:
-            out[name] = (rng.standard_normal(shape) * 0.02).astype(c["dtype"])
-        elif ".ln" in "." + name and name.endswith(".w"):
-            out[name] = np.ones(shape, c["dtype"])
-        else:
-            out[name] = np.zeros(shape, c["dtype"])
-    return out
-
-
-def synthetic_tokens(c, batch, seed, replicas):
-    rng = np.random.default_rng(seed)
-    xs, ys = [], []
-    for _ in range(replicas):
-        xs.append(rng.integers(0, c["vocab"], (batch, c["ctx"])))
-        ys.append(rng.integers(0, c["vocab"], (batch, c["ctx"])))
-    return xs, ys
-
-
 def gemm_flops_per_step(c, batch, world):
     """Algorithmic FLOP of every GEMM launch of one step (forward Y = XW, dX, dW)."""
     M = batch * c["ctx"]
@@ -88,40 +54,101 @@ def gemm_flops_per_step(c, batch, world):
     return world * 3 * fwd
 
 
+def _cpu_info():
+    """Host CPU model (from /proc/cpuinfo, what lscpu reports as 'Model name'),
+    the cores this process may run on, and the BLAS thread count in use."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "affinity_cores": len(os.sched_getaffinity(0)), "blas_threads": _threads()}
+
+
+def _median(xs):
+    return sorted(xs)[len(xs) // 2]
+
+
 def cpu_baseline(weights, xs, ys, seq: int):
-    """The oracle (NumPy restatement of dtrain) on a bounded sample of the same
-    step: one replica's forward+backward on `seq` sequences, plus the 4-replica
-    bucket average, global norm, clip and AdamW over all parameters once.
-    Returns tokens/s extrapolated to the full step (32 x the sampled tokens of
-    forward+backward, 1 x the optimizer part)."""
-    from oracle import model as OM, optim as OO
+    """The oracle (NumPy restatement of dtrain) on the host cores, on a bounded
+    sample of the same step, as BASELINE's CPU plan asks:
+      - forward+backward of one replica's first `seq` sequences: 1 warm-up,
+        then the median of 3 runs, with the BLAS thread count the machine is
+        configured for, and once more with 1 thread;
+      - the 4-replica bucket average, global norm, clip and AdamW over all
+        163,109,376 parameters, timed once;
+      - tokens/s extrapolated to the full step (4 x 8 sequences of
+        forward+backward, one optimizer pass);
+      - dtrain's own published benchmark configuration (float32, dim 128, 4
+        layers, 4 heads, ctx 64, batch 8, vocabulary 65) with 1 thread: median
+        of 3 full steps after 1 warm-up, beside dtrain's 2,577 tokens/s
+        (docs/benchmarks.md:51 of the reference, a 4-vCPU Xeon, 1 BLAS thread)."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import model as OM, optim as OO, step as OS
     from oracle.ddp import ddp_average
 
     c = OM.GPTConfig(**CFG)
     P = {k: v.copy() for k, v in weights.items()}
-    t0 = time.perf_counter()
-    loss, g = OM.loss_and_grads(P, c, xs[0][:seq], ys[0][:seq])
-    t_fb = time.perf_counter() - t0
+    info = _cpu_info()
+    x, y = xs[0][:seq], ys[0][:seq]
+
+    def fb():
+        t0 = time.perf_counter()
+        _, g = OM.loss_and_grads(P, c, x, y)
+        return time.perf_counter() - t0, g
+
+    _, g = fb()  # warm-up
+    runs = [fb()[0] for _ in range(3)]
+    t_fb = _median(runs)
+    with threadpool_limits(limits=1):
+        t_fb1, _ = fb()
     names = list(P)
     glist = [g[k] for k in names]
     t1 = time.perf_counter()
-    avg = ddp_average([glist] * WORLD, 4, 1.0)
+    avg = ddp_average([glist] * WORLD, 4, 1.0, "ring")
     sq = OO.global_sq_norm(avg)
     s = OO.clip_scale(sq, CLIP)
     opt = OO.AdamW([P[k] for k in names], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
-    opt.step([x * s for x in avg])
+    opt.step([v * s for v in avg])
     t_opt = time.perf_counter() - t1
+    del avg, glist, g
     tokens_step = WORLD * BATCH * CFG["ctx"]
-    full = (tokens_step / (seq * CFG["ctx"])) * t_fb + t_opt
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:  # noqa: BLE001
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
-    return {"value": round(tokens_step / full, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle (NumPy) forward+backward of 1 replica x {seq} x {CFG['ctx']} tokens "
-                       f"({t_fb:.1f} s) + 4-replica bucket average, clip and AdamW over 163,109,376 params "
-                       f"({t_opt:.1f} s); extrapolated to the full 4 x 8 x 1024-token step")}
+    per_step = (WORLD * BATCH / seq) * t_fb + t_opt
+    per_step1 = (WORLD * BATCH / seq) * t_fb1 + t_opt
+
+    # dtrain's published configuration, 1 thread
+    rc = OM.GPTConfig(vocab=65, ctx=64, dim=128, heads=4, layers=4, dtype="float32")
+    RP = OM.dtrain_init(rc, seed=0)
+    rx, ry = OM.synthetic_tokens(rc, batch=8, seed=0)
+    ropt = OO.AdamW(list(RP.values()), lr=1e-3)
+    with threadpool_limits(limits=1):
+        rt = []
+        for i in range(4):
+            t0 = time.perf_counter()
+            OS.single_step(RP, rc, [(rx[0], ry[0])], ropt, clip=1.0)
+            if i:
+                rt.append(time.perf_counter() - t0)
+    ref_tps = 8 * 64 / _median(rt)
+    return {"value": round(tokens_step / per_step, 2), "unit": "tokens/s", "cores": info["blas_threads"],
+            "kind": "port", **info,
+            "value_1_thread": round(tokens_step / per_step1, 2),
+            "sample": (f"oracle (NumPy) forward+backward of 1 replica x {seq} x {CFG['ctx']} tokens: median of 3 "
+                       f"after 1 warm-up {t_fb:.2f} s ({', '.join(f'{r:.2f}' for r in runs)}), 1 thread {t_fb1:.2f} s; "
+                       f"4-replica bucket average (ring order), clip and AdamW over 163,109,376 params once "
+                       f"({t_opt:.2f} s); extrapolated to the full 4 x 8 x 1024-token step "
+                       f"({per_step:.1f} s, 1 thread {per_step1:.1f} s)"),
+            "reference_config_1_thread": {
+                "value": round(ref_tps, 1), "unit": "tokens/s",
+                "config": "float32 GPT, dim 128, 4 layers, 4 heads, ctx 64, batch 8, vocab 65 (dtrain's benchmark)",
+                "sample": f"oracle full step (fwd, bwd, clip, AdamW), median of 3 after 1 warm-up, "
+                          f"{_median(rt) * 1e3:.1f} ms",
+                "dtrain_published": {"value": 2577, "unit": "tokens/s",
+                                     "where": "docs/benchmarks.md:51, 4-vCPU Xeon 2.80 GHz, 1 BLAS thread"}}}
 
 
 def main(argv=None):
@@ -130,7 +157,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seq", type=int, default=3, help="sequences in the CPU baseline sample")
+    ap.add_argument("--cpu-seq", type=int, default=1, help="sequences in the CPU baseline sample")
     ap.add_argument("--seed", type=int, default=5)
     ap.add_argument("--workload", default="gpt2",
                     choices=["gpt2", "ln_linear", "attention", "bucket_adamw", "chargpt", "copy"],
@@ -155,18 +182,19 @@ def main(argv=None):
     from dtmi import _lib
     from dtmi import ddp as P, nn as N, optim as O, replicas as R, train as S
     from dtmi.autograd import Indices
+    from dtmi.workload import synthetic_tokens, synthetic_weights
 
     _lib.set_gemm_math(a.gemm_math)
 
     info = _lib.device_info()
     print(f"[bench] device {info['name']} ({info['num_cus']} CUs); building GPT-2-small weights", file=sys.stderr,
           flush=True)
-    weights = synthetic_weights(CFG, a.seed)
-    xs, ys = synthetic_tokens(CFG, BATCH, a.seed, WORLD)
+    weights = synthetic_weights(N.GPTConfig(**CFG), a.seed)
+    xs, ys = synthetic_tokens(N.GPTConfig(**CFG), BATCH, a.seed, WORLD)
     model = N.GPT(N.GPTConfig(**CFG), seed=a.seed)
     model.load_numpy(weights)
     pg = R.SimGroup(WORLD)
-    ddp = P.DDP(model, pg, bucket_mb=1.0, overlap=True, algo="direct")
+    ddp = P.DDP(model, pg, bucket_mb=1.0, overlap=True, algo="ring")  # dtrain's default all-reduce order
     opt = O.AdamW([p.data for p in model.parameters()], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
     # token ids and targets uploaded once: the timed steps copy nothing from the host
     batches = [[(Indices(xs[r]), Indices(ys[r]))] for r in range(WORLD)]
@@ -259,9 +287,9 @@ def main(argv=None):
            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
            "config": {"workload": ("GPT-2-small-shape float32 train step: 12 layers, d_model 768, 12 heads, "
                                    "T 1024, vocab 50304, batch 8 per replica x 4 simulated replicas, 1 MiB "
-                                   "buckets, fixed-order average, clip 1.0, AdamW"),
+                                   "buckets, ring-order average, clip 1.0, AdamW"),
                       "global_batch": WORLD * BATCH, "seq_len": CFG["ctx"], "parallelism": "dp4-simulated",
-                      "params": sum(int(np.prod(s)) for _, s in param_spec(CFG))},
+                      "params": sum(int(v.size) for v in weights.values())},
            "roofline": roofline, "kernels": kernels, "loss": round(loss, 5), "gemm_math": a.gemm_math,
            "timing_note": (f"value and ms_per_step: {a.steps} steps with no instrumentation; roofline and kernels: "
                            f"the next {a.steps} steps with HIP events around every launch "
@@ -379,8 +407,8 @@ def micro_ln_linear(a):
             reps += 1
         t = (time.perf_counter() - t0) / reps
         cpu = {"value": round(flop / t / 1e9, 2), "unit": "GFLOP/s", "cores": _threads(),
-               "kind": "port", "sample": f"oracle LN forward + Linear and LN backward on all {M} rows, "
-                                         f"{reps} repetitions, {t:.2f} s each"}
+               "kind": "port", **_cpu_info(), "sample": f"oracle LN forward + Linear and LN backward on all {M} "
+                                                        f"rows, mean of {reps} repetitions, {t:.2f} s each"}
     return _line("LN + Linear backward GEMM throughput (dX, dW) at x[16384,768] W[768,3072]",
                  round(flop / (1e-3 * ms / a.steps) / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"LayerNorm + Linear backward, x [16384,768], W [768,3072], dY [16384,3072], {a.dtype}"},
@@ -410,15 +438,18 @@ def micro_attention(a):
     cpu = None
     if not a.no_cpu_baseline:
         from oracle import ops as OP
-        bs = 2
-        t0 = time.perf_counter()
+        bs = 4
         _, p, sc = OP.attention_fwd(q[:bs], k[:bs], v[:bs])
-        t1 = time.perf_counter()
-        OP.attention_bwd(g[:bs], q[:bs], k[:bs], v[:bs], p, sc)
-        t = time.perf_counter() - t1
+        runs = []
+        for _ in range(4):
+            t1 = time.perf_counter()
+            OP.attention_bwd(g[:bs], q[:bs], k[:bs], v[:bs], p, sc)
+            runs.append(time.perf_counter() - t1)
+        t = _median(runs[1:])
         fl = 5 * 2 * bs * H * Dh * T * (T + 1) / 2
         cpu = {"value": round(fl / t / 1e9, 2), "unit": "GFLOP/s", "cores": _threads(), "kind": "port",
-               "sample": f"oracle causal_attention backward on {bs} of {B} batches ({t:.2f} s), causal-exact FLOP"}
+               **_cpu_info(), "sample": f"oracle causal_attention backward on {bs} of {B} batches, median of 3 "
+                                        f"after 1 warm-up ({t:.3f} s), causal-exact FLOP"}
     return _line("causal attention backward throughput (5 GEMMs, causal-exact FLOP) at B16 H12 T256 D64",
                  round(ach / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"causal self-attention backward B=16 H=12 T=256 D=64 {a.dtype}"},
@@ -465,15 +496,19 @@ def micro_bucket_adamw(a):
         from oracle.ddp import fixed_order_sum
         k = n
         rr = rng.standard_normal((W, k)).astype(dt)
-        t0 = time.perf_counter()
-        gg = fixed_order_sum(list(rr))
-        gg *= 1.0 / W
-        s = OO.clip_scale(float(np.dot(gg.astype(np.float64), gg.astype(np.float64))), 1.0)
-        pp, mm, vv = p[:k].copy(), m[:k].copy(), v[:k].copy()
-        OO.adamw_update(pp, gg * s, mm, vv, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t)
-        t = time.perf_counter() - t0
+        runs = []
+        for _ in range(3):
+            pp, mm, vv = p[:k].copy(), m[:k].copy(), v[:k].copy()
+            t0 = time.perf_counter()
+            gg = fixed_order_sum(list(rr))
+            gg *= 1.0 / W
+            s = OO.clip_scale(float(np.dot(gg.astype(np.float64), gg.astype(np.float64))), 1.0)
+            OO.adamw_update(pp, gg * s, mm, vv, 3e-4, 0.9, 0.95, 1e-8, 0.1, b1t, b2t)
+            runs.append(time.perf_counter() - t0)
+        t = _median(runs)
         cpu = {"value": round((5 + 7) * k * dt.itemsize / t / 1e9, 2), "unit": "GB/s", "cores": _threads(),
-               "kind": "port", "sample": f"oracle average + clip + AdamW over all {k} elements ({t:.2f} s)"}
+               "kind": "port", **_cpu_info(),
+               "sample": f"oracle average + clip + AdamW over all {k} elements, median of 3 ({t:.2f} s)"}
     return _line("gradient bucket average + AdamW bandwidth over 124,439,808 params (4 replicas)",
                  round(total_bytes / (total_ms * 1e-3) / 1e9, 1), "GB/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"124,439,808-element 4-replica fixed-order average + clip + AdamW (full + 1/4 shard) "
@@ -487,9 +522,10 @@ def micro_bucket_adamw(a):
 def micro_chargpt(a):
     """The float64 char-GPT step (vocab 65, ctx 32, dim 64, 4 heads, 2 layers, batch 8)."""
     from dtmi import nn as N, optim as O, train as S
+    from dtmi.workload import synthetic_weights
     a.dtype = "float64"
     c = dict(vocab=65, ctx=32, dim=64, heads=4, layers=2, dtype="float64")
-    w = synthetic_weights(c, 0)
+    w = synthetic_weights(N.GPTConfig(**c), 0)
     rng = np.random.default_rng(0)
     x, y = rng.integers(0, 65, (8, 32)), rng.integers(0, 65, (8, 32))
     m = N.GPT(N.GPTConfig(**c))

@@ -117,3 +117,24 @@ def test_ring_segments_cover_gpt2_small_buckets():
         segs = ring_segments([sizes[i] for i in sorted(idx)], 4)
         assert 1 <= len(segs) <= 32
         assert {f for _, f in segs} <= {0, 1, 2, 3}
+
+
+def test_benchmark_inputs_equal_the_oracles():
+    """bench.py draws its weights and tokens with dtmi.workload; they are the
+    oracle's synthetic inputs bit for bit (one source of truth for both)."""
+    from dtmi import workload as Wk
+    from dtmi.nn import GPTConfig
+    for cfg in (dict(vocab=65, ctx=32, dim=64, heads=4, layers=2, dtype="float64"),
+                dict(vocab=50304, ctx=16, dim=48, heads=4, layers=2, dtype="float32")):
+        c, oc = GPTConfig(**cfg), OM.GPTConfig(**cfg)
+        assert Wk.param_spec(c) == OM.param_spec(oc)
+        a, b = Wk.synthetic_weights(c, 5), OM.synthetic_init(oc, seed=5)
+        assert list(a) == list(b)
+        for k in a:
+            assert a[k].dtype == b[k].dtype and a[k].tobytes() == b[k].tobytes(), k
+        xa, ya = Wk.synthetic_tokens(c, 3, 7, 4)
+        xb, yb = OM.synthetic_tokens(oc, batch=3, seed=7, replicas=4)
+        for u, v in zip(xa + ya, xb + yb):
+            assert np.array_equal(u, v)
+    gpt2 = GPTConfig(vocab=50304, ctx=1024, dim=768, heads=12, layers=12)
+    assert sum(int(np.prod(s)) for _, s in Wk.param_spec(gpt2)) == 163_109_376
