@@ -20,13 +20,17 @@
 // rows) read from LDS at the matching row. The k-permutation is the same on
 // both operands, so every product is a plain sum over the reduction index.
 //
-// Backward without atomics: kernel A owns a key block and loops over the query
-// tiles that see it, recomputing P = exp(s - max) / sum (dK, dV accumulate in
+// Backward without atomics: kernel A owns keys and loops over the query tiles
+// that see them, recomputing P = exp(s - max) / sum (dK, dV accumulate in
 // registers) and writing dS = P * (dP - rowsum(dO * O)) to a [B, H, T, T]
-// workspace; kernel B owns a query block and accumulates dQ = dS K from it
-// (when the workspace would exceed 4 GiB, kernel B recomputes dS instead).
-// Float32 kernel A keeps its query and dO tiles also transposed in LDS so the
-// dK / dV MFMAs read them with 16-byte vectors. Results are deterministic.
+// workspace; kernel B owns queries and accumulates dQ = dS K from it (when
+// the workspace would exceed its bound, kernel B recomputes dS instead).
+// Float32 with D = 64 and T a multiple of 32 uses one 32-key (32-query) tile
+// per block, whose four waves split the tile's query (key) range and add
+// their partial sums in wave order at the end; otherwise a block owns 128
+// keys (queries), one 32-wide tile per wave, and the float32 kernel A keeps
+// its query and dO tiles also transposed in LDS so the dK / dV MFMAs read
+// them with 16-byte vectors. Results are deterministic.
 #include <cmath>
 
 #include "common.h"
@@ -151,6 +155,22 @@ __device__ __forceinline__ typename AM<T>::acc_t mma_rows_frag(typename AM<T>::a
         *reinterpret_cast<const typename AM<T>::vec_t*>(lds + (rbase + c) * LD + 8 * ch + VEC * g);
 #pragma unroll
     for (int s = 0; s < VEC; ++s) acc = AM<T>::mma(a[s], f[ch][s], acc);
+  }
+  return acc;
+}
+
+// The same product with the B rows also read from LDS: acc += sum_d
+// ldsA[rbase + row][d] * ldsB[col][d] (lane column c reads row c of ldsB).
+template <typename T, int DP>
+__device__ __forceinline__ typename AM<T>::acc_t mma_rows_rows(typename AM<T>::acc_t acc, const T* __restrict__ ldsA,
+                                                                const T* __restrict__ ldsB, int g, int c) {
+  constexpr int VEC = AM<T>::VEC, LD = DP + AM<T>::PAD;
+#pragma unroll
+  for (int ch = 0; ch < DP / 8; ++ch) {
+    const typename AM<T>::vec_t x = *reinterpret_cast<const typename AM<T>::vec_t*>(ldsA + c * LD + 8 * ch + VEC * g);
+    const typename AM<T>::vec_t y = *reinterpret_cast<const typename AM<T>::vec_t*>(ldsB + c * LD + 8 * ch + VEC * g);
+#pragma unroll
+    for (int s = 0; s < VEC; ++s) acc = AM<T>::mma(x[s], y[s], acc);
   }
   return acc;
 }
@@ -705,6 +725,174 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   store_result<T, DP, KBB>(lds, dv, T(1), DV, a.sdv.t, k0, Tn, D, wave, g, c);
 }
 
+// ------------------------- backward A, one key tile per block (float32)
+// One block owns MT = 32 keys of one (batch, head); its four waves take the
+// query tiles that see those keys in turn (wave w: tiles kt + w, kt + w + 4,
+// ...), each with its own LDS copy of its tile's Q and dO rows and row
+// statistics. The waves never wait for each other inside the loop, and no
+// wave carries more than a quarter of its key tile's query range, so short
+// sequences still spread over the whole chip and a long one ends without a
+// single-wave tail. Each wave prefetches its next tile into registers while
+// it computes the current one. The four partial dK / dV are added in wave
+// order at the end. Aligned path only: D = DP = 64, T a multiple of 32,
+// 16-byte access, the dS workspace present.
+template <int DP>
+__global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
+  using M = AM<float>;
+  typedef M::vec_t V4;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  constexpr int TILE = MT * LD;                 // 32 rows, row form
+  constexpr int WAVE_LDS = 2 * TILE + 2 * MT;   // Q rows, dO rows, (max + log2 sum, rowsum(dO * O))
+  constexpr int RED = 2 * DP * (MT + 1);        // a wave's dK^T and dV^T for the final sum
+  constexpr int PER_WAVE = WAVE_LDS > RED ? WAVE_LDS : RED;
+  constexpr int NV = MT * DP / 4 / 64;          // 16-byte vectors per lane per tile and operand
+  // four wave regions, then the block's V rows (shared: the B operand of dP)
+  __shared__ __attribute__((aligned(16))) float lds[4 * PER_WAVE + TILE];
+
+  int kt, bh;  // kt: the block's key tile; 0 sees the most query tiles
+  causal_block(kt, bh);
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int Tn = (int)a.T;
+  const int nt = Tn / MT;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane / MT, c = lane % MT;
+  const int k0 = kt * MT;
+  const int kj = k0 + c;  // this lane's key (column)
+  const float* Q = (const float*)a.q + b * a.sq.b + h * a.sq.h;
+  const float* K = (const float*)a.k + b * a.sk.b + h * a.sk.h;
+  const float* Vv = (const float*)a.v + b * a.sv.b + h * a.sv.h;
+  const float* G = (const float*)a.dO + b * a.sdo.b + h * a.sdo.h;
+  const float* RM = (const float*)a.rowmax + (int64_t)bh * Tn;
+  const float* RS = (const float*)a.rowsum + (int64_t)bh * Tn;
+  const float* DR = (const float*)a.drow + (int64_t)bh * Tn;
+  float* DS = (float*)a.ds + (int64_t)bh * Tn * Tn;
+  const float sl2 = (float)(a.scale * 1.4426950408889634);
+  const unsigned ds_lane = (unsigned)(4 * g * Tn + kj) * 4u;
+
+  float* W = lds + wave * PER_WAVE;
+  float* Qs = W;
+  float* Gs = W + TILE;
+  float* ST = W + 2 * TILE;  // [0, MT): max + log2 sum; [MT, 2 MT): rowsum(dO * O)
+
+  M::vec_t kf[DP / 8];
+  load_frag_rows<float, DP>(kf, K, a.sk.t, kj, Tn, DP, g, true);
+  float* Vs = lds + 4 * PER_WAVE;
+  for (int f = threadIdx.x; f < MT * DP / 4; f += 256) {
+    const int r = f / (DP / 4), d = (f % (DP / 4)) * 4;
+    *reinterpret_cast<V4*>(Vs + r * LD + d) = *reinterpret_cast<const V4*>(Vv + (int64_t)(k0 + r) * a.sv.t + d);
+  }
+  M::acc_t dk[DP / MT], dv[DP / MT];
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt) dk[dt] = dv[dt] = M::acc_t(0);
+
+  // this lane's share of a tile: vector v covers row 4 v + lane / 16, columns 4 (lane % 16) ..
+  const int lrow = lane >> 4, lcol = (lane & 15) * 4;
+  V4 rq[NV], rg[NV];
+  float rm = 0.f, rl = 1.f, rd = 0.f;
+  auto fetch = [&](int qs) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int64_t r = qs + 4 * v + lrow;
+      rq[v] = *reinterpret_cast<const V4*>(Q + r * a.sq.t + lcol);
+      rg[v] = *reinterpret_cast<const V4*>(G + r * a.sdo.t + lcol);
+    }
+    const int sr = qs + (lane & (MT - 1));
+    rm = RM[sr];
+    rl = RS[sr];
+    rd = DR[sr];
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int r = 4 * v + lrow;
+      *reinterpret_cast<V4*>(Qs + r * LD + lcol) = rq[v];
+      *reinterpret_cast<V4*>(Gs + r * LD + lcol) = rg[v];
+    }
+    if (lane < MT) {
+      ST[lane] = rm + log2(rl);
+      ST[MT + lane] = rd;
+    }
+  };
+  // the wave's LDS is its own: a wave-level barrier orders its writes and reads
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  int qt = kt + wave;
+  if (qt < nt) {
+    fetch(qt * MT);
+    put();
+  }
+  __syncthreads();  // V rows and every wave's first tile in place
+  for (; qt < nt; qt += 4) {
+    const int qs = qt * MT;
+    const bool more = qt + 4 < nt;
+    if (more) fetch(qs + 4 * MT);
+    M::acc_t s = mma_rows_frag<float, DP>(M::acc_t(0), Qs, 0, kf, g, c);
+    M::acc_t dp = mma_rows_rows<float, DP>(M::acc_t(0), Gs, Vs, g, c);
+    const int lim = kj - qs - 4 * g;  // row qs + 4g + x sees key kj iff x >= lim
+    float* dsb = DS + (int64_t)qs * Tn;
+    auto probs = [&](auto maskc) {
+      constexpr bool MASK = decltype(maskc)::value;
+#pragma unroll
+      for (int a4 = 0; a4 < NACC / 4; ++a4) {
+        const int r0 = 8 * a4 + 4 * g;
+        const V4 ml4 = *reinterpret_cast<const V4*>(&ST[r0]);
+        const V4 d4 = *reinterpret_cast<const V4*>(&ST[MT + r0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * a4 + e;
+          float p = ex2(__builtin_fmaf(s[i], sl2, -ml4[e]));
+          if constexpr (MASK) p = 8 * a4 + e >= lim ? p : 0.f;
+          s[i] = p;
+          const float v = p * (dp[i] - d4[e]);
+          dp[i] = v;
+          *(float*)((char*)(dsb + (int64_t)(8 * a4 + e) * Tn) + ds_lane) = v;
+        }
+      }
+    };
+    if (qt == kt)
+      probs(std::true_type());
+    else
+      probs(std::false_type());
+    // dV^T += dO^T P ; dK^T += Q^T dS
+    mma_lds_t_regs<float, DP>(dv, Gs, 0, s, g, c);
+    mma_lds_t_regs<float, DP>(dk, Qs, 0, dp, g, c);
+    wave_sync();
+    if (more) put();
+    wave_sync();
+  }
+  // partial dK^T / dV^T of the four waves, added in wave order
+  __syncthreads();
+  float* R = lds + wave * PER_WAVE;
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt)
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) {
+      const int d = dt * MT + M::row(i, g);
+      R[d * (MT + 1) + c] = dk[dt][i];
+      R[DP * (MT + 1) + d * (MT + 1) + c] = dv[dt][i];
+    }
+  __syncthreads();
+  float* DK = (float*)a.dk + b * a.sdk.b + h * a.sdk.h;
+  float* DV = (float*)a.dv + b * a.sdv.b + h * a.sdv.h;
+  const float scale = (float)a.scale;
+  for (int f = threadIdx.x; f < MT * DP; f += 256) {
+    const int key = f / DP, d = f % DP;
+    const int o = d * (MT + 1) + key;
+    float sk = lds[o], sv = lds[DP * (MT + 1) + o];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) {
+      sk += lds[w * PER_WAVE + o];
+      sv += lds[w * PER_WAVE + DP * (MT + 1) + o];
+    }
+    DK[(int64_t)(k0 + key) * a.sdk.t + d] = sk * scale;
+    DV[(int64_t)(k0 + key) * a.sdv.t + d] = sv;
+  }
+}
+
 // ------------------------------------------------------- backward B: dQ
 // dQ from the dS the key-block pass wrote: dQ^T += K^T dS^T over the key
 // tiles up to the block's last query, with dS read straight into the MFMA B
@@ -813,6 +1001,108 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   }
   T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h;
   store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c);
+}
+
+// dQ from the dS workspace, one query tile per block (float32): the block's
+// four waves take the key tiles up to the query tile in turn (wave w: tiles
+// w, w + 4, ...), each staging its key tile's rows in its own LDS region and
+// prefetching the next tile's K rows and dS entries into registers; the four
+// partial dQ are added in wave order at the end. Aligned path only (D = DP =
+// 64, T a multiple of 32, 16-byte access).
+template <int DP>
+__global__ void __launch_bounds__(256, 2) attn_bwd_q1_kernel(AttnArgs a) {
+  using M = AM<float>;
+  typedef M::vec_t V4;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  constexpr int TILE = MT * LD;
+  constexpr int RED = DP * (MT + 1);
+  constexpr int PER_WAVE = TILE > RED ? TILE : RED;
+  constexpr int NV = MT * DP / 4 / 64;
+  __shared__ __attribute__((aligned(16))) float lds[4 * PER_WAVE];
+
+  int rank, bh;  // rank 0: the last query tile, which sees every key tile
+  causal_block(rank, bh);
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int Tn = (int)a.T;
+  const int nt = Tn / MT;
+  const int qt = nt - 1 - rank;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane / MT, c = lane % MT;
+  const int q0 = qt * MT;
+  const int qr = q0 + c;  // this lane's query (column)
+  const float* K = (const float*)a.k + b * a.sk.b + h * a.sk.h;
+  const float* DSr = (const float*)a.ds + (int64_t)bh * Tn * Tn + (int64_t)qr * Tn;  // row qr of dS
+  float* Ks = lds + wave * PER_WAVE;
+  const int lrow = lane >> 4, lcol = (lane & 15) * 4;
+  V4 rk[NV];
+  M::acc_t dsn;
+  auto fetch = [&](int kt) {
+    const int j0 = kt * MT;
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+      rk[v] = *reinterpret_cast<const V4*>(K + (int64_t)(j0 + 4 * v + lrow) * a.sk.t + lcol);
+    // lane (c, g), register 4 a + e: dS[qr][j0 + 8 a + 4 g + e]
+#pragma unroll
+    for (int a4 = 0; a4 < NACC / 4; ++a4) {
+      const V4 x = *reinterpret_cast<const V4*>(DSr + j0 + 8 * a4 + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) dsn[4 * a4 + e] = x[e];
+    }
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) *reinterpret_cast<V4*>(Ks + (4 * v + lrow) * LD + lcol) = rk[v];
+  };
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  M::acc_t dq[DP / MT];
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt) dq[dt] = M::acc_t(0);
+  int kt = wave;
+  M::acc_t dsr = M::acc_t(0);
+  if (kt <= qt) {
+    fetch(kt);
+    put();
+    dsr = dsn;
+  }
+  wave_sync();
+  for (; kt <= qt; kt += 4) {
+    const bool more = kt + 4 <= qt;
+    if (more) fetch(kt + 4);
+    if (kt == qt) {  // the diagonal tile: entries above it were never written
+      const int lim = c - 4 * g;  // key 8a + 4g + e <= query c
+#pragma unroll
+      for (int a4 = 0; a4 < NACC / 4; ++a4)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dsr[4 * a4 + e] = 8 * a4 + e <= lim ? dsr[4 * a4 + e] : 0.f;
+    }
+    // dQ^T += K^T dS^T
+    mma_lds_t_regs<float, DP>(dq, Ks, 0, dsr, g, c);
+    wave_sync();
+    if (more) put();
+    wave_sync();
+    dsr = dsn;
+  }
+  __syncthreads();
+  float* R = lds + wave * PER_WAVE;
+#pragma unroll
+  for (int dt = 0; dt < DP / MT; ++dt)
+#pragma unroll
+    for (int i = 0; i < NACC; ++i) R[(dt * MT + M::row(i, g)) * (MT + 1) + c] = dq[dt][i];
+  __syncthreads();
+  float* DQ = (float*)a.dq + b * a.sdq.b + h * a.sdq.h;
+  const float scale = (float)a.scale;
+  for (int f = threadIdx.x; f < MT * DP; f += 256) {
+    const int q = f / DP, d = f % DP;
+    const int o = d * (MT + 1) + q;
+    float sq = lds[o];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) sq += lds[w * PER_WAVE + o];
+    DQ[(int64_t)(q0 + q) * a.sdq.t + d] = sq * scale;
+  }
 }
 
 template <typename T, int DP, bool FAST>
@@ -977,12 +1267,21 @@ static int attn_bwd_impl(AttnArgs& a) {
     else
       attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
     dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
-    if (a.ds) {
+    // float32, D = 64, T a multiple of 32: one key (query) tile per block with
+    // independent waves; otherwise 128-key (128-query) blocks
+    const bool kv1 = std::is_same<T, float>::value && a.ds && a.vec && a.D == 64 && a.T % 32 == 0;
+    if (kv1) {
+      dim3 g1((unsigned)(a.T / 32), (unsigned)(a.B * a.H));
+      attn_bwd_kv1_kernel<64><<<g1, 256, 0, stream()>>>(a);
+    } else if (a.ds) {
       DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
     } else {  // the aligned key-block pass writes dS unconditionally
       DP_SWITCH_F(dp, attn_bwd_kv_kernel, T, grid, false)
     }
-    if (a.ds) {
+    if (kv1) {
+      dim3 g1((unsigned)(a.T / 32), (unsigned)(a.B * a.H));
+      attn_bwd_q1_kernel<64><<<g1, 256, 0, stream()>>>(a);
+    } else if (a.ds) {
       DP_SWITCH(dp, attn_bwd_q_ds_kernel, T, grid)
     } else {
       DP_SWITCH(dp, attn_bwd_q_kernel, T, grid)

@@ -114,7 +114,8 @@ def test_recompute_dq_path_matches_oracle(dev, dt, shape):
 def test_backward_without_the_ds_workspace_matches_with_it(dev):
     """B*H*T*T float32 above 4 GiB: the dQ pass recomputes dS instead of
     reading it from a workspace. Splitting the heads in two keeps each half
-    under the limit (dS path); the two paths must agree."""
+    under the limit (dS path); the two paths must agree to the float32 bar (their
+    key passes add dK and dV over 6144 queries in different orders)."""
     D, K = _dev()
     B, H, T, Dh = 1, 32, 6144, 64
     rng = np.random.default_rng(21)
@@ -131,4 +132,4 @@ def test_backward_without_the_ds_workspace_matches_with_it(dev):
         halves.append([t.numpy() for t in K.attn_bwd(*sub, *stats)])  # 2.4 GB each: dS path
     for i, full in enumerate((dq, dk, dv)):
         ref = np.concatenate([halves[0][i], halves[1][i]], axis=1)
-        assert rel_err(full.numpy(), ref) <= 1e-6
+        assert rel_err(full.numpy(), ref) <= 1e-5
