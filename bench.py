@@ -75,7 +75,7 @@ def _median(xs):
 
 def cpu_baseline(weights, xs, ys, seq: int):
     """The oracle (NumPy restatement of dtrain) on the host cores, on a bounded
-    sample of the same step, as BASELINE's CPU plan asks:
+    sample of the same step:
       - forward+backward of one replica's first `seq` sequences: 1 warm-up,
         then the median of 3 runs, with the BLAS thread count the machine is
         configured for, and once more with 1 thread;
@@ -472,7 +472,7 @@ def micro_bucket_adamw(a):
     dp_, dm_, dv_, dr_ = D.from_numpy(p), D.from_numpy(m), D.from_numpy(v), D.from_numpy(reps)
     del reps
     g_ = D.empty((n,), dt)
-    nb = K.average_blocks(n)
+    nb = K.average_blocks(n, dt)
     parts = D.empty((nb,), np.float64)
     sq, s_dev = D.empty((1,), np.float64), D.empty((1,), np.float64)
     b1t, b2t = 1 - 0.9 ** 101, 1 - 0.95 ** 101

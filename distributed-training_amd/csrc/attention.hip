@@ -195,6 +195,25 @@ __device__ __forceinline__ void mma_lds_t_regs(typename AM<T>::acc_t (&out)[DP /
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ double ex2(double x) { return exp2(x); }
 
+// Raw buffer accesses: a wave-uniform resource (base address and byte range),
+// a per-lane byte offset that stays fixed over a loop and a wave-uniform byte
+// offset, so addressing takes no vector instructions (accesses beyond the
+// range read 0 and write nothing).
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint64_t bytes) {
+  const uint32_t n = bytes < 0xFFFFFFFFull ? (uint32_t)bytes : 0xFFFFFFFFu;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ AM<float>::vec_t buf_load4(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(AM<float>::vec_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ float buf_load1(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ void buf_store1(float x, Rsrc r, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, x), r, (int)voff, (int)soff, 0);
+}
+
 // Column swizzle of the transposed LDS tiles: XOR of bits 2-3 of the column
 // with bits 4-5 of the row, so groups of 4 columns stay 16-byte aligned and a
 // wave's transposed stores (16 rows 4 apart, 4 columns) hit 64 distinct banks.
@@ -767,7 +786,12 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
   const float* DR = (const float*)a.drow + (int64_t)bh * Tn;
   float* DS = (float*)a.ds + (int64_t)bh * Tn * Tn;
   const float sl2 = (float)(a.scale * 1.4426950408889634);
-  const unsigned ds_lane = (unsigned)(4 * g * Tn + kj) * 4u;
+  // buffer resources over this (batch, head)'s rows; byte offsets below
+  const Rsrc rQ = make_rsrc(Q, (uint64_t)Tn * a.sq.t * 4), rG = make_rsrc(G, (uint64_t)Tn * a.sdo.t * 4);
+  const Rsrc rM = make_rsrc(RM, (uint64_t)Tn * 4), rL = make_rsrc(RS, (uint64_t)Tn * 4),
+             rD = make_rsrc(DR, (uint64_t)Tn * 4);
+  const Rsrc rS = make_rsrc(DS, (uint64_t)Tn * Tn * 4);
+  const uint32_t ds_lane = (uint32_t)(4 * g * Tn + kj) * 4u;  // dS of row 4g, column kj
 
   float* W = lds + wave * PER_WAVE;
   float* Qs = W;
@@ -789,17 +813,17 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
   const int lrow = lane >> 4, lcol = (lane & 15) * 4;
   V4 rq[NV], rg[NV];
   float rm = 0.f, rl = 1.f, rd = 0.f;
+  const uint32_t vq = (uint32_t)(lrow * a.sq.t + lcol) * 4u, vg = (uint32_t)(lrow * a.sdo.t + lcol) * 4u;
+  const uint32_t vs = (uint32_t)(lane & (MT - 1)) * 4u;
   auto fetch = [&](int qs) {
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      const int64_t r = qs + 4 * v + lrow;
-      rq[v] = *reinterpret_cast<const V4*>(Q + r * a.sq.t + lcol);
-      rg[v] = *reinterpret_cast<const V4*>(G + r * a.sdo.t + lcol);
+      rq[v] = buf_load4(rQ, vq, (uint32_t)((qs + 4 * v) * a.sq.t) * 4u);
+      rg[v] = buf_load4(rG, vg, (uint32_t)((qs + 4 * v) * a.sdo.t) * 4u);
     }
-    const int sr = qs + (lane & (MT - 1));
-    rm = RM[sr];
-    rl = RS[sr];
-    rd = DR[sr];
+    rm = buf_load1(rM, vs, (uint32_t)qs * 4u);
+    rl = buf_load1(rL, vs, (uint32_t)qs * 4u);
+    rd = buf_load1(rD, vs, (uint32_t)qs * 4u);
   };
   auto put = [&]() {
 #pragma unroll
@@ -833,7 +857,6 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
     M::acc_t s = mma_rows_frag<float, DP>(M::acc_t(0), Qs, 0, kf, g, c);
     M::acc_t dp = mma_rows_rows<float, DP>(M::acc_t(0), Gs, Vs, g, c);
     const int lim = kj - qs - 4 * g;  // row qs + 4g + x sees key kj iff x >= lim
-    float* dsb = DS + (int64_t)qs * Tn;
     auto probs = [&](auto maskc) {
       constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
@@ -849,7 +872,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
           s[i] = p;
           const float v = p * (dp[i] - d4[e]);
           dp[i] = v;
-          *(float*)((char*)(dsb + (int64_t)(8 * a4 + e) * Tn) + ds_lane) = v;
+          buf_store1(v, rS, ds_lane, (uint32_t)((qs + 8 * a4 + e) * Tn) * 4u);  // dS[qs + 8a + 4g + e][kj]
         }
       }
     };
@@ -1031,20 +1054,22 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q1_kernel(AttnArgs a) {
   const int q0 = qt * MT;
   const int qr = q0 + c;  // this lane's query (column)
   const float* K = (const float*)a.k + b * a.sk.b + h * a.sk.h;
-  const float* DSr = (const float*)a.ds + (int64_t)bh * Tn * Tn + (int64_t)qr * Tn;  // row qr of dS
+  const float* DS = (const float*)a.ds + (int64_t)bh * Tn * Tn;
+  const Rsrc rK = make_rsrc(K, (uint64_t)Tn * a.sk.t * 4), rS = make_rsrc(DS, (uint64_t)Tn * Tn * 4);
   float* Ks = lds + wave * PER_WAVE;
   const int lrow = lane >> 4, lcol = (lane & 15) * 4;
+  const uint32_t vk = (uint32_t)(lrow * a.sk.t + lcol) * 4u;
+  const uint32_t vd = (uint32_t)(qr * Tn + 4 * g) * 4u;  // dS[qr][4g]
   V4 rk[NV];
   M::acc_t dsn;
   auto fetch = [&](int kt) {
     const int j0 = kt * MT;
 #pragma unroll
-    for (int v = 0; v < NV; ++v)
-      rk[v] = *reinterpret_cast<const V4*>(K + (int64_t)(j0 + 4 * v + lrow) * a.sk.t + lcol);
+    for (int v = 0; v < NV; ++v) rk[v] = buf_load4(rK, vk, (uint32_t)((j0 + 4 * v) * a.sk.t) * 4u);
     // lane (c, g), register 4 a + e: dS[qr][j0 + 8 a + 4 g + e]
 #pragma unroll
     for (int a4 = 0; a4 < NACC / 4; ++a4) {
-      const V4 x = *reinterpret_cast<const V4*>(DSr + j0 + 8 * a4 + 4 * g);
+      const V4 x = buf_load4(rS, vd, (uint32_t)(j0 + 8 * a4) * 4u);
 #pragma unroll
       for (int e = 0; e < 4; ++e) dsn[4 * a4 + e] = x[e];
     }
@@ -1193,6 +1218,85 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c);
 }
 
+// ------------------------------------------- head dimensions beyond 64
+// For D > 64 the scores of one batch element are materialised, [H, T, T] in
+// a pooled workspace, and the products run as batched GEMMs (dtmi_gemm):
+// S = Q K^T, P = softmax(S * scale + mask), O = P V; backward P recomputed
+// from S and the saved row statistics, dV = P^T dO, dP = dO V^T,
+// dS = P * (dP - rowsum(dP * P)) * scale, dQ = dS K, dK = dS^T Q -- dtrain's
+// products (autograd.py:226-246), one batch element at a time. One block per
+// row for the row passes, fixed reduction order.
+template <typename T>
+__device__ __forceinline__ T block_reduce_256(T x, T* red, bool is_max) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const T y = __shfl_xor(x, off, 64);
+    x = is_max ? fmax(x, y) : x + y;
+  }
+  __syncthreads();  // red is free
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  return is_max ? fmax(fmax(red[0], red[1]), fmax(red[2], red[3])) : ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// Rows t of one batch element's S [H, T, T] (row r = h * T + t): P in place,
+// row statistics to rowmax / rowsum at (b * H + h) * T + t (rowmax in base-2
+// units, as the flash kernels keep it).
+template <typename T>
+__global__ void __launch_bounds__(256) attn_rows_softmax_kernel(T* __restrict__ S, T* __restrict__ rowmax,
+                                                                 T* __restrict__ rowsum, int64_t Tn, int64_t row0,
+                                                                 double scale) {
+  __shared__ T red[4];
+  const int64_t r = blockIdx.x;
+  const int64_t t = r % Tn;
+  T* sr = S + r * Tn;
+  const T sc = (T)scale;
+  T m = -INFINITY;
+  for (int64_t j = threadIdx.x; j <= t; j += 256) m = fmax(m, sr[j] * sc);
+  m = block_reduce_256(m, red, true);
+  T l = T(0);
+  for (int64_t j = threadIdx.x; j < Tn; j += 256) {
+    const T p = j <= t ? exp(sr[j] * sc - m) : T(0);
+    sr[j] = p;
+    l += p;
+  }
+  l = block_reduce_256(l, red, false);
+  const T linv = T(1) / l;
+  for (int64_t j = threadIdx.x; j <= t; j += 256) sr[j] = sr[j] * linv;
+  if (threadIdx.x == 0) {
+    rowmax[row0 + r] = m * (T)1.4426950408889634;
+    rowsum[row0 + r] = l;
+  }
+}
+
+// P from S and the saved statistics, in place (entries above the diagonal 0).
+template <typename T>
+__global__ void __launch_bounds__(256) attn_rows_prob_kernel(T* __restrict__ S, const T* __restrict__ rowmax,
+                                                              const T* __restrict__ rowsum, int64_t Tn, int64_t row0,
+                                                              double scale) {
+  const int64_t r = blockIdx.x;
+  const int64_t t = r % Tn;
+  T* sr = S + r * Tn;
+  const T sl2 = (T)(scale * 1.4426950408889634);
+  const T m = rowmax[row0 + r], linv = T(1) / rowsum[row0 + r];
+  for (int64_t j = threadIdx.x; j < Tn; j += 256) sr[j] = j <= t ? ex2(sr[j] * sl2 - m) * linv : T(0);
+}
+
+// dS = P * (dP - rowsum(dP * P)) * scale, into dP.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_rows_dsoft_kernel(const T* __restrict__ P, T* __restrict__ dP, int64_t Tn,
+                                                               double scale) {
+  __shared__ T red[4];
+  const int64_t r = blockIdx.x;
+  const T* pr = P + r * Tn;
+  T* dr = dP + r * Tn;
+  T s = T(0);
+  for (int64_t j = threadIdx.x; j < Tn; j += 256) s += dr[j] * pr[j];
+  s = block_reduce_256(s, red, false);
+  const T sc = (T)scale;
+  for (int64_t j = threadIdx.x; j < Tn; j += 256) dr[j] = pr[j] * (dr[j] - s) * sc;
+}
+
 // ----------------------------------------------------------------- host
 static bool strides_vec(const Strides3& s, int64_t vec) { return s.b % vec == 0 && s.h % vec == 0 && s.t % vec == 0; }
 
@@ -1218,11 +1322,99 @@ static int pick_dp(int64_t D) {
     DP_SWITCH_F(dp, KERNEL, T, grid, false)             \
   }
 
+static int gemm_call(int dt, int akc, int bkc, int64_t M, int64_t N, int64_t K, const void* A, int64_t lda,
+                     int64_t sA, const void* B, int64_t ldb, int64_t sB, void* C, int64_t ldc, int64_t sC,
+                     int64_t batch) {
+  return dtmi_gemm(dt, akc, bkc, M, N, K, A, lda, sA, B, ldb, sB, C, ldc, sC, batch, nullptr, 0, 0);
+}
+
+template <typename T>
+static int attn_fwd_wide(AttnArgs& a) {
+  const int dt = sizeof(T) == 4 ? DTMI_F32 : DTMI_F64;
+  const int64_t B = a.B, H = a.H, Tn = a.T, D = a.D;
+  void* S = nullptr;
+  int rc = pool_alloc(&S, (size_t)H * Tn * Tn * sizeof(T));
+  if (rc) return rc;
+  for (int64_t b = 0; b < B && rc == 0; ++b) {
+    const T* Q = (const T*)a.q + b * a.sq.b;
+    const T* K = (const T*)a.k + b * a.sk.b;
+    const T* V = (const T*)a.v + b * a.sv.b;
+    T* O = (T*)a.out + b * a.so.b;
+    // S[h] = Q[h] K[h]^T (the scale is applied in the row pass)
+    rc = gemm_call(dt, 1, 1, Tn, Tn, D, Q, a.sq.t, a.sq.h, K, a.sk.t, a.sk.h, S, Tn, Tn * Tn, H);
+    if (rc) break;
+    {
+      TimedLaunch tl(DTMI_FAM_ATTN_FWD, 0.0);
+      attn_rows_softmax_kernel<T><<<(unsigned)(H * Tn), 256, 0, stream()>>>((T*)S, (T*)a.rowmax, (T*)a.rowsum, Tn,
+                                                                             b * H * Tn, a.scale);
+    }
+    // O[h] = P[h] V[h]
+    rc = gemm_call(dt, 1, 0, Tn, D, Tn, S, Tn, Tn * Tn, V, a.sv.t, a.sv.h, O, a.so.t, a.so.h, H);
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(S);
+  if (rc) return rc;
+  if (le != hipSuccess) return fail_hip(le, "attention (D > 64) kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+}
+
+template <typename T>
+static int attn_bwd_wide(AttnArgs& a) {
+  const int dt = sizeof(T) == 4 ? DTMI_F32 : DTMI_F64;
+  const int64_t B = a.B, H = a.H, Tn = a.T, D = a.D;
+  void* P = nullptr;
+  void* dP = nullptr;
+  int rc = pool_alloc(&P, (size_t)H * Tn * Tn * sizeof(T));
+  if (rc) return rc;
+  rc = pool_alloc(&dP, (size_t)H * Tn * Tn * sizeof(T));
+  if (rc) {
+    pool_free(P);
+    return rc;
+  }
+  const int64_t TT = Tn * Tn;
+  for (int64_t b = 0; b < B && rc == 0; ++b) {
+    const T* Q = (const T*)a.q + b * a.sq.b;
+    const T* K = (const T*)a.k + b * a.sk.b;
+    const T* V = (const T*)a.v + b * a.sv.b;
+    const T* G = (const T*)a.dO + b * a.sdo.b;
+    T* dQ = (T*)a.dq + b * a.sdq.b;
+    T* dK = (T*)a.dk + b * a.sdk.b;
+    T* dV = (T*)a.dv + b * a.sdv.b;
+    rc = gemm_call(dt, 1, 1, Tn, Tn, D, Q, a.sq.t, a.sq.h, K, a.sk.t, a.sk.h, P, Tn, TT, H);  // S
+    if (rc) break;
+    {
+      TimedLaunch tl(DTMI_FAM_ATTN_BWD, 0.0);
+      attn_rows_prob_kernel<T><<<(unsigned)(H * Tn), 256, 0, stream()>>>((T*)P, (const T*)a.rowmax,
+                                                                          (const T*)a.rowsum, Tn, b * H * Tn, a.scale);
+    }
+    // dV = P^T dO: A(m = key, k = query) = P[query][key]
+    rc = gemm_call(dt, 0, 0, Tn, D, Tn, P, Tn, TT, G, a.sdo.t, a.sdo.h, dV, a.sdv.t, a.sdv.h, H);
+    if (rc) break;
+    // dP = dO V^T
+    rc = gemm_call(dt, 1, 1, Tn, Tn, D, G, a.sdo.t, a.sdo.h, V, a.sv.t, a.sv.h, dP, Tn, TT, H);
+    if (rc) break;
+    {
+      TimedLaunch tl(DTMI_FAM_ATTN_BWD, 0.0);
+      attn_rows_dsoft_kernel<T><<<(unsigned)(H * Tn), 256, 0, stream()>>>((const T*)P, (T*)dP, Tn, a.scale);
+    }
+    // dQ = dS K ; dK = dS^T Q
+    rc = gemm_call(dt, 1, 0, Tn, D, Tn, dP, Tn, TT, K, a.sk.t, a.sk.h, dQ, a.sdq.t, a.sdq.h, H);
+    if (rc) break;
+    rc = gemm_call(dt, 0, 0, Tn, D, Tn, dP, Tn, TT, Q, a.sq.t, a.sq.h, dK, a.sdk.t, a.sdk.h, H);
+  }
+  hipError_t le = hipGetLastError();
+  pool_free(P);
+  pool_free(dP);
+  if (rc) return rc;
+  if (le != hipSuccess) return fail_hip(le, "attention backward (D > 64) kernels", __FILE__, __LINE__);
+  return DTMI_OK;
+}
+
 template <typename T>
 static int attn_fwd_impl(AttnArgs& a) {
   constexpr int MT = AM<T>::MT;
   const int dp = pick_dp<T>(a.D);
-  DTMI_CHECK(dp > 0, "dtmi_attn_fwd: head dimension %lld > 64 is not supported", (long long)a.D);
+  if (dp < 0) return attn_fwd_wide<T>(a);
   dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
   // causal-exact FLOP: 2 GEMMs of 2*D*T(T+1)/2 per (b, h)
   TimedLaunch tl(DTMI_FAM_ATTN_FWD, 2.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
@@ -1240,7 +1432,7 @@ template <typename T>
 static int attn_bwd_impl(AttnArgs& a) {
   constexpr int MT = AM<T>::MT;
   const int dp = pick_dp<T>(a.D);
-  DTMI_CHECK(dp > 0, "dtmi_attn_bwd: head dimension %lld > 64 is not supported", (long long)a.D);
+  if (dp < 0) return attn_bwd_wide<T>(a);
   const int64_t rows = a.B * a.H * a.T;
   void* drow = nullptr;
   int rc = pool_alloc(&drow, (size_t)rows * sizeof(T));

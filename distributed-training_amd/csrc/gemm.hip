@@ -44,6 +44,7 @@
 // summed in split order by a second kernel (deterministic, no atomics).
 #include "common.h"
 #include "gelu.h"
+#include "rowln.h"
 
 namespace dtmi {
 
@@ -1135,6 +1136,81 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
   }
 }
 
+// Split-K sum, bias and residual of an output row, then the LayerNorm of the
+// finished row, in one pass: one wave per row, the row in registers. The
+// output element is (((p_0 + p_1) + ...) + bias) then residual + that -- the
+// reduction kernel's and epilogue's order -- and the LayerNorm is the shared
+// row code of the LayerNorm kernel, so C, ln_out, mean and rstd are the bits
+// the separate kernels give. 16-byte aligned rows, unbatched.
+template <typename T, int NV, int VW>
+__global__ void __launch_bounds__(256) splitk_ln_kernel(GemmArgs a, const T* __restrict__ ws, int splits,
+                                                         T* __restrict__ hout, T* __restrict__ mean,
+                                                         T* __restrict__ rstd, const T* __restrict__ lw,
+                                                         const T* __restrict__ lb, T eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t M = a.M;
+  const int cols = (int)a.N;
+  if (row >= M) return;
+  const int64_t total = M * a.N;
+  const T* bias = (const T*)a.bias;
+  const T* add = (const T*)a.addend;
+  T* C = (T*)a.C;
+  // every load of the row is issued before the first add, from addresses
+  // that are always valid (a missing split, bias or residual re-reads the
+  // first partial and is then left out), so no load waits behind a branch
+  constexpr int SP = NV * VW <= 16 ? 4 : (NV * VW <= 32 ? 2 : 1);
+  T pv[SP][NV][VW], bv[NV][VW], rv[NV][VW];
+  const T* bsrc = bias ? bias : ws;
+  const T* rsrc = add ? add + row * a.ldc : ws + row * a.N;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = VW * lane + 64 * VW * j;
+    const int cc = c < cols ? c : 0;
+    const int64_t idx = row * a.N + cc;
+#pragma unroll
+    for (int sp = 0; sp < SP; ++sp) load_vec<T, VW>(pv[sp][j], ws + (int64_t)(sp < splits ? sp : 0) * total + idx);
+    load_vec<T, VW>(bv[j], bsrc + cc);
+    load_vec<T, VW>(rv[j], rsrc + cc);
+  }
+  T xv[NV][VW];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = VW * lane + 64 * VW * j;
+    T v[VW];
+#pragma unroll
+    for (int e = 0; e < VW; ++e) v[e] = pv[0][j][e];
+#pragma unroll
+    for (int sp = 1; sp < SP; ++sp)
+      if (sp < splits)
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v[e] = v[e] + pv[sp][j][e];
+    if (c < cols) {
+      for (int sp = SP; sp < splits; ++sp) {  // more splits than held in registers
+        T t[VW];
+        load_vec<T, VW>(t, ws + (int64_t)sp * total + row * a.N + c);
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v[e] = v[e] + t[e];
+      }
+    }
+    if (bias)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[e] = v[e] + bv[j][e];
+    if (add)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) v[e] = rv[j][e] + v[e];
+    if (c < cols) {
+      store_vec<T, VW>(C + row * a.ldc + c, v);
+#pragma unroll
+      for (int e = 0; e < VW; ++e) xv[j][e] = v[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) xv[j][e] = T(0);
+    }
+  }
+  ln_row_fwd<T, NV, VW>(xv, cols, lane, lw, lb, eps, hout + row * cols, mean + row, rstd + row);
+}
+
 template <typename T, int BM, int BN, bool AKC, bool BKC>
 static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb, bool dma) {
   if constexpr (std::is_same<T, float>::value) {
@@ -1187,6 +1263,14 @@ struct EpiArgs {
   void* aux = nullptr;
   void* colsum = nullptr;  // column sums of B (length N), unbatched
   int colsum_accumulate = 0;
+  // LayerNorm of the finished output rows (after bias and residual):
+  // ln_out = layer_norm(C; ln_w, ln_b, ln_eps), with the row mean and rstd
+  void* ln_out = nullptr;
+  void* ln_mean = nullptr;
+  void* ln_rstd = nullptr;
+  const void* ln_w = nullptr;
+  const void* ln_b = nullptr;
+  double ln_eps = 1e-5;
 };
 
 // K splits. A grid of b blocks on C CUs runs ceil(b / C) rounds, so its
@@ -1279,6 +1363,14 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
     a.ws = ws;
     if (a.colsum) a.colsum_ws = (char*)ws + main_bytes;
   }
+  // A LayerNorm of the output rows is fused into the split-K sum when the
+  // rows fit the row kernel; otherwise it runs as its own pass afterwards.
+  constexpr int LVW = 16 / sizeof(T);
+  const int ln_nv = ep.ln_out ? ln_pick_nv(cdiv(N, 64LL * LVW)) : -1;
+  const bool ln_fused = splits > 1 && ep.ln_out && batch == 1 && !a.accumulate && a.epi == kEpiNone &&
+                        N % LVW == 0 && ldc == N && ln_nv > 0 && aligned(C, 16) && (!bias || aligned(bias, 16)) &&
+                        (!a.addend || aligned(a.addend, 16)) && aligned(ep.ln_out, 16) && aligned(ep.ln_w, 16) &&
+                        aligned(ep.ln_b, 16);
   dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
   {
     TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
@@ -1294,7 +1386,7 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
     } else {
       launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb, dma);
     }
-    if (splits > 1) {
+    if (splits > 1 && !ln_fused) {
       int64_t total = batch * M * N;
       int rg = (int)(cdiv(total, 256 * 4) < 8192 ? cdiv(total, 256 * 4) : 8192);
       GemmArgs r = a;
@@ -1314,9 +1406,25 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
         splitk_reduce_kernel<T, false, 1><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
     }
   }
+  if (ln_fused) {
+    // split-K partials, bias and residual in; C and the LayerNorm out
+    TimedLaunch tl(DTMI_FAM_OTHER, (double)M * N * sizeof(T) * (splits + (a.addend ? 3 : 2)));
+    GemmArgs r = a;
+    r.ws = nullptr;
+    const unsigned lg = (unsigned)cdiv(M, 4);
+#define CALL_LN(NV)                                                                                          \
+  splitk_ln_kernel<T, NV, LVW><<<lg, 256, 0, stream()>>>(r, (const T*)ws, splits, (T*)ep.ln_out, (T*)ep.ln_mean, \
+                                                          (T*)ep.ln_rstd, (const T*)ep.ln_w, (const T*)ep.ln_b,   \
+                                                          (T)ep.ln_eps)
+    LN_NV_SWITCH(ln_nv, CALL_LN)
+#undef CALL_LN
+  }
   hipError_t le = hipGetLastError();
   if (ws) pool_free(ws);
   if (le != hipSuccess) return fail_hip(le, "gemm kernels", __FILE__, __LINE__);
+  if (ep.ln_out && !ln_fused)  // the LayerNorm as its own pass over C
+    return dtmi_layernorm_fwd(std::is_same<T, float>::value ? DTMI_F32 : DTMI_F64, ep.ln_out, ep.ln_mean, ep.ln_rstd,
+                              C, ep.ln_w, ep.ln_b, M, N, ep.ln_eps);
   return DTMI_OK;
 }
 
@@ -1390,6 +1498,25 @@ DTMI_EXPORT int dtmi_linear_fwd_fused(int dtype, void* Y, void* act, const void*
   ep.epi = act ? kEpiGeluFwd : kEpiNone;
   ep.aux = act;
   DTMI_CHECK(!(act && residual), "dtmi_linear_fwd_fused: GELU and residual are not fused together");
+  return gemm_dispatch(dtype, 1, 0, M, N, K, X, K, 0, W, N, 0, Y, N, 0, 1, b, 0, 0, ep);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_fwd_ln(int dtype, void* Y, void* H, void* mean, void* rstd, const void* X, const void* W,
+                                   const void* b, const void* residual, const void* ln_w, const void* ln_b, double eps,
+                                   int64_t M, int64_t K, int64_t N) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_CHECK(H && mean && rstd && ln_w && ln_b, "dtmi_linear_fwd_ln: NULL LayerNorm pointer");
+  DTMI_CHECK(H != Y, "dtmi_linear_fwd_ln: the LayerNorm output must not be Y");
+  EpiArgs ep;
+  ep.addend = residual;
+  ep.ln_out = H;
+  ep.ln_mean = mean;
+  ep.ln_rstd = rstd;
+  ep.ln_w = ln_w;
+  ep.ln_b = ln_b;
+  ep.ln_eps = eps;
   return gemm_dispatch(dtype, 1, 0, M, N, K, X, K, 0, W, N, 0, Y, N, 0, 1, b, 0, 0, ep);
   DTMI_BODY_END
 }

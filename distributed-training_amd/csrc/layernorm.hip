@@ -3,7 +3,8 @@
 // One 64-lane wave owns one row; the row lives in registers (each lane holds
 // NV 16-byte vectors, or NV scalars when the row is not vector-aligned), so x
 // and dy are read from HBM exactly once and the row reductions are wave
-// butterflies (no LDS, no barriers). Four waves per 256-thread block.
+// butterflies (no LDS, no barriers). Four waves per 256-thread block. Rows
+// longer than 16 vectors per lane take a block per row instead (below).
 //
 // Backward fuses dx with the column reductions dgamma = sum_rows(dy * xh) and
 // dbeta = sum_rows(dy): every wave accumulates its rows' contributions in
@@ -15,41 +16,9 @@
 
 #include "colreduce.h"
 #include "common.h"
+#include "rowln.h"
 
 namespace dtmi {
-
-template <typename T>
-__device__ __forceinline__ T wave_sum(T x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
-
-// Lane `lane` owns elements  VW*lane + 64*VW*j + e  (j < NV, e < VW).
-template <typename T, int NV, int VW>
-struct RowRegs {
-  T v[NV][VW];
-};
-
-template <typename T, int VW>
-__device__ __forceinline__ void load_vec(T (&dst)[VW], const T* __restrict__ src) {
-  if constexpr (VW * sizeof(T) == 16) {
-    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
-  } else {
-#pragma unroll
-    for (int e = 0; e < VW; ++e) dst[e] = src[e];
-  }
-}
-
-template <typename T, int VW>
-__device__ __forceinline__ void store_vec(T* __restrict__ dst, const T (&src)[VW]) {
-  if constexpr (VW * sizeof(T) == 16) {
-    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
-  } else {
-#pragma unroll
-    for (int e = 0; e < VW; ++e) dst[e] = src[e];
-  }
-}
 
 template <typename T, int NV, int VW>
 __global__ void __launch_bounds__(256) ln_fwd_kernel(T* __restrict__ y, T* __restrict__ mean_out,
@@ -61,7 +30,6 @@ __global__ void __launch_bounds__(256) ln_fwd_kernel(T* __restrict__ y, T* __res
   if (row >= rows) return;
   const T* xr = x + row * cols;
   T xv[NV][VW];
-  T s = T(0);
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int c = VW * lane + 64 * VW * j;
@@ -71,45 +39,8 @@ __global__ void __launch_bounds__(256) ln_fwd_kernel(T* __restrict__ y, T* __res
 #pragma unroll
       for (int e = 0; e < VW; ++e) xv[j][e] = T(0);
     }
-#pragma unroll
-    for (int e = 0; e < VW; ++e) s += xv[j][e];
   }
-  const T n = (T)cols;
-  const T mu = wave_sum(s) / n;
-  T q = T(0);
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = VW * lane + 64 * VW * j;
-    if (c < cols) {
-#pragma unroll
-      for (int e = 0; e < VW; ++e) {
-        T xc = xv[j][e] - mu;
-        q += xc * xc;
-      }
-    }
-  }
-  const T var = wave_sum(q) / n;
-  const T rstd = T(1) / sqrt(var + eps);
-  T* yr = y + row * cols;
-#pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int c = VW * lane + 64 * VW * j;
-    if (c < cols) {
-      T wv[VW], bv[VW], o[VW];
-      load_vec<T, VW>(wv, w + c);
-      load_vec<T, VW>(bv, b + c);
-#pragma unroll
-      for (int e = 0; e < VW; ++e) {
-        T xh = (xv[j][e] - mu) * rstd;
-        o[e] = xh * wv[e] + bv[e];
-      }
-      store_vec<T, VW>(yr + c, o);
-    }
-  }
-  if (lane == 0) {
-    mean_out[row] = mu;
-    rstd_out[row] = rstd;
-  }
+  ln_row_fwd<T, NV, VW>(xv, cols, lane, w, b, eps, y + row * cols, mean_out + row, rstd_out + row);
 }
 
 // Blocks needed for the deterministic column partials: a function of rows only.
@@ -259,6 +190,102 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
   }
 }
 
+// ------------------------------------------------------------- wide rows
+// Rows longer than a wave's registers hold (more than 16 vectors per lane):
+// one 256-thread block per row, the row re-read from memory per pass (mean,
+// variance, output; backward: the two row sums, then dx). Column partials of
+// dgamma / dbeta: each block accumulates its rows' contributions into its own
+// partial row in memory (each thread owns the same columns of every row, so
+// the updates are ordered), summed in block order by the column reduction.
+template <typename T>
+__device__ __forceinline__ T block_sum_bcast(T x, T* red) {
+  x = wave_sum(x);
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();  // red is free (its previous values were read)
+  if ((threadIdx.x & 63) == 0) red[wave] = x;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) ln_fwd_wide_kernel(T* __restrict__ y, T* __restrict__ mean_out,
+                                                           T* __restrict__ rstd_out, const T* __restrict__ x,
+                                                           const T* __restrict__ w, const T* __restrict__ b,
+                                                           int64_t rows, int64_t cols, T eps) {
+  __shared__ T red[4];
+  const T n = (T)cols;
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T* xr = x + row * cols;
+    T s = T(0);
+    for (int64_t c = threadIdx.x; c < cols; c += 256) s += xr[c];
+    const T mu = block_sum_bcast(s, red) / n;
+    T q = T(0);
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      T xc = xr[c] - mu;
+      q += xc * xc;
+    }
+    const T var = block_sum_bcast(q, red) / n;
+    const T rstd = T(1) / sqrt(var + eps);
+    T* yr = y + row * cols;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      T xh = (xr[c] - mu) * rstd;
+      yr[c] = xh * w[c] + b[c];
+    }
+    if (threadIdx.x == 0) {
+      mean_out[row] = mu;
+      rstd_out[row] = rstd;
+    }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) ln_bwd_wide_kernel(T* __restrict__ dx, T* __restrict__ part_dw,
+                                                           T* __restrict__ part_db, const T* __restrict__ dy,
+                                                           const T* __restrict__ x, const T* __restrict__ w,
+                                                           const T* __restrict__ mean, const T* __restrict__ rstd,
+                                                           const T* __restrict__ addend, int64_t rows, int64_t cols,
+                                                           int accumulate_dx) {
+  __shared__ T red[4];
+  const T n = (T)cols;
+  T* pw = part_dw + (int64_t)blockIdx.x * cols;
+  T* pb = part_db + (int64_t)blockIdx.x * cols;
+  for (int64_t c = threadIdx.x; c < cols; c += 256) pw[c] = pb[c] = T(0);
+  for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const T mu = mean[row], rs = rstd[row];
+    const T* xr = x + row * cols;
+    const T* gr = dy + row * cols;
+    T s1 = T(0), s2 = T(0);
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      const T xh = (xr[c] - mu) * rs;
+      const T gxh = gr[c] * w[c];
+      s1 += gxh;
+      s2 += gxh * xh;
+    }
+    const T m1 = block_sum_bcast(s1, red) / n;
+    const T m2 = block_sum_bcast(s2, red) / n;
+    T* dr = dx + row * cols;
+    const T* ar = addend ? addend + row * cols : nullptr;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+      const T gv = gr[c];
+      const T xh = (xr[c] - mu) * rs;
+      const T gxh = gv * w[c];
+      const T r = rs * ((gxh - m1) - xh * m2);
+      dr[c] = accumulate_dx ? dr[c] + r : (ar ? ar[c] + r : r);
+      pw[c] += gv * xh;
+      pb[c] += gv;
+    }
+  }
+}
+
+// Blocks of the wide backward: one partial row each, at most 512 and at most
+// 64 MiB of partials.
+static int ln_bwd_wide_blocks(int64_t rows, int64_t cols, size_t es) {
+  int64_t b = rows < 512 ? rows : 512;
+  const int64_t cap = ((int64_t)64 << 20) / (2 * cols * (int64_t)es);
+  if (b > cap) b = cap;
+  return (int)(b < 1 ? 1 : b);
+}
+
 // ---------------------------------------------------------------- dispatch
 template <typename T, int VW>
 struct LnDispatch {
@@ -274,33 +301,21 @@ struct LnDispatch {
   }
 };
 
-#define LN_NV_SWITCH(nv, CALL) \
-  switch (nv) {                \
-    case 1: CALL(1); break;    \
-    case 2: CALL(2); break;    \
-    case 3: CALL(3); break;    \
-    case 4: CALL(4); break;    \
-    case 6: CALL(6); break;    \
-    case 8: CALL(8); break;    \
-    case 12: CALL(12); break;  \
-    default: CALL(16); break;  \
-  }
-
-static int pick_nv(int64_t per_lane) {
-  static const int opts[] = {1, 2, 3, 4, 6, 8, 12, 16};
-  for (int o : opts)
-    if (per_lane <= o) return o;
-  return -1;
-}
-
 template <typename T>
 static int ln_fwd(void* y, void* mean, void* rstd, const void* x, const void* w, const void* b, int64_t rows,
                   int64_t cols, double eps) {
   constexpr int VWV = 16 / sizeof(T);
   bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(y, 16) && aligned(w, 16) && aligned(b, 16);
   int vw = vec ? VWV : 1;
-  int nv = pick_nv(cdiv(cols, 64LL * vw));
-  DTMI_CHECK(nv > 0, "dtmi_layernorm_fwd: rows of %lld elements exceed the supported %d", (long long)cols, 64 * 16 * vw);
+  int nv = ln_pick_nv(cdiv(cols, 64LL * vw));
+  if (nv < 0) {  // longer rows than a wave holds
+    TimedLaunch tl(DTMI_FAM_OTHER, (double)rows * cols * 2 * sizeof(T));
+    const unsigned g = (unsigned)(rows < 4096 ? rows : 4096);
+    ln_fwd_wide_kernel<T><<<g, 256, 0, stream()>>>((T*)y, (T*)mean, (T*)rstd, (const T*)x, (const T*)w,
+                                                    (const T*)b, rows, cols, (T)eps);
+    LAUNCH_CHECK("ln_fwd_wide_kernel");
+    return DTMI_OK;
+  }
   int grid = (int)cdiv(rows, 4);
   TimedLaunch tl(DTMI_FAM_OTHER, (double)rows * cols * 2 * sizeof(T));
   T* Y = (T*)y;
@@ -330,9 +345,9 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
   bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(dy, 16) && aligned(dx, 16) && aligned(w, 16) &&
              aligned(addend, 16);
   int vw = vec ? VWV : 1;
-  int nv = pick_nv(cdiv(cols, 64LL * vw));
-  DTMI_CHECK(nv > 0, "dtmi_layernorm_bwd: rows of %lld elements exceed the supported %d", (long long)cols, 64 * 16 * vw);
-  const int grid = ln_bwd_blocks(rows);
+  const int nv = ln_pick_nv(cdiv(cols, 64LL * vw));
+  const bool wide = nv < 0;  // longer rows than a wave holds
+  const int grid = wide ? ln_bwd_wide_blocks(rows, cols, sizeof(T)) : ln_bwd_blocks(rows);
   const size_t part_bytes = (size_t)2 * grid * cols * sizeof(T);
   void* parts = scratch_ptr;
   if (scratch_ptr) {
@@ -356,7 +371,9 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
     int c = (int)cols;
     int acc = (accumulate & 1) ? 1 : 0;
     const T* ADD = (const T*)addend;
-    if (vec) {
+    if (wide) {
+      ln_bwd_wide_kernel<T><<<grid, 256, 0, stream()>>>(DX, pdw, pdb, DY, X, W, MU, RS, ADD, rows, cols, acc);
+    } else if (vec) {
 #define CALLV(NV) LnDispatch<T, VWV>::template bwd<NV>(grid, DX, pdw, pdb, DY, X, W, MU, RS, ADD, rows, c, acc)
       LN_NV_SWITCH(nv, CALLV)
 #undef CALLV

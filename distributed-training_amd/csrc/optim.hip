@@ -1,13 +1,14 @@
 // Optimizer and gradient-bucket kernels: fused AdamW (flat and multi-tensor),
-// bucket flatten, fixed-order replica average with fused sum of squares,
+// bucket flatten, rank-ordered replica average with fused sum of squares,
 // deterministic sum of squares and the clip factor.
 //
 // All of these are HBM-bound streaming kernels: 16-byte vector loads and stores
 // (4 floats / 2 doubles) when every operand is 16-byte aligned, over a grid
 // that depends only on the problem size (so per-block partial sums, and
-// therefore results, are the same on every run and every device). AdamW and
-// the replica average run one pass of 1024-element blocks with non-temporal
-// accesses; the multi-tensor kernels walk 32768-element chunks.
+// therefore results, are the same on every run and every device). AdamW runs
+// one pass of 1024-element blocks, the replica average one pass of blocks of
+// four vectors per thread, both with non-temporal accesses; the multi-tensor
+// kernels walk 32768-element chunks.
 //
 // Bit-exactness: this file is compiled with -ffp-contract=off and every update
 // below is written as the same sequence of IEEE operations NumPy performs for
@@ -327,39 +328,52 @@ __device__ __forceinline__ double sq64(T x) {
 // With SUMSQ the block's float64 sum of out^2 goes to partials[blockIdx.x]
 // (fixed pattern). WC > 0 fixes the replica count at compile time (the vector
 // path then loads all replicas at once); WC = 0 takes it from `world`.
-constexpr int kMaxSegs = 32;
+constexpr int kMaxSegs = 16;
+// Vectors per thread of the average's blocks: 4 (all of a block's loads in
+// flight at once) for arrays of at least 4M elements, else 1 (more blocks).
+constexpr int64_t kAvgWideFrom = (int64_t)1 << 22;
+template <typename T>
+constexpr int64_t avg_elems(int per) {
+  return 256 * per * (16 / (int64_t)sizeof(T));
+}
+// Segments of one launch: start[j] (start[0] = 0; entries past nseg hold
+// INT32_MAX, so every test below ignores them without a count) and the first
+// rank of each, packed four to a word. Read with compile-time indices only,
+// so the table stays in scalar registers.
 struct RankSegs {
-  int64_t start[kMaxSegs + 1];  // start[0] = 0, start[nseg] = n
-  int first[kMaxSegs];
-  int nseg;
+  int32_t start[kMaxSegs];
+  uint32_t first4[kMaxSegs / 4];
 };
+__device__ __forceinline__ int seg_rank(const RankSegs& sg, int j) { return (sg.first4[j >> 2] >> (8 * (j & 3))) & 0xFF; }
 
-// The first rank of element k's segment (a compare per segment, all indices
-// compile-time constants, so the table stays in scalar kernel-argument loads).
+// The first rank of element k's segment.
 __device__ __forceinline__ int seg_first(const RankSegs& sg, int64_t k) {
-  int f = sg.first[0];
+  int f = seg_rank(sg, 0);
 #pragma unroll
   for (int j = 1; j < kMaxSegs; ++j)
-    if (j < sg.nseg && k >= sg.start[j]) f = sg.first[j];
+    if (k >= sg.start[j]) f = seg_rank(sg, j);
   return f;
 }
 
-template <typename T, bool VEC, bool SUMSQ, int WC, bool ROT>
+template <typename T, bool VEC, bool SUMSQ, int WC, bool ROT, int PER>
 __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out, const T* __restrict__ rep,
                                                               int world, int64_t n, int64_t stride, T inv,
                                                               double* __restrict__ partials, RankSegs sg) {
   __shared__ double lds[4];
-  const int64_t base = (int64_t)blockIdx.x * kBlockElems;
+  constexpr int64_t kAvgElems = avg_elems<T>(PER);
+  const int64_t base = (int64_t)blockIdx.x * kAvgElems;
   // rank order of the block: uniform when the block lies in one segment
   int bfirst = 0;
   bool mixed = false;
   if (ROT) {
-    const int64_t bend = base + kBlockElems < n ? base + kBlockElems : n;
-    bfirst = seg_first(sg, base);
-    mixed = seg_first(sg, bend - 1) != bfirst;
+    const int64_t bend = base + kAvgElems < n ? base + kAvgElems : n;
+    bfirst = seg_rank(sg, 0);
 #pragma unroll
-    for (int j = 1; j < kMaxSegs; ++j)  // a segment boundary strictly inside the block
-      if (j < sg.nseg && sg.start[j] > base && sg.start[j] < bend) mixed = true;
+    for (int j = 1; j < kMaxSegs; ++j) {
+      const int64_t st = sg.start[j];
+      if (st <= base) bfirst = seg_rank(sg, j);
+      mixed = mixed || (st > base && st < bend);  // a segment boundary strictly inside the block
+    }
   }
   // replica row of position r in the block's order
   auto row = [&](int r) {
@@ -379,26 +393,87 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
     return a;
   };
   double acc = 0.0;
-  if (VEC && !(ROT && mixed)) {
+  if (VEC && (WC > 0 || !(ROT && mixed))) {
     using VT = typename V16<T>::type;
     constexpr int N = V16<T>::N;
-    constexpr int PER = kBlockElems / 256 / N;
+    if constexpr (WC > 0) {
+      // WC replicas known at compile time: every load of the block is issued
+      // before the first add (rows in rank order 0..W-1, so no load waits for
+      // the segment lookup), and the adds follow the block's rank order
+      VT v[PER][WC];
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int64_t e0 = base + (int64_t)(u * 256 + threadIdx.x) * N;
+        if (e0 + N <= n)
+#pragma unroll
+          for (int r = 0; r < WC; ++r) v[u][r] = ld_nt(reinterpret_cast<const VT*>(rep + (int64_t)r * stride) + e0 / N);
+      }
+      // ((v_f + v_{f+1}) + ...) + v_{f-1}: one compile-time order per first rank
+      auto ordered_sum = [&](const VT(&x)[WC]) {
+        VT a = x[0];
+        auto fold = [&](auto fc) {
+          constexpr int F = decltype(fc)::value;
+          a = x[F];
+#pragma unroll
+          for (int r = 1; r < WC; ++r) a = a + x[(F + r) % WC];
+        };
+        if (!ROT) {
+          fold(std::integral_constant<int, 0>{});
+        } else {
+          switch (bfirst) {
+            case 0: fold(std::integral_constant<int, 0>{}); break;
+            case 1: fold(std::integral_constant<int, 1 % WC>{}); break;
+            case 2: fold(std::integral_constant<int, 2 % WC>{}); break;
+            default: fold(std::integral_constant<int, 3 % WC>{}); break;
+          }
+        }
+        return a;
+      };
+      // a block across a segment edge: each element in its own segment's
+      // order (every order is summed, the element's is kept)
+      auto mixed_sum = [&](const VT(&x)[WC], int64_t e0) {
+        VT a;
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          const int f = seg_first(sg, e0 + e);
+          T pick = T(0);
+#pragma unroll
+          for (int F = 0; F < WC; ++F) {
+            T t = vget<T>(x[F], e);
+#pragma unroll
+            for (int r = 1; r < WC; ++r) t = t + vget<T>(x[(F + r) % WC], e);
+            pick = f == F ? t : pick;
+          }
+          vset<T>(a, e, pick);
+        }
+        return a;
+      };
+#pragma unroll
+      for (int u = 0; u < PER; ++u) {
+        const int64_t e0 = base + (int64_t)(u * 256 + threadIdx.x) * N;
+        if (e0 + N <= n) {
+          VT a = ROT && mixed ? mixed_sum(v[u], e0) : ordered_sum(v[u]);
+          a = a * inv;
+          if (SUMSQ)
+#pragma unroll
+            for (int e = 0; e < N; ++e) acc += sq64(vget<T>(a, e));
+          st_nt(a, reinterpret_cast<VT*>(out) + e0 / N);
+        } else if (e0 < n) {
+          for (int64_t k = e0; k < n; ++k) {  // ragged end
+            T o = elem(k) * inv;
+            out[k] = o;
+            if (SUMSQ) acc += sq64(o);
+          }
+        }
+      }
+    } else {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int64_t e0 = base + (int64_t)(u * 256 + threadIdx.x) * N;
       if (e0 + N <= n) {
         const int64_t k = e0 / N;
         VT a;
-        if constexpr (WC > 0) {
-          // WC replicas known at compile time: every load is issued before
-          // the first add, and the adds keep the rank order
-          VT v[WC];
-#pragma unroll
-          for (int r = 0; r < WC; ++r) v[r] = ld_nt(reinterpret_cast<const VT*>(row(r)) + k);
-          a = v[0];
-#pragma unroll
-          for (int r = 1; r < WC; ++r) a = a + v[r];
-        } else {
+        {
           a = ld_nt(reinterpret_cast<const VT*>(row(0)) + k);
           for (int r = 1; r < world; ++r) a = a + ld_nt(reinterpret_cast<const VT*>(row(r)) + k);
         }
@@ -415,8 +490,9 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
         }
       }
     }
+    }
   } else {
-    for (int64_t k = base + threadIdx.x; k < base + kBlockElems && k < n; k += 256) {
+    for (int64_t k = base + threadIdx.x; k < base + kAvgElems && k < n; k += 256) {
       T o = elem(k) * inv;
       out[k] = o;
       if (SUMSQ) acc += sq64(o);
@@ -428,7 +504,11 @@ __global__ void __launch_bounds__(256) bucket_average_kernel(T* __restrict__ out
   }
 }
 
-static int average_grid(int64_t n) { return (int)onepass_grid(n); }
+template <typename T>
+static int average_grid(int64_t n) {
+  const int64_t e = avg_elems<T>(n >= kAvgWideFrom ? 4 : 1);
+  return n > 0 ? (int)((n + e - 1) / e) : 1;
+}
 
 // -------------------------------------------------------- sum of squares
 struct SumsqEntry {
@@ -615,22 +695,17 @@ DTMI_EXPORT int dtmi_bucket_flatten(int dtype, void* dst, const void* const* src
   DTMI_BODY_END
 }
 
-template <typename T, bool ROT>
-static int launch_average_t(void* out, const void* rep, int world, int64_t n, int64_t stride, double inv_w,
-                            double* partials, const RankSegs& sg) {
-  bool vec = aligned(out, 16) && aligned(rep, 16) && ((stride * (int64_t)sizeof(T)) % 16 == 0);
-  int grid = average_grid(n);
-  T inv = (T)inv_w;
-  T* O = (T*)out;
-  const T* R = (const T*)rep;
+template <typename T, bool ROT, int PER>
+static void launch_average_p(int grid, T* O, const T* R, int world, int64_t n, int64_t stride, T inv,
+                             double* partials, const RankSegs& sg, bool vec) {
   if (vec) {
     auto go = [&](auto wc) {
       constexpr int WC = decltype(wc)::value;
       if (partials)
-        bucket_average_kernel<T, true, true, WC, ROT>
+        bucket_average_kernel<T, true, true, WC, ROT, PER>
             <<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials, sg);
       else
-        bucket_average_kernel<T, true, false, WC, ROT>
+        bucket_average_kernel<T, true, false, WC, ROT, PER>
             <<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv, partials, sg);
     };
     switch (world) {
@@ -641,12 +716,26 @@ static int launch_average_t(void* out, const void* rep, int world, int64_t n, in
     }
   } else {
     if (partials)
-      bucket_average_kernel<T, false, true, 0, ROT><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv,
-                                                                                 partials, sg);
+      bucket_average_kernel<T, false, true, 0, ROT, PER><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv,
+                                                                                      partials, sg);
     else
-      bucket_average_kernel<T, false, false, 0, ROT><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv,
-                                                                                  partials, sg);
+      bucket_average_kernel<T, false, false, 0, ROT, PER><<<grid, 256, 0, stream()>>>(O, R, world, n, stride, inv,
+                                                                                       partials, sg);
   }
+}
+
+template <typename T, bool ROT>
+static int launch_average_t(void* out, const void* rep, int world, int64_t n, int64_t stride, double inv_w,
+                            double* partials, const RankSegs& sg) {
+  bool vec = aligned(out, 16) && aligned(rep, 16) && ((stride * (int64_t)sizeof(T)) % 16 == 0);
+  int grid = average_grid<T>(n);
+  T inv = (T)inv_w;
+  T* O = (T*)out;
+  const T* R = (const T*)rep;
+  if (n >= kAvgWideFrom)
+    launch_average_p<T, ROT, 4>(grid, O, R, world, n, stride, inv, partials, sg, vec);
+  else
+    launch_average_p<T, ROT, 1>(grid, O, R, world, n, stride, inv, partials, sg, vec);
   LAUNCH_CHECK("bucket_average_kernel");
   return DTMI_OK;
 }
@@ -658,28 +747,27 @@ static int launch_average(void* out, const void* rep, int world, int64_t n, int6
                           double* partials, const int64_t* seg_start, const int* seg_first, int nseg) {
   TimedLaunch tl(DTMI_FAM_BUCKET_AVG, (double)(world + 1) * (double)n * sizeof(T));
   RankSegs sg{};
+  for (int j = 0; j < kMaxSegs; ++j) sg.start[j] = INT32_MAX;
   bool rot = false;
   for (int s = 0; s < nseg; ++s) rot = rot || seg_first[s] != 0;
   if (!rot || world <= 2) {  // one order for all (for W <= 2 every order gives the same bits)
-    sg.nseg = 1;
-    sg.start[1] = n;
+    sg.start[0] = 0;
     return launch_average_t<T, false>(out, rep, world, n, stride, inv_w, partials, sg);
   }
   int s0 = 0;
-  int64_t done_blocks = 0;
   while (s0 < nseg) {
     const int cnt = nseg - s0 < kMaxSegs ? nseg - s0 : kMaxSegs;
     const int64_t lo = seg_start[s0], hi = s0 + cnt < nseg ? seg_start[s0 + cnt] : n;
-    sg.nseg = cnt;
+    DTMI_CHECK(hi - lo < INT32_MAX, "dtmi_bucket_average_ring: a run of %d segments spans %lld elements (< 2^31)",
+               cnt, (long long)(hi - lo));
+    for (int j = 0; j < kMaxSegs; ++j) sg.start[j] = INT32_MAX;
+    for (int j = 0; j < kMaxSegs / 4; ++j) sg.first4[j] = 0;
     for (int j = 0; j < cnt; ++j) {
-      sg.start[j] = seg_start[s0 + j] - lo;
-      sg.first[j] = seg_first[s0 + j];
+      sg.start[j] = (int32_t)(seg_start[s0 + j] - lo);
+      sg.first4[j >> 2] |= (uint32_t)seg_first[s0 + j] << (8 * (j & 3));
     }
-    sg.start[cnt] = hi - lo;
-    int rc = launch_average_t<T, true>((T*)out + lo, (const T*)rep + lo, world, hi - lo, stride, inv_w,
-                                       partials ? partials + done_blocks : nullptr, sg);
+    int rc = launch_average_t<T, true>((T*)out + lo, (const T*)rep + lo, world, hi - lo, stride, inv_w, partials, sg);
     if (rc) return rc;
-    done_blocks += average_grid(hi - lo);
     s0 += cnt;
   }
   return DTMI_OK;
@@ -700,7 +788,7 @@ DTMI_EXPORT int dtmi_bucket_average(int dtype, void* out, const void* replicas, 
   DTMI_REQUIRE_INIT();
   DTMI_DTYPE_OK(dtype);
   DTMI_CHECK(n >= 0, "dtmi_bucket_average: negative size");
-  if (nblocks) *nblocks = n > 0 ? average_grid(n) : 0;
+  if (nblocks) *nblocks = n > 0 ? (dtype == DTMI_F32 ? average_grid<float>(n) : average_grid<double>(n)) : 0;
   if (sumsq_partials == nullptr && nblocks != nullptr && out == nullptr) return DTMI_OK;  // size query
   if (n == 0) return DTMI_OK;
   int rc = check_average(world, n, out, replicas, replica_stride, "dtmi_bucket_average");
@@ -726,8 +814,8 @@ DTMI_EXPORT int dtmi_bucket_average_ring(int dtype, void* out, const void* repli
   DTMI_CHECK(nseg >= 1 && seg_start && seg_first, "dtmi_bucket_average_ring: need at least one segment");
   DTMI_CHECK(seg_start[0] == 0, "dtmi_bucket_average_ring: the first segment must start at 0");
   for (int s = 0; s < nseg; ++s) {
-    DTMI_CHECK(seg_first[s] >= 0 && seg_first[s] < world, "dtmi_bucket_average_ring: segment %d starts at rank %d",
-               s, seg_first[s]);
+    DTMI_CHECK(seg_first[s] >= 0 && seg_first[s] < world && seg_first[s] < 256,
+               "dtmi_bucket_average_ring: segment %d starts at rank %d", s, seg_first[s]);
     DTMI_CHECK((s + 1 < nseg ? seg_start[s + 1] : n) > seg_start[s],
                "dtmi_bucket_average_ring: segment starts must increase inside [0, n)");
   }

@@ -74,7 +74,7 @@ def _broadcast_to(g: DeviceArray, shape) -> DeviceArray:
 
 class Tensor:
     __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "_hooks", "name", "grad_dest",
-                 "_dest_live", "__weakref__")
+                 "_dest_live", "_ln_pre", "__weakref__")
 
     def __init__(self, data, requires_grad=False, _parents=(), _backward=None, name=None):
         self.data = data if isinstance(data, DeviceArray) else dev.asarray(np.asarray(data))
@@ -89,6 +89,9 @@ class Tensor:
         # the gradient writes straight into it, so the bucket needs no copy.
         self.grad_dest = None
         self._dest_live = None
+        # A LayerNorm of this tensor computed by the kernel that produced it
+        # (w, b, eps, y, mean, rstd); layer_norm(self, w, b, eps) takes it once.
+        self._ln_pre = None
 
     # ------------------------------------------------------------ utilities
     @property
@@ -354,9 +357,15 @@ def embedding(weight: Tensor, idx) -> Tensor:
 
 
 def layer_norm(x: Tensor, w: Tensor, b: Tensor, eps=1e-5) -> Tensor:
-    """dtrain/autograd.py:207-223."""
+    """dtrain/autograd.py:207-223. When the kernel that produced x already
+    computed this LayerNorm of it (nn.linear(..., ln=...)), its result is used
+    (the same bits)."""
     xd = _contig(x.data)
-    y, mean, rstd = K.layernorm_fwd(xd, _contig(w.data), _contig(b.data), eps)
+    pre, x._ln_pre = x._ln_pre, None
+    if pre is not None and pre[0] is w and pre[1] is b and pre[2] == eps:
+        y, mean, rstd = pre[3:]
+    else:
+        y, mean, rstd = K.layernorm_fwd(xd, _contig(w.data), _contig(b.data), eps)
 
     def bw(g, dx_addend=None):
         return K.layernorm_bwd(_contig(g), xd, _contig(w.data), mean, rstd, dw_out=grad_out(w), db_out=grad_out(b),

@@ -214,9 +214,10 @@ def bucket_flatten(dst: DeviceArray, srcs, counts):
        _lib.ptr_array([s.ptr if s is not None else 0 for s in srcs]), _lib.i64_array(counts), len(counts))
 
 
-def average_blocks(n: int) -> int:
+def average_blocks(n: int, dtype=np.float32) -> int:
+    """Blocks (sum-of-squares partials) of a bucket average over n elements."""
     nb = C.c_int64()
-    _c("dtmi_bucket_average", 0, None, None, 1, int(n), int(n), 1.0, None, C.byref(nb))
+    _c("dtmi_bucket_average", _lib.dtype_code(dtype), None, None, 1, int(n), int(n), 1.0, None, C.byref(nb))
     return nb.value
 
 
@@ -233,7 +234,7 @@ def bucket_average(out: DeviceArray, replicas: DeviceArray, world: int, inv_w: f
     if replicas.shape[1] > 1 and replicas.strides[1] != 1:
         raise ValueError("bucket_average: replica rows must be contiguous")
     stride = replicas.strides[0] if world > 1 else replicas.shape[1]
-    if partials is not None and (partials.dtype != np.float64 or partials.size < average_blocks(out.size)):
+    if partials is not None and (partials.dtype != np.float64 or partials.size < average_blocks(out.size, out.dtype)):
         raise ValueError("bucket_average: partials too small")
     if segments is None:
         _c("dtmi_bucket_average", _dt(out, replicas), out.ptr, replicas.ptr, int(world), out.size, int(stride),
@@ -484,6 +485,31 @@ def linear_fwd_fused(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None, res
     _c("dtmi_linear_fwd_fused", _dt(x2, w), y.ptr, act.ptr if act is not None else None, x2.ptr, w.ptr,
        b.ptr if b is not None else None, residual.ptr if residual is not None else None, M, K, N)
     return y, act
+
+
+def linear_fwd_ln(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None, residual: DeviceArray | None,
+                  ln_w: DeviceArray, ln_b: DeviceArray, eps: float = 1e-5):
+    """y = residual + (x @ w + b), then h = layer_norm(y; ln_w, ln_b). Returns
+    (y, h, mean, rstd); the same bits as linear_fwd_fused then layernorm_fwd."""
+    _contig(x2, w, ln_w, ln_b)
+    M, K = x2.shape
+    K2, N = w.shape
+    if K != K2:
+        raise ValueError("linear: shape mismatch")
+    if residual is not None:
+        _contig(residual)
+        if residual.shape != (M, N) or residual.dtype != x2.dtype:
+            raise ValueError("linear: residual must match the output")
+    if ln_w.shape != (N,) or ln_b.shape != (N,):
+        raise ValueError("linear_fwd_ln: LayerNorm parameters must be [N]")
+    y = empty((M, N), x2.dtype)
+    h = empty((M, N), x2.dtype)
+    mean = empty((M,), x2.dtype)
+    rstd = empty((M,), x2.dtype)
+    _c("dtmi_linear_fwd_ln", _dt(x2, w, ln_w, ln_b), y.ptr, h.ptr, mean.ptr, rstd.ptr, x2.ptr, w.ptr,
+       b.ptr if b is not None else None, residual.ptr if residual is not None else None, ln_w.ptr, ln_b.ptr,
+       float(eps), M, K, N)
+    return y, h, mean, rstd
 
 
 def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, need_db=True,

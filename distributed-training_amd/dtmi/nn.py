@@ -76,17 +76,31 @@ def param(arr, name=None):
     return Tensor(arr, requires_grad=True, name=name)
 
 
-def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = None) -> Tensor:
+def _with_ln(X2, W, b, R2, ln: "LayerNorm | None", lead):
+    """y = residual + (x @ w + b) as [*lead, N]; with `ln`, the kernel also
+    computes ln(y), returned as the (w, b, eps, y, mean, rstd) that
+    layer_norm(y, w, b) takes instead of recomputing it."""
+    N = W.shape[1]
+    if ln is None:
+        out, _ = K.linear_fwd_fused(X2, W, b, residual=R2)
+        return out.reshape(*lead, N), None
+    out, h, mean, rstd = K.linear_fwd_ln(X2, W, b, R2, _contig(ln.w.data), _contig(ln.b.data))
+    return out.reshape(*lead, N), (ln.w, ln.b, 1e-5, h.reshape(*lead, N), mean, rstd)
+
+
+def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = None,
+           ln: "LayerNorm | None" = None) -> Tensor:
     """y = x @ w (+ b) for x [..., K], w [K, N], b [N]: one GEMM, bias fused.
     With `residual` (same shape as y): y = residual + (x @ w + b), the add
-    fused into the same epilogue; its gradient passes straight through."""
+    fused into the same epilogue; its gradient passes straight through. With
+    `ln`, the LayerNorm that reads y next (ln(y)) is computed in the same
+    pass over y's rows."""
     X = _contig(x.data)
     lead = X.shape[:-1]
     X2 = X.reshape(-1, X.shape[-1])
     W = w.data
     R2 = _contig(residual.data).reshape(-1, W.shape[1]) if residual is not None else None
-    y, _ = K.linear_fwd_fused(X2, W, b.data if b is not None else None, residual=R2)
-    y = y.reshape(*lead, W.shape[1])
+    y, pre = _with_ln(X2, W, b.data if b is not None else None, R2, ln, lead)
 
     def bw(g):
         g2 = _contig(g).reshape(-1, W.shape[1])
@@ -99,10 +113,12 @@ def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = Non
             out.append(g)
         return tuple(out)
     parents = [x, w] + ([b] if b is not None else []) + ([residual] if residual is not None else [])
-    return Tensor._make(y, tuple(parents), bw)
+    t = Tensor._make(y, tuple(parents), bw)
+    t._ln_pre = pre
+    return t
 
 
-def mlp(x: Tensor, fc: "Linear", out: "Linear", residual: Tensor) -> Tensor:
+def mlp(x: Tensor, fc: "Linear", out: "Linear", residual: Tensor, ln: "LayerNorm | None" = None) -> Tensor:
     """residual + out(gelu(fc(x))), Block's MLP branch (dtrain/nn.py:105) as two
     GEMMs: the fc GEMM's epilogue adds the bias and also writes gelu of the
     result, the out GEMM's epilogue adds bias and residual; in the backward
@@ -115,8 +131,7 @@ def mlp(x: Tensor, fc: "Linear", out: "Linear", residual: Tensor) -> Tensor:
     bf, bo = fc.b, out.b
     h, act = K.linear_fwd_fused(X2, Wf, bf.data if bf is not None else None, gelu=True)
     R2 = _contig(residual.data).reshape(-1, Wo.shape[1])
-    y, _ = K.linear_fwd_fused(act, Wo, bo.data if bo is not None else None, residual=R2)
-    y = y.reshape(*lead, Wo.shape[1])
+    y, pre = _with_ln(act, Wo, bo.data if bo is not None else None, R2, ln, lead)
 
     def bw(g):
         g2 = _contig(g).reshape(-1, Wo.shape[1])
@@ -133,7 +148,9 @@ def mlp(x: Tensor, fc: "Linear", out: "Linear", residual: Tensor) -> Tensor:
         res.append(g)
         return tuple(res)
     parents = [x, fc.w] + ([bf] if bf is not None else []) + [out.w] + ([bo] if bo is not None else []) + [residual]
-    return Tensor._make(y, tuple(parents), bw)
+    t = Tensor._make(y, tuple(parents), bw)
+    t._ln_pre = pre
+    return t
 
 
 def qkv_attention(qkv: Tensor, heads: int) -> Tensor:
@@ -196,10 +213,14 @@ class Block(Module):
         self.fc = Linear(c.dim, 4 * c.dim, rng, dt)
         self.out = Linear(4 * c.dim, c.dim, rng, dt, std=0.02 / np.sqrt(2 * c.layers))
 
-    def forward(self, x):
+    def forward(self, x, next_ln: "LayerNorm | None" = None):
+        """dtrain/nn.py:98-105. `next_ln` is the LayerNorm that reads this
+        block's output (the next block's ln1, or the model's final ln): the
+        output GEMM computes it in the same pass over the rows, as the proj
+        GEMM does for ln2."""
         a = qkv_attention(self.qkv(self.ln1(x)), self.c.heads)
-        x = linear(a, self.proj.w, self.proj.b, residual=x)  # x + self.proj(a)
-        return mlp(self.ln2(x), self.fc, self.out, residual=x)  # x + self.out(self.fc(self.ln2(x)).gelu())
+        x = linear(a, self.proj.w, self.proj.b, residual=x, ln=self.ln2)  # x + self.proj(a)
+        return mlp(self.ln2(x), self.fc, self.out, residual=x, ln=next_ln)  # x + self.out(self.fc(self.ln2(x)).gelu())
 
 
 class GPT(Module):
@@ -250,8 +271,8 @@ class GPT(Module):
         idx = as_indices(idx)
         B, T = idx.shape
         x = embedding(self.tok, idx) + embedding(self.pos, self._positions(T))
-        for b in self.blocks:
-            x = b(x)
+        for i, b in enumerate(self.blocks):
+            x = b(x, next_ln=self.blocks[i + 1].ln1 if i + 1 < len(self.blocks) else self.ln)
         logits = self.head(self.ln(x))
         if targets is None:
             return logits

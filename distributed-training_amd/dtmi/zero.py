@@ -94,7 +94,7 @@ class ZeroAdamW:
         self._index = self.grads.index
         for p in self.params:
             p.register_grad_ready_hook(self._on_grad)
-        self._nblocks = [K.average_blocks(self.bounds[r + 1] - self.bounds[r]) for r in range(pg.world)]
+        self._nblocks = [K.average_blocks(self.bounds[r + 1] - self.bounds[r], dtype) for r in range(pg.world)]
         self._partials = dev.empty((max(1, max(self._nblocks)),), np.float64)
 
     # dtrain attributes

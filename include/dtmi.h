@@ -138,7 +138,7 @@ int dtmi_bucket_average(int dtype, void* out, const void* replicas, int world, i
  * (shard r summed starting at rank r). The host computes where the chunks of
  * dtrain's bucket buffer (reverse parameter order) fall in this layout.
  * seg_start / seg_first are host arrays of nseg entries. sumsq_partials as
- * for dtmi_bucket_average (one launch, so at most 32 segments with it). */
+ * for dtmi_bucket_average (one launch, so at most 16 segments with it). */
 int dtmi_bucket_average_ring(int dtype, void* out, const void* replicas, int world, int64_t n,
                              int64_t replica_stride, double inv_w, const int64_t* seg_start, const int* seg_first,
                              int nseg, double* sumsq_partials);
@@ -318,6 +318,17 @@ int dtmi_linear_bwd_dw(int dtype, void* dW, void* db, const void* X, const void*
  * The two are not combined in one call. */
 int dtmi_linear_fwd_fused(int dtype, void* Y, void* act, const void* X, const void* W, const void* b,
                           const void* residual, int64_t M, int64_t K, int64_t N);
+/* Y = residual + (X W + b) followed by the next LayerNorm of the block,
+ * H = layer_norm(Y; ln_w, ln_b, eps) with its row mean and rstd [M]: Block's
+ * `x + self.proj(...)` / `x + self.out(...)` (dtrain/nn.py:104-105) and the
+ * ln2 / next block's ln1 / final ln that reads that x (nn.py:101, 105, 136;
+ * autograd.py:207-214). When the product is split over K, the split sum, bias,
+ * residual and LayerNorm run as one row pass (Y is still written: the
+ * residual stream and the LayerNorm backward read it). The same bits as
+ * dtmi_linear_fwd_fused followed by dtmi_layernorm_fwd. residual may be NULL. */
+int dtmi_linear_fwd_ln(int dtype, void* Y, void* H, void* mean, void* rstd, const void* X, const void* W,
+                       const void* b, const void* residual, const void* ln_w, const void* ln_b, double eps, int64_t M,
+                       int64_t K, int64_t N);
 /* dX = gelu'(pre) * (dY W^T): the Linear input gradient followed by the GELU
  * backward of autograd.py:139-143 (pre = the saved pre-activation [M, K]). */
 int dtmi_linear_bwd_dx_gelu(int dtype, void* dX, const void* dY, const void* W, const void* pre, int64_t M, int64_t K,

@@ -500,3 +500,22 @@ def test_ddp_ring_training_steps_match_dtrain_fixture(dev, golden):
         for n, p in m.named_parameters():
             assert rel_err(p.grad.numpy(), S[f"s{s}/g/{n}"]) <= 1e-12, (s, n)
         shadow.check(m, res.clip_scale)
+
+
+@pytest.mark.parametrize("dt", ["float64", "float32"])
+def test_model_with_head_dimension_128_matches_oracle(dev, dt):
+    """dtrain's `--dim 256 --heads 2` (head dimension 128) trains: loss and every
+    gradient against the oracle."""
+    N = _api()[1]
+    c = dict(vocab=19, ctx=16, dim=256, heads=2, layers=1)
+    P = OM.dtrain_init(OM.GPTConfig(dtype=dt, **c), seed=3)
+    x = rng.integers(0, 19, size=(2, 16))
+    y = rng.integers(0, 19, size=(2, 16))
+    loss_ref, G = OM.loss_and_grads(P, OM.GPTConfig(dtype=dt, **c), x, y)
+    m = N.GPT(N.GPTConfig(dtype=dt, **c), seed=3)
+    _, loss = m(x, y)
+    loss.backward()
+    tol = TOL[np.dtype(dt).type]
+    assert rel_err(loss.numpy(), loss_ref) <= tol
+    for name, p in m.named_parameters():
+        assert rel_err(p.grad.numpy(), G[name]) <= tol, name

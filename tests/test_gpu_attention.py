@@ -133,3 +133,14 @@ def test_backward_without_the_ds_workspace_matches_with_it(dev):
     for i, full in enumerate((dq, dk, dv)):
         ref = np.concatenate([halves[0][i], halves[1][i]], axis=1)
         assert rel_err(full.numpy(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("shape", [(2, 2, 64, 128), (1, 3, 100, 80), (2, 1, 33, 256)])
+def test_head_dimensions_beyond_64(dev, dt, shape):
+    """D > 64 (e.g. dtrain's --dim 256 --heads 2): scores materialised per batch
+    element and the products as batched GEMMs; against the oracle."""
+    D, K = _dev()
+    rng = np.random.default_rng(sum(shape) + 1)
+    q, k, v, g = (rng.standard_normal(shape).astype(dt) for _ in range(4))
+    _check(D, K, q, k, v, g, dt)

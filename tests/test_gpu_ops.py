@@ -23,8 +23,11 @@ def _dev():
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
 @pytest.mark.parametrize("shape", [(2, 3, 6), (256, 64), (4096, 768), (5, 1000), (3, 17), (2400, 1000), (5000, 768),
-                                   (33, 2000), (9, 2048)])
+                                   (33, 2000), (9, 2048), (3, 1025), (7, 5000), (130, 2304), (2, 70001), (600, 4097)])
 def test_layernorm_forward_backward(dev, dt, shape):
+    """Rows in registers (up to 16 vectors per lane) and longer rows (a block
+    per row: unaligned rows above 1024, float64 above 2048, float32 above
+    4096 elements)."""
     D, K = _dev()
     rng = np.random.default_rng(sum(shape))
     C = shape[-1]
@@ -46,7 +49,7 @@ def test_layernorm_forward_backward(dev, dt, shape):
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
-@pytest.mark.parametrize("shape", [(4096, 768), (33, 1000), (3, 17)])
+@pytest.mark.parametrize("shape", [(4096, 768), (33, 1000), (3, 17), (9, 5000)])
 def test_layernorm_backward_with_addend_bits(dev, dt, shape):
     """dtmi_layernorm_bwd_add: dx = addend + the input gradient in the same
     pass, bit for bit the separate sum addend + dx (the backward engine's
@@ -337,3 +340,31 @@ def test_fused_linear_epilogues_equal_the_unfused_ops(dev, dt, M, K, N):
     assert bits_equal(dx_fused.numpy(), K_.gelu_bwd(pre, dx_plain).numpy())
     ref = (x.numpy().astype(np.float64) @ w.numpy().astype(np.float64)) + b.numpy() + r.numpy()
     assert rel_err(y_res.numpy(), ref) <= TOL[dt]
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("M,K,N,resid", [(8192, 768, 768, True), (8192, 3072, 768, True), (512, 3072, 768, False),
+                                         (300, 64, 2304, True), (96, 200, 130, True)])
+def test_linear_with_the_next_layernorm_equals_the_separate_ops(dev, dt, M, K, N, resid):
+    """dtmi_linear_fwd_ln: y = residual + (x @ w + b) and h = layer_norm(y) in
+    one call (split-K sum, bias, residual and LayerNorm in one row pass when
+    the product is split over K) -- bit for bit the separate fused Linear and
+    LayerNorm kernels, on split and unsplit shapes, ragged rows and float64."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(M + K + N)
+    x = D.from_numpy(rng.standard_normal((M, K)).astype(dt))
+    w = D.from_numpy((rng.standard_normal((K, N)) * 0.02).astype(dt))
+    b = D.from_numpy((rng.standard_normal(N) * 0.1).astype(dt))
+    r = D.from_numpy(rng.standard_normal((M, N)).astype(dt)) if resid else None
+    lw = D.from_numpy((1 + 0.1 * rng.standard_normal(N)).astype(dt))
+    lb = D.from_numpy((0.1 * rng.standard_normal(N)).astype(dt))
+    y, h, mean, rstd = K_.linear_fwd_ln(x, w, b, r, lw, lb)
+    y2, _ = K_.linear_fwd_fused(x, w, b, residual=r)
+    h2, mean2, rstd2 = K_.layernorm_fwd(y2, lw, lb)
+    for a, ref in ((y, y2), (h, h2), (mean, mean2), (rstd, rstd2)):
+        assert bits_equal(a.numpy(), ref.numpy())
+    # and the values: the oracle's Linear + residual and LayerNorm
+    ref_y = x.numpy() @ w.numpy() + b.numpy() + (r.numpy() if resid else 0)
+    assert rel_err(y.numpy(), ref_y) <= (1e-5 if dt == np.float32 else 1e-12)
+    ref_h, _ = ops.layer_norm_fwd(ref_y, lw.numpy(), lb.numpy())
+    assert rel_err(h.numpy(), ref_h) <= (1e-4 if dt == np.float32 else 1e-10)

@@ -117,7 +117,7 @@ def test_bucket_average_fixed_order_bit_exact(dev, dt, world, n):
     rng = np.random.default_rng(world * 7 + n)
     reps = (rng.standard_normal((world, n)) * 1e-3).astype(dt)
     out = D.empty((n,), dt)
-    nb = K.average_blocks(n)
+    nb = K.average_blocks(n, dt)
     parts = D.empty((nb,), np.float64)
     K.bucket_average(out, D.from_numpy(reps), world, 1.0 / world, partials=parts)
     ref = fixed_order_sum(list(reps))
@@ -205,7 +205,7 @@ def test_bucket_average_and_adamw_at_124m_params(dev, dt):
     p_sh, m_sh, v_sh = p[:sh].copy(), m[:sh].copy(), v[:sh].copy()
     dp, dm, dv = D.from_numpy(p), D.from_numpy(m), D.from_numpy(v)
     dg = D.empty((n,), dt)
-    nb = K.average_blocks(n)
+    nb = K.average_blocks(n, dt)
     parts = D.empty((nb,), np.float64)
     drep = D.from_numpy(reps)
     K.bucket_average(dg, drep, W, 0.25, partials=parts)
@@ -264,15 +264,16 @@ def _ring_ref(reps, segs, dt):
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
 @pytest.mark.parametrize("world", [3, 4, 5])
-@pytest.mark.parametrize("case", ["one_rotated", "block_edges", "inside_blocks", "many"])
+@pytest.mark.parametrize("case", ["one_rotated", "block_edges", "inside_blocks", "many", "large"])
 def test_bucket_average_ring_order_bit_exact(dev, dt, world, case):
     """Segments with their own starting rank (dtrain's ring order): whole
-    buffer rotated, edges on and inside 1024-element blocks, more than 32
-    segments (several launches), against a NumPy rank-order sum per segment;
-    gradients over 16 decades so that any other order changes bits."""
+    buffer rotated, edges on and inside blocks, more than 16 segments
+    (several launches), a 5M-element buffer (blocks of four vectors per
+    thread), against a NumPy rank-order sum per segment; gradients over 16
+    decades so that any other order changes bits."""
     D, K = _dev()
     rng = np.random.default_rng(world + len(case))
-    n = 70_001
+    n = 5_000_003 if case == "large" else 70_001
     reps = (rng.standard_normal((world, n)) * 10.0 ** rng.uniform(-8, 8, (world, n))).astype(dt)
     if case == "one_rotated":
         segs = [(0, world - 1)]
@@ -280,6 +281,8 @@ def test_bucket_average_ring_order_bit_exact(dev, dt, world, case):
         segs = [(0, 1), (1024, 2), (4096, 0), (40960, world - 1)]
     elif case == "inside_blocks":
         segs = [(0, 2), (5, 1), (1030, 0), (1031, world - 1), (33333, 1), (70_000, 2)]
+    elif case == "large":
+        segs = [(0, 1), (2048, 0), (4100, 2), (1_666_667, world - 1), (3_333_334, 1), (4_999_999, 0)]
     else:
         cuts = np.sort(rng.choice(np.arange(1, n), 70, replace=False))
         segs = [(0, 1)] + [(int(c), int(rng.integers(0, world))) for c in cuts]
@@ -288,8 +291,8 @@ def test_bucket_average_ring_order_bit_exact(dev, dt, world, case):
     ref = _ring_ref(reps, segs, dt)
     assert bits_equal(out.numpy(), ref)
     assert not bits_equal(ref, fixed_order_sum(list(reps)) * dt(1.0 / world))
-    if len(segs) <= 32:  # with sum-of-squares partials (one launch)
-        nb = K.average_blocks(n)
+    if len(segs) <= 16:  # with sum-of-squares partials (one launch)
+        nb = K.average_blocks(n, dt)
         parts = D.empty((nb,), np.float64)
         out2 = D.empty((n,), dt)
         K.bucket_average(out2, D.from_numpy(reps), world, 1.0 / world, partials=parts, segments=segs)
