@@ -33,6 +33,7 @@
 // them with 16-byte vectors. Results are deterministic.
 #include <cmath>
 
+#include "bufrsrc.h"
 #include "common.h"
 
 namespace dtmi {
@@ -194,25 +195,6 @@ __device__ __forceinline__ void mma_lds_t_regs(typename AM<T>::acc_t (&out)[DP /
 // about 1 ulp, which it gives); the accurate library exp2 for double.
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ double ex2(double x) { return exp2(x); }
-
-// Raw buffer accesses: a wave-uniform resource (base address and byte range),
-// a per-lane byte offset that stays fixed over a loop and a wave-uniform byte
-// offset, so addressing takes no vector instructions (accesses beyond the
-// range read 0 and write nothing).
-typedef __amdgpu_buffer_rsrc_t Rsrc;
-__device__ __forceinline__ Rsrc make_rsrc(const void* base, uint64_t bytes) {
-  const uint32_t n = bytes < 0xFFFFFFFFull ? (uint32_t)bytes : 0xFFFFFFFFu;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
-}
-__device__ __forceinline__ AM<float>::vec_t buf_load4(Rsrc r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(AM<float>::vec_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
-}
-__device__ __forceinline__ float buf_load1(Rsrc r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0));
-}
-__device__ __forceinline__ void buf_store1(float x, Rsrc r, uint32_t voff, uint32_t soff) {
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(int, x), r, (int)voff, (int)soff, 0);
-}
 
 // Column swizzle of the transposed LDS tiles: XOR of bits 2-3 of the column
 // with bits 4-5 of the row, so groups of 4 columns stay 16-byte aligned and a

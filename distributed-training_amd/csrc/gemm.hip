@@ -43,6 +43,7 @@
 // Small tile counts with long K are split along K; the split partials are
 // summed in split order by a second kernel (deterministic, no atomics).
 #include "common.h"
+#include "bufrsrc.h"
 #include "gelu.h"
 #include "rowln.h"
 
@@ -334,7 +335,7 @@ __device__ __forceinline__ void finish_colsum(const GemmArgs& a, double csum, in
 // A wave's TM x TN MFMA accumulators (its tile starts at row m0, column n0):
 // split-K partials go to the workspace as they are; otherwise the fused
 // epilogue writes C (and aux).
-template <typename T, int TM, int TN>
+template <typename T, int TM, int TN, bool FAST_EPI = false>
 __device__ __forceinline__ void write_acc(const GemmArgs& a, const typename MF<T>::acc_t (&acc)[TM][TN], int64_t m0,
                                           int64_t n0, int g, int c, int split, int64_t batch) {
   using MFT = MF<T>;
@@ -362,6 +363,42 @@ __device__ __forceinline__ void write_acc(const GemmArgs& a, const typename MF<T
         }
       }
   } else {
+    if constexpr (FAST_EPI && std::is_same<T, float>::value) {
+      if (a.epi == kEpiGeluBwd && a.addend == nullptr && !a.accumulate && m0 + TM * MT <= a.M &&
+          n0 + TN * MT <= a.N) {
+        // GELU backward over a whole wave tile in range: the pre-activation
+        // is read for a row of MFMA tiles before its first store -- the
+        // stores may alias it as far as the compiler can tell, so element by
+        // element each read would wait a full memory round trip. Buffer
+        // accesses off the wave tile's corner: one lane offset, and per
+        // element a wave-uniform one. Same operations as epilogue_store.
+        const Rsrc rs = make_rsrc((const float*)a.aux + batch * a.sC + m0 * ldc + n0, ~0ull);
+        const Rsrc rc = make_rsrc(C + m0 * ldc + n0, ~0ull);
+        const uint32_t voff = (uint32_t)((4 * g * ldc + c) * 4);
+        const float* bias = (const float*)a.bias;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          float x[TN][NACC];
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < NACC; ++r)
+              x[j][r] = buf_load1(rs, voff, (uint32_t)(((i * MT + MFT::row(r, 0)) * ldc + j * MT) * 4));
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const float bn = bias ? bias[n0 + j * MT + c] : 0.f;
+#pragma unroll
+            for (int r = 0; r < NACC; ++r) {
+              float v = acc[i][j][r];
+              if (bias) v = v + bn;
+              buf_store1(gelu_b<float>(x[j][r], v), rc, voff,
+                         (uint32_t)(((i * MT + MFT::row(r, 0)) * ldc + j * MT) * 4));
+            }
+          }
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -756,7 +793,7 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
     compute(st);
   }
   if (take_colsum) finish_colsum<float>(a, csum, n0 + threadIdx.x, split);
-  write_acc<float, TM, TN>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
+  write_acc<float, TM, TN, true>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
 }
 
 // ---------------------------------------------------------------------------
@@ -1058,7 +1095,7 @@ __global__ void __launch_bounds__(256, 3) gemm_x6_kernel(GemmArgs a) {
       }
     }
   }
-  write_acc<float, TM, TN>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
+  write_acc<float, TM, TN, true>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
 }
 
 // Sum of the split-K partials in split order 0, 1, ..., S-1, then the

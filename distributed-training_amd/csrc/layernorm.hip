@@ -82,7 +82,10 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
   // is used instead (a second row set would spill). The arithmetic per row is
   // the same.
   constexpr bool PF = NV <= 8;
-  T gn[NV][VW], xn[NV][VW];
+  // what dx adds to: the existing dx, or the addend (a row's own rows only,
+  // so the next row's are read ahead of this row's store)
+  const T* base = accumulate_dx ? dx : addend;
+  T gn[NV][VW], xn[NV][VW], an[NV][VW];
   T mun = T(0), rsn = T(0);
   int64_t row = (int64_t)blockIdx.x * 4 + wave;
   auto load_row = [&](int64_t r) {
@@ -94,13 +97,14 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
       if (c < cols) {
         load_vec<T, VW>(gn[j], dy + r * cols + c);
         load_vec<T, VW>(xn[j], x + r * cols + c);
+        if (base) load_vec<T, VW>(an[j], base + r * cols + c);
       }
     }
   };
   if (PF && row < rows) load_row(row);
   for (; row < rows; row += wstride) {
     T mu, rs;
-    T gv[NV][VW], xh[NV][VW];
+    T gv[NV][VW], xh[NV][VW], av[NV][VW];
     if constexpr (PF) {
       mu = mun;
       rs = rsn;
@@ -110,6 +114,7 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
         for (int e = 0; e < VW; ++e) {
           gv[j][e] = gn[j][e];
           xh[j][e] = xn[j][e];
+          av[j][e] = an[j][e];
         }
       if (row + wstride < rows) load_row(row + wstride);
     } else {
@@ -145,9 +150,13 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
         // dx (+)= r: onto the existing dx, or a separate addend written to dx
         // (pending + r: the order of the backward engine's sum)
         T o[VW];
-        if (accumulate_dx) load_vec<T, VW>(o, dx + row * cols + c);
-        else if (addend) load_vec<T, VW>(o, addend + row * cols + c);
-        const bool add = accumulate_dx || addend;
+        const bool add = base != nullptr;
+        if constexpr (PF) {
+#pragma unroll
+          for (int e = 0; e < VW; ++e) o[e] = av[j][e];
+        } else {
+          if (add) load_vec<T, VW>(o, base + row * cols + c);
+        }
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
           T gxh = gv[j][e] * wv[j][e];
