@@ -343,6 +343,58 @@ __device__ __forceinline__ void write_acc(const GemmArgs& a, const typename MF<T
   const bool to_ws = a.ws != nullptr;
   T* C = to_ws ? (T*)a.ws + ((int64_t)split * gridDim.z + batch) * a.M * a.N : (T*)a.C + batch * a.sC;
   const int64_t ldc = to_ws ? a.N : a.ldc;
+  if constexpr (FAST_EPI && std::is_same<T, float>::value) {
+    if ((to_ws || (a.addend == nullptr && !a.accumulate)) && m0 + TM * MT <= a.M && n0 + TN * MT <= a.N) {
+      // A whole wave tile in range with no residual or accumulation (every
+      // split-K partial, the bias-only products, the GELU epilogues): buffer
+      // accesses off the wave tile's corner -- one lane offset, and per
+      // element a wave-uniform offset, so no per-element address arithmetic
+      // on the SIMD the MFMAs share. The GELU backward's pre-activation of a
+      // row of MFMA tiles is read before its first store (the stores may
+      // alias it as far as the compiler can tell). Same operations as
+      // epilogue_store.
+      const int64_t corner = m0 * ldc + n0;
+      const float* bias = to_ws ? nullptr : (const float*)a.bias;
+      const Rsrc rc = make_rsrc(C + corner, ~0ull);
+      const Rsrc rx = make_rsrc(to_ws ? C : (const float*)a.aux + batch * a.sC + corner, ~0ull);
+      const uint32_t voff = (uint32_t)((4 * g * ldc + c) * 4);
+      auto run = [&](auto modec) {
+        constexpr int MODE = decltype(modec)::value;  // an epilogue kind
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          float x[TN][NACC];
+          if constexpr (MODE == kEpiGeluBwd) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+#pragma unroll
+              for (int r = 0; r < NACC; ++r)
+                x[j][r] = buf_load1(rx, voff, (uint32_t)(((i * MT + MFT::row(r, 0)) * ldc + j * MT) * 4));
+          }
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            const float bn = bias ? bias[n0 + j * MT + c] : 0.f;
+#pragma unroll
+            for (int r = 0; r < NACC; ++r) {
+              const uint32_t so = (uint32_t)(((i * MT + MFT::row(r, 0)) * ldc + j * MT) * 4);
+              float v = acc[i][j][r];
+              if (bias) v = v + bn;
+              if constexpr (MODE == kEpiGeluFwd) buf_store1(gelu_f<float>(v), rx, voff, so);
+              if constexpr (MODE == kEpiGeluBwd) v = gelu_b<float>(x[j][r], v);
+              buf_store1(v, rc, voff, so);
+            }
+          }
+        }
+      };
+      const int epi = to_ws ? kEpiNone : a.epi;
+      if (epi == kEpiGeluBwd)
+        run(std::integral_constant<int, kEpiGeluBwd>());
+      else if (epi == kEpiGeluFwd)
+        run(std::integral_constant<int, kEpiGeluFwd>());
+      else
+        run(std::integral_constant<int, kEpiNone>());
+      return;
+    }
+  }
   const bool plain = to_ws || (a.addend == nullptr && a.epi == kEpiNone && !a.accumulate);
   if (plain) {  // raw split-K partial, or v + bias
     const T* bias = to_ws ? nullptr : (const T*)a.bias;
@@ -363,42 +415,6 @@ __device__ __forceinline__ void write_acc(const GemmArgs& a, const typename MF<T
         }
       }
   } else {
-    if constexpr (FAST_EPI && std::is_same<T, float>::value) {
-      if (a.epi == kEpiGeluBwd && a.addend == nullptr && !a.accumulate && m0 + TM * MT <= a.M &&
-          n0 + TN * MT <= a.N) {
-        // GELU backward over a whole wave tile in range: the pre-activation
-        // is read for a row of MFMA tiles before its first store -- the
-        // stores may alias it as far as the compiler can tell, so element by
-        // element each read would wait a full memory round trip. Buffer
-        // accesses off the wave tile's corner: one lane offset, and per
-        // element a wave-uniform one. Same operations as epilogue_store.
-        const Rsrc rs = make_rsrc((const float*)a.aux + batch * a.sC + m0 * ldc + n0, ~0ull);
-        const Rsrc rc = make_rsrc(C + m0 * ldc + n0, ~0ull);
-        const uint32_t voff = (uint32_t)((4 * g * ldc + c) * 4);
-        const float* bias = (const float*)a.bias;
-#pragma unroll
-        for (int i = 0; i < TM; ++i) {
-          float x[TN][NACC];
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-#pragma unroll
-            for (int r = 0; r < NACC; ++r)
-              x[j][r] = buf_load1(rs, voff, (uint32_t)(((i * MT + MFT::row(r, 0)) * ldc + j * MT) * 4));
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            const float bn = bias ? bias[n0 + j * MT + c] : 0.f;
-#pragma unroll
-            for (int r = 0; r < NACC; ++r) {
-              float v = acc[i][j][r];
-              if (bias) v = v + bn;
-              buf_store1(gelu_b<float>(x[j][r], v), rc, voff,
-                         (uint32_t)(((i * MT + MFT::row(r, 0)) * ldc + j * MT) * 4));
-            }
-          }
-        }
-        return;
-      }
-    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
