@@ -9,8 +9,9 @@ dtrain/ddp.py on one GPU. Same constructor, attributes and step protocol:
   (ddp.py:46-56);
 * a grad-ready hook on every parameter hands its gradient to the bucket; when
   all of a bucket's gradients of the last replica are in, the fixed-order
-  average of the bucket is launched right away (`overlap=True`) or at
-  `finish()` (`overlap=False`);
+  average of the bucket is launched right away (`overlap=True`; a run of
+  adjacent buckets that complete one after another shares one launch, up to
+  MERGE_BYTES) or at `finish()` (`overlap=False`);
 * `no_sync()` skips all of this for gradient-accumulation micro-steps;
 * `finish()` zero-fills missing gradients (ddp.py:88-94), reduces what is left,
   and points every `param.grad` at its slice of the averaged gradients
@@ -109,6 +110,7 @@ class DDP:
         for p in self.params:
             p.register_grad_ready_hook(self._on_grad)
         self._sync = True
+        self._pend = []
         self.comm_wait_s = 0.0
         self.grad_sq = None
 
@@ -128,12 +130,45 @@ class DDP:
         b.ready[r].clear()
         b.flushed[r] = True
 
+    # Buckets that complete one after another are adjacent column ranges
+    # (reverse parameter order), so a run of them is averaged by one launch
+    # once it holds MERGE_BYTES of gradients, or at finish(): the average is
+    # elementwise with each element's own rank order, so the grouping changes
+    # no value, and a 1 MiB bucket alone is too short a launch to reach the
+    # memory bandwidth. MAX_SEGS: the rank-order segments one launch takes.
+    MERGE_BYTES = 32 << 20
+    MAX_SEGS = 16
+
     def _reduce(self, b: _Bucket):
         if b.reduced or b.n == 0:
             b.reduced = True
             return
-        self.pg.average(b.out, b.rows, segments=b.segments)
+        p = self._pend
+        if p:
+            lo, hi = min(x.lo for x in p), max(x.hi for x in p)
+            nseg = sum(len(x.segments or ((0, 0),)) for x in p) + len(b.segments or ((0, 0),))
+            if not (b.hi == lo or b.lo == hi) or nseg > self.MAX_SEGS:
+                self._flush()
+        self._pend.append(b)
         b.reduced = True
+        if sum(x.n for x in self._pend) * self.avg.itemsize >= self.MERGE_BYTES:
+            self._flush()
+
+    def _flush(self):
+        """Average the pending run of adjacent buckets in one launch."""
+        p = sorted(self._pend, key=lambda x: x.lo)
+        self._pend = []
+        if not p:
+            return
+        lo, hi = p[0].lo, p[-1].hi
+        segs = None
+        if any(x.segments for x in p):
+            segs = []
+            for x in p:
+                for st, first in x.segments or ((0, 0),):
+                    if not segs or segs[-1][1] != first:
+                        segs.append((x.lo - lo + st, first))
+        self.pg.average(self.avg[lo:hi], self.grads.columns(lo, hi), segments=segs)
 
     def _on_grad(self, p):
         if not self._sync:
@@ -158,6 +193,7 @@ class DDP:
                 if not b.flushed[r]:
                     self._complete(b, r)
             self._reduce(b)
+        self._flush()
         self.grad_sq = dev.empty((1,), np.float64)
         K.sumsq([self.avg[:self.grads.n]], self.grad_sq)
         for p, o in zip(self.params, self.grads.offsets):
