@@ -453,7 +453,8 @@ def micro_attention(a):
     return _line("causal attention backward throughput (5 GEMMs, causal-exact FLOP) at B16 H12 T256 D64",
                  round(ach / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"causal self-attention backward B=16 H=12 T=256 D=64 {a.dtype}"},
-                 {"bound": "mfma", "kernel": "attn_bwd_kv_kernel + attn_bwd_q_kernel", "achieved": round(ach / 1e12, 2),
+                 {"bound": "mfma", "kernel": ("attn_drow64 + attn_bwd_kv1 + attn_bwd_q1 (aligned float32), attn_drow + attn_bwd_kv + "
+                             "attn_bwd_q_ds otherwise"), "achieved": round(ach / 1e12, 2),
                   "peak": _mfma_peak(a.dtype) / 1e12, "unit": "TFLOP/s",
                   "frac": round(ach / _mfma_peak(a.dtype), 4), "traffic": None}, cpu)
 
@@ -559,18 +560,41 @@ def micro_chargpt(a):
 
 def micro_copy(a):
     """A plain 256 MiB device-to-device copy through the flatten kernel (reads
-    256 MiB, writes 256 MiB): the calibration point for HBM byte counters."""
-    from dtmi import device as D, kernels as K
+    256 MiB, writes 256 MiB): the calibration point for HBM byte counters.
+    Beside it, what other streams of the same size sustain (wall clock over
+    `steps` calls, GB/s of algorithmic bytes): the elementwise scale (one read,
+    one write), the runtime's own device-to-device copy, and AdamW (four reads,
+    three writes) -- the measured ceilings the bandwidth kernels are held to."""
+    from dtmi import _lib, device as D, kernels as K
     n = (256 << 20) // 4
     src = D.full((n,), 1.0, np.float32)
     dst = D.empty((n,), np.float32)
     dtm, fams = _timed(a, lambda: K.bucket_flatten(dst, [src], [n]), ["flatten"])
     cnt, ms, work = fams["flatten"]
     ach = work / (ms * 1e-3)
+
+    def wall(fn, nbytes):
+        for _ in range(max(a.warmup, 1)):
+            fn()
+        _lib.sync()
+        t0 = time.perf_counter()
+        for _ in range(a.steps):
+            fn()
+        _lib.sync()
+        return round(nbytes * a.steps / (time.perf_counter() - t0) / 1e9, 1)
+
+    from dtmi import optim as O
+    g = D.full((n,), 0.5, np.float32)
+    opt = O.AdamW([dst], lr=1e-4)
+    streams = {"flatten_kernel (1 read, 1 write)": wall(lambda: K.bucket_flatten(dst, [src], [n]), 8 * n),
+               "scale_kernel (1 read, 1 write)": wall(lambda: K.scale(src, 1.0, out=dst), 8 * n),
+               "hipMemcpyAsync device to device": wall(lambda: K.copy_into(dst, src), 8 * n),
+               "adamw_flat_kernel (4 reads, 3 writes)": wall(lambda: opt.step([g]), 28 * n)}
     return _line("device copy bandwidth (256 MiB read + 256 MiB write)", round(ach / 1e9, 1), "GB/s", a,
                  1e3 * dtm / a.steps, {"workload": "flatten_kernel copy of 67,108,864 float32"},
                  {"bound": "hbm", "kernel": "flatten_kernel", "achieved": round(ach / 1e9, 1), "peak": 8000.0,
-                  "unit": "GB/s", "frac": round(ach / 8e12, 4), "traffic": None}, None)
+                  "unit": "GB/s", "frac": round(ach / 8e12, 4), "traffic": None}, None,
+                 {"streams_GB/s": streams})
 
 
 MICRO = {"ln_linear": micro_ln_linear, "attention": micro_attention, "bucket_adamw": micro_bucket_adamw,
