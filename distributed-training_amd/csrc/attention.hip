@@ -126,18 +126,29 @@ template <typename T, int DP>
 __device__ __forceinline__ void load_frag_rows(typename AM<T>::vec_t (&f)[DP / 8], const T* __restrict__ base,
                                                int64_t rs, int64_t r, int64_t Tn, int64_t D, int g, bool vec) {
   constexpr int VEC = AM<T>::VEC;
+  typedef typename AM<T>::vec_t VT;
+  if (vec) {
+    // every vector load is issued before the first is used: a row past T or
+    // a chunk past D reads a valid address and is zeroed afterwards (a load
+    // behind a per-lane branch would wait for the one before it)
+    const bool in = r < Tn;
+    const T* row = base + (in ? r : 0) * rs;
+#pragma unroll
+    for (int ch = 0; ch < DP / 8; ++ch) {
+      const int d = 8 * ch + VEC * g;
+      const VT x = *reinterpret_cast<const VT*>(row + (d < D ? d : 0));
+      f[ch] = in && d < D ? x : VT(0);
+    }
+    return;
+  }
 #pragma unroll
   for (int ch = 0; ch < DP / 8; ++ch) {
     const int d = 8 * ch + VEC * g;
-    typename AM<T>::vec_t x = typename AM<T>::vec_t(0);
+    VT x = VT(0);
     if (r < Tn) {
-      if (vec) {
-        if (d < D) x = *reinterpret_cast<const typename AM<T>::vec_t*>(base + r * rs + d);
-      } else {
 #pragma unroll
-        for (int s = 0; s < VEC; ++s)
-          if (d + s < D) x[s] = base[r * rs + d + s];
-      }
+      for (int s = 0; s < VEC; ++s)
+        if (d + s < D) x[s] = base[r * rs + d + s];
     }
     f[ch] = x;
   }
@@ -783,9 +794,16 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
   M::vec_t kf[DP / 8];
   load_frag_rows<float, DP>(kf, K, a.sk.t, kj, Tn, DP, g, true);
   float* Vs = lds + 4 * PER_WAVE;
-  for (int f = threadIdx.x; f < MT * DP / 4; f += 256) {
-    const int r = f / (DP / 4), d = (f % (DP / 4)) * 4;
-    *reinterpret_cast<V4*>(Vs + r * LD + d) = *reinterpret_cast<const V4*>(Vv + (int64_t)(k0 + r) * a.sv.t + d);
+  // the block's V rows: this thread's vectors go to registers first, and to
+  // LDS only after the first tile's loads are issued too, so the prologue
+  // waits for global memory once
+  constexpr int VN = MT * DP / 4 / 256;
+  static_assert(VN * 256 == MT * DP / 4, "V rows: whole vectors per thread");
+  V4 vrow[VN];
+#pragma unroll
+  for (int i = 0; i < VN; ++i) {
+    const int f = threadIdx.x + 256 * i, r = f / (DP / 4), d = (f % (DP / 4)) * 4;
+    vrow[i] = *reinterpret_cast<const V4*>(Vv + (int64_t)(k0 + r) * a.sv.t + d);
   }
   M::acc_t dk[DP / MT], dv[DP / MT];
 #pragma unroll
@@ -827,10 +845,13 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
   };
 
   int qt = kt + wave;
-  if (qt < nt) {
-    fetch(qt * MT);
-    put();
+  if (qt < nt) fetch(qt * MT);
+#pragma unroll
+  for (int i = 0; i < VN; ++i) {
+    const int f = threadIdx.x + 256 * i, r = f / (DP / 4), d = (f % (DP / 4)) * 4;
+    *reinterpret_cast<V4*>(Vs + r * LD + d) = vrow[i];
   }
+  if (qt < nt) put();
   __syncthreads();  // V rows and every wave's first tile in place
   for (; qt < nt; qt += 4) {
     const int qs = qt * MT;
