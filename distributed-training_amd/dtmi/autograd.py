@@ -397,7 +397,13 @@ def causal_attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
 
 def cross_entropy(logits: Tensor, targets) -> Tensor:
     """dtrain/autograd.py:250-266: mean cross-entropy; `targets`: a host integer
-    array or an Indices."""
+    array or an Indices.
+
+    With gradients enabled the logits' gradient ([rows, V], as large as the
+    logits) is computed by the forward pass and held until backward runs or
+    the returned loss tensor is dropped. Evaluate under `no_grad()` to skip
+    it: a validation loss taken with gradients on keeps that array alive for
+    as long as its loss tensor lives."""
     z = _contig(logits.data)
     V = z.shape[-1]
     t = as_indices(targets)
