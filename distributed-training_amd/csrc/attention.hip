@@ -1432,15 +1432,15 @@ static int attn_fwd_impl(AttnArgs& a) {
 static int64_t g_max_ds_bytes = (int64_t)4 << 30;
 
 template <typename T>
-static int attn_bwd_impl(AttnArgs& a) {
+static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
   constexpr int MT = AM<T>::MT;
   const int dp = pick_dp<T>(a.D);
   if (dp < 0) return attn_bwd_wide<T>(a);
   const int64_t rows = a.B * a.H * a.T;
-  void* drow = nullptr;
-  int rc = pool_alloc(&drow, (size_t)rows * sizeof(T));
+  void* drow = nullptr;  // rowsum(dO * O): given, or computed below
+  int rc = drow_in ? 0 : pool_alloc(&drow, (size_t)rows * sizeof(T));
   if (rc) return rc;
-  a.drow = drow;
+  a.drow = drow_in ? const_cast<void*>(drow_in) : drow;
   // dS for the dQ pass: B*H*T*T elements, up to g_max_ds_bytes; beyond that
   // the dQ pass recomputes S, P and dP itself.
   a.ds = nullptr;
@@ -1457,10 +1457,12 @@ static int attn_bwd_impl(AttnArgs& a) {
     TimedLaunch tl(DTMI_FAM_ATTN_BWD, 5.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
     const bool drow64 = std::is_same<T, float>::value && a.D == 64 && aligned(a.o, 16) && aligned(a.dO, 16) &&
                         strides_vec(a.so, 4) && strides_vec(a.sdo, 4);
-    if (drow64)
+    if (drow_in) {
+    } else if (drow64) {
       attn_drow64_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, stream()>>>(a);
-    else
+    } else {
       attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
+    }
     dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
     // float32, D = 64, T a multiple of 32: one key (query) tile per block with
     // independent waves; otherwise 128-key (128-query) blocks
@@ -1532,13 +1534,12 @@ DTMI_EXPORT int dtmi_attn_fwd(int dtype, int64_t B, int64_t H, int64_t T, int64_
   DTMI_BODY_END
 }
 
-DTMI_EXPORT int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
-                              const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
-                              const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dO,
-                              const int64_t* dO_strides, const void* rowmax, const void* rowsum, void* dq,
-                              const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
-                              const int64_t* dv_strides) {
-  DTMI_BODY_BEGIN
+static int attn_bwd_entry(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
+                          const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                          const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dO,
+                          const int64_t* dO_strides, const void* rowmax, const void* rowsum, void* dq,
+                          const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                          const int64_t* dv_strides, const void* drow) {
   DTMI_REQUIRE_INIT();
   DTMI_DTYPE_OK(dtype);
   DTMI_CHECK(B >= 0 && H >= 0 && T >= 0 && D > 0 && B * H < 65536, "dtmi_attn_bwd: bad shape (B*H must be < 65536)");
@@ -1576,8 +1577,32 @@ DTMI_EXPORT int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_
            strides_vec(a.sdo, vecn))
               ? 1
               : 0;
-  if (dtype == DTMI_F32) return attn_bwd_impl<float>(a);
-  return attn_bwd_impl<double>(a);
+  if (dtype == DTMI_F32) return attn_bwd_impl<float>(a, drow);
+  return attn_bwd_impl<double>(a, drow);
+}
+
+DTMI_EXPORT int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
+                              const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                              const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dO,
+                              const int64_t* dO_strides, const void* rowmax, const void* rowsum, void* dq,
+                              const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                              const int64_t* dv_strides) {
+  DTMI_BODY_BEGIN
+  return attn_bwd_entry(dtype, B, H, T, D, scale, q, q_strides, k, k_strides, v, v_strides, o, o_strides, dO,
+                        dO_strides, rowmax, rowsum, dq, dq_strides, dk, dk_strides, dv, dv_strides, nullptr);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_attn_bwd_rowsum(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale,
+                                     const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                     const void* v, const int64_t* v_strides, const void* o, const int64_t* o_strides,
+                                     const void* dO, const int64_t* dO_strides, const void* rowmax,
+                                     const void* rowsum, const void* drow, void* dq, const int64_t* dq_strides,
+                                     void* dk, const int64_t* dk_strides, void* dv, const int64_t* dv_strides) {
+  DTMI_BODY_BEGIN
+  DTMI_CHECK(drow != nullptr, "dtmi_attn_bwd_rowsum: NULL rowsum(dO * O)");
+  return attn_bwd_entry(dtype, B, H, T, D, scale, q, q_strides, k, k_strides, v, v_strides, o, o_strides, dO,
+                        dO_strides, rowmax, rowsum, dq, dq_strides, dk, dk_strides, dv, dv_strides, drow);
   DTMI_BODY_END
 }
 

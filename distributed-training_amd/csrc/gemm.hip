@@ -1189,6 +1189,62 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs a, const T*
   }
 }
 
+// Row dots of a float32 product whose rows are H = N / 64 groups of 64
+// columns -- the attention output's gradient dO = dY W^T of the projection
+// that reads the attention output X = O -- with X: rowdot[(b H + h) T + t] =
+// sum_d C[m, 64 h + d] X[m, 64 h + d] for row m = b T + t, the rowsum(dO * O)
+// term of the attention backward. Summed as the attention backward's own
+// row pass sums it (four products in order, then a 16-lane butterfly), so the
+// bits are that pass's. splitk_rowdot_kernel also forms C as the plain
+// split-K sum (splitk_reduce_kernel's order); rowdot64_kernel reads a finished
+// C. 16 consecutive threads cover one (row, group): N % 64 == 0.
+__device__ __forceinline__ void rowdot_group(float d, int64_t idx, int64_t N, int64_t T, float* __restrict__ rowdot) {
+#pragma unroll
+  for (int off = 8; off >= 1; off >>= 1) d += __shfl_xor(d, off, 16);
+  if ((threadIdx.x & 15) == 0) {
+    const int64_t m = idx / N, h = (idx - m * N) / 64, b = m / T, t = m - b * T;
+    rowdot[(b * (N / 64) + h) * T + t] = d;
+  }
+}
+
+__global__ void __launch_bounds__(256) splitk_rowdot_kernel(GemmArgs a, const float* __restrict__ ws, int splits,
+                                                             const float* __restrict__ X, float* __restrict__ rowdot,
+                                                             int64_t T) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const int64_t N = a.N, total = a.M * N, nvec = total / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  float* C = (float*)a.C;
+  for (int64_t iv = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; iv < nvec; iv += stride) {
+    const int64_t idx = iv * 4;
+    f4 v = *reinterpret_cast<const f4*>(ws + idx);
+    int s = 1;
+    for (; s + 3 < splits; s += 4) {
+      f4 t[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) t[u] = *reinterpret_cast<const f4*>(ws + (int64_t)(s + u) * total + idx);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v = v + t[u];
+    }
+    for (; s < splits; ++s) v = v + *reinterpret_cast<const f4*>(ws + (int64_t)s * total + idx);
+    *reinterpret_cast<f4*>(C + idx) = v;
+    const f4 o = *reinterpret_cast<const f4*>(X + idx);
+    rowdot_group(((o[0] * v[0] + o[1] * v[1]) + o[2] * v[2]) + o[3] * v[3], idx, N, T, rowdot);
+  }
+}
+
+__global__ void __launch_bounds__(256) rowdot64_kernel(const float* __restrict__ C, const float* __restrict__ X,
+                                                        float* __restrict__ rowdot, int64_t M, int64_t N, int64_t T) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const int64_t nvec = M * N / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t iv = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; iv < nvec; iv += stride) {
+    const int64_t idx = iv * 4;
+    const f4 v = *reinterpret_cast<const f4*>(C + idx);
+    const f4 o = *reinterpret_cast<const f4*>(X + idx);
+    rowdot_group(((o[0] * v[0] + o[1] * v[1]) + o[2] * v[2]) + o[3] * v[3], idx, N, T, rowdot);
+  }
+}
+
 // Split-K sum, bias and residual of an output row, then the LayerNorm of the
 // finished row, in one pass: one wave per row, the row in registers. The
 // output element is (((p_0 + p_1) + ...) + bias) then residual + that -- the
@@ -1316,6 +1372,10 @@ struct EpiArgs {
   void* aux = nullptr;
   void* colsum = nullptr;  // column sums of B (length N), unbatched
   int colsum_accumulate = 0;
+  // float32 row dots with X per 64-column group (see splitk_rowdot_kernel)
+  const void* rowdot_x = nullptr;
+  void* rowdot_out = nullptr;
+  int64_t rowdot_T = 1;
   // LayerNorm of the finished output rows (after bias and residual):
   // ln_out = layer_norm(C; ln_w, ln_b, ln_eps), with the row mean and rstd
   void* ln_out = nullptr;
@@ -1428,6 +1488,12 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
                         N % LVW == 0 && ldc == N && ln_nv > 0 && aligned(C, 16) && (!bias || aligned(bias, 16)) &&
                         (!a.addend || aligned(a.addend, 16)) && aligned(ep.ln_out, 16) && aligned(ep.ln_w, 16) &&
                         aligned(ep.ln_b, 16);
+  // row dots of C with X fused into the split-K sum when C is a plain sum,
+  // else a pass over the finished C
+  const bool rowdot_fused = ep.rowdot_out && splits > 1 && batch == 1 && !bias && !a.addend && !a.accumulate &&
+                            a.epi == kEpiNone && ldc == N && N % 64 == 0 && aligned(C, 16) &&
+                            aligned(ep.rowdot_x, 16);
+  bool rowdot_done = false;
   dim3 grid((unsigned)tiles, (unsigned)splits, (unsigned)batch);
   {
     TimedLaunch tl(DTMI_FAM_GEMM, 2.0 * (double)M * N * K * batch);
@@ -1453,7 +1519,15 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
       const bool vec_ok = N % V == 0 && ldc % V == 0 && (batch == 1 || sC % V == 0) && aligned(C, 16) &&
                           (!bias || aligned(bias, 16)) && (!a.addend || aligned(a.addend, 16)) &&
                           (!a.aux || aligned(a.aux, 16));
-      if (plain && vec_ok)
+      if constexpr (std::is_same<T, float>::value) {
+        if (rowdot_fused) {
+          splitk_rowdot_kernel<<<rg, 256, 0, stream()>>>(r, (const float*)ws, splits, (const float*)ep.rowdot_x,
+                                                          (float*)ep.rowdot_out, ep.rowdot_T);
+          rowdot_done = true;
+        }
+      }
+      if (rowdot_done) {
+      } else if (plain && vec_ok)
         splitk_reduce_kernel<T, true, V><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
       else if (vec_ok)
         splitk_reduce_kernel<T, false, V><<<rg, 256, 0, stream()>>>(r, (const T*)ws, splits, batch);
@@ -1475,6 +1549,14 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
                                                           (T)ep.ln_eps)
     LN_NV_SWITCH(ln_nv, CALL_LN)
 #undef CALL_LN
+  }
+  if constexpr (std::is_same<T, float>::value) {
+    if (ep.rowdot_out && !rowdot_done) {
+      TimedLaunch tl(DTMI_FAM_OTHER, 2.0 * (double)M * N * sizeof(T));
+      const int64_t nv = M * N / 4;
+      rowdot64_kernel<<<(unsigned)(cdiv(nv, 256) < 8192 ? cdiv(nv, 256) : 8192), 256, 0, stream()>>>(
+          (const float*)C, (const float*)ep.rowdot_x, (float*)ep.rowdot_out, M, N, ep.rowdot_T);
+    }
   }
   hipError_t le = hipGetLastError();
   if (ws) pool_free(ws);
@@ -1596,6 +1678,23 @@ DTMI_EXPORT int dtmi_linear_bwd_dx(int dtype, void* dX, const void* dY, const vo
   DTMI_REQUIRE_INIT();
   // dX[m, k] = sum_n dY[m, n] W[k, n]: A = dY (k-contiguous over n), B(n, k) = W[k, n] (k-contiguous)
   return gemm_dispatch(dtype, 1, 1, M, K, N, dY, N, 0, W, N, 0, dX, K, 0, 1, nullptr, accumulate, 0);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_bwd_dx_rowdot(int dtype, void* dX, const void* dY, const void* W, const void* X,
+                                          void* rowdot, int64_t M, int64_t K, int64_t N, int64_t T) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_CHECK(dtype == DTMI_F32, "dtmi_linear_bwd_dx_rowdot: float32 only");
+  DTMI_CHECK(M >= 0 && K > 0 && N >= 0 && T > 0 && K % 64 == 0 && M % T == 0,
+             "dtmi_linear_bwd_dx_rowdot: needs K %% 64 == 0 and M %% T == 0 (M=%lld K=%lld T=%lld)", (long long)M,
+             (long long)K, (long long)T);
+  DTMI_CHECK(X && rowdot && aligned(dX, 16) && aligned(X, 16), "dtmi_linear_bwd_dx_rowdot: NULL or unaligned X / dX");
+  EpiArgs ep;
+  ep.rowdot_x = X;
+  ep.rowdot_out = rowdot;
+  ep.rowdot_T = T;
+  return gemm_dispatch(dtype, 1, 1, M, K, N, dY, N, 0, W, N, 0, dX, K, 0, 1, nullptr, 0, 0, ep);
   DTMI_BODY_END
 }
 

@@ -80,9 +80,12 @@ SIGNATURES: dict[str, list] = {
     "dtmi_linear_fwd_fused": [i32, vp, vp, vp, vp, vp, vp, i64, i64, i64],
     "dtmi_linear_fwd_ln": [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, f64, i64, i64, i64],
     "dtmi_linear_bwd_dx_gelu": [i32, vp, vp, vp, vp, i64, i64, i64],
+    "dtmi_linear_bwd_dx_rowdot": [i32, vp, vp, vp, vp, vp, i64, i64, i64, i64],
     "dtmi_attn_fwd": [i32, i64, i64, i64, i64, f64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, vp],
     "dtmi_attn_bwd": [i32, i64, i64, i64, i64, f64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, vp,
                       vp, pi64, vp, pi64, vp, pi64],
+    "dtmi_attn_bwd_rowsum": [i32, i64, i64, i64, i64, f64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, pi64, vp, vp,
+                             vp, vp, pi64, vp, pi64, vp, pi64],
     "dtmi_attn_set_ds_limit": [i64, pi64],
 }
 

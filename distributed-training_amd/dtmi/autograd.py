@@ -74,7 +74,7 @@ def _broadcast_to(g: DeviceArray, shape) -> DeviceArray:
 
 class Tensor:
     __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "_hooks", "name", "grad_dest",
-                 "_dest_live", "_ln_pre", "__weakref__")
+                 "_dest_live", "_ln_pre", "_rowdot", "__weakref__")
 
     def __init__(self, data, requires_grad=False, _parents=(), _backward=None, name=None):
         self.data = data if isinstance(data, DeviceArray) else dev.asarray(np.asarray(data))
@@ -92,6 +92,7 @@ class Tensor:
         # A LayerNorm of this tensor computed by the kernel that produced it
         # (w, b, eps, y, mean, rstd); layer_norm(self, w, b, eps) takes it once.
         self._ln_pre = None
+        self._rowdot = None
 
     # ------------------------------------------------------------ utilities
     @property

@@ -514,10 +514,13 @@ def linear_fwd_ln(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None, residu
 
 def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, need_db=True,
                dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None,
-               gelu_pre: DeviceArray | None = None):
+               gelu_pre: DeviceArray | None = None, rowdot: DeviceArray | None = None, rowdot_t: int = 1):
     """Returns (dx, dw, db) for y = x @ w + b with x [M, K], w [K, N]; dw / db
     are written into dw_out / db_out when given. With gelu_pre (the [M, K]
-    pre-activation whose GELU is x), dx is the gradient of that pre-activation."""
+    pre-activation whose GELU is x), dx is the gradient of that pre-activation.
+    With rowdot (float32 [M / rowdot_t * K / 64 * rowdot_t]): also the per-64-
+    column row dots of dx with x, laid out [B, K / 64, T] for rows m = b T + t
+    (the attention backward's rowsum(dO * O) when x is the attention output)."""
     _contig(x2, w, dy2)
     M, K = x2.shape
     N = w.shape[1]
@@ -532,6 +535,11 @@ def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, 
             if gelu_pre.shape != (M, K):
                 raise ValueError("linear_bwd: pre-activation shape mismatch")
             _c("dtmi_linear_bwd_dx_gelu", dt, dx.ptr, dy2.ptr, w.ptr, gelu_pre.ptr, M, K, N)
+        elif rowdot is not None:
+            _contig(rowdot)
+            if rowdot.dtype != x2.dtype or rowdot.size != M * (K // 64):
+                raise ValueError("linear_bwd: rowdot must hold M * K / 64 values of x's dtype")
+            _c("dtmi_linear_bwd_dx_rowdot", dt, dx.ptr, dy2.ptr, w.ptr, x2.ptr, rowdot.ptr, M, K, N, int(rowdot_t))
         else:
             _c("dtmi_linear_bwd_dx", dt, dx.ptr, dy2.ptr, w.ptr, M, K, N, 0)
     dw = _out_or_new(dw_out, (K, N), x2.dtype, "linear_bwd")
@@ -567,8 +575,10 @@ def attn_fwd(q: DeviceArray, k: DeviceArray, v: DeviceArray, out: DeviceArray | 
     return out, rowmax, rowsum
 
 
-def attn_bwd(q, k, v, o, dO, rowmax, rowsum, dq=None, dk=None, dv=None, scale=None):
-    """Returns (dq, dk, dv); each may be passed as a (B, H, T, D) view to fill."""
+def attn_bwd(q, k, v, o, dO, rowmax, rowsum, dq=None, dk=None, dv=None, scale=None, drow=None):
+    """Returns (dq, dk, dv); each may be passed as a (B, H, T, D) view to fill.
+    `drow`: rowsum(dO * O) [B, H, T] when the caller already formed it
+    (linear_bwd(..., rowdot=)); the backward then skips its own row pass."""
     B, H, T, D = q.shape
     for x in (k, v, o, dO):
         if x.shape != q.shape:
@@ -579,6 +589,14 @@ def attn_bwd(q, k, v, o, dO, rowmax, rowsum, dq=None, dk=None, dv=None, scale=No
     dk = dk if dk is not None else empty(q.shape, q.dtype)
     dv = dv if dv is not None else empty(q.shape, q.dtype)
     s = float(1.0 / np.sqrt(D)) if scale is None else float(scale)
+    if drow is not None:
+        _contig(drow)
+        if drow.dtype != q.dtype or drow.size != B * H * T:
+            raise ValueError("attn_bwd: drow must be [B, H, T] of the operands' dtype")
+        _c("dtmi_attn_bwd_rowsum", dt, B, H, T, D, s, q.ptr, _bht_strides(q), k.ptr, _bht_strides(k), v.ptr,
+           _bht_strides(v), o.ptr, _bht_strides(o), dO.ptr, _bht_strides(dO), rowmax.ptr, rowsum.ptr, drow.ptr,
+           dq.ptr, _bht_strides(dq), dk.ptr, _bht_strides(dk), dv.ptr, _bht_strides(dv))
+        return dq, dk, dv
     _c("dtmi_attn_bwd", dt, B, H, T, D, s, q.ptr, _bht_strides(q), k.ptr, _bht_strides(k), v.ptr, _bht_strides(v),
        o.ptr, _bht_strides(o), dO.ptr, _bht_strides(dO), rowmax.ptr, rowsum.ptr, dq.ptr, _bht_strides(dq), dk.ptr,
        _bht_strides(dk), dv.ptr, _bht_strides(dv))

@@ -20,6 +20,7 @@ in place.
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 
 import numpy as np
@@ -76,6 +77,13 @@ def param(arr, name=None):
     return Tensor(arr, requires_grad=True, name=name)
 
 
+# rowsum(dO * O) of an attention backward, formed by the projection's input-
+# gradient GEMM while it produces dO (linear -> qkv_attention): keyed by that
+# gradient array, so the attention backward uses it only when the gradient it
+# receives is exactly that array (not a sum with another path's gradient)
+_ROWSUMS: "weakref.WeakKeyDictionary" = weakref.WeakKeyDictionary()
+
+
 def _with_ln(X2, W, b, R2, ln: "LayerNorm | None", lead):
     """y = residual + (x @ w + b) as [*lead, N]; with `ln`, the kernel also
     computes ln(y), returned as the (w, b, eps, y, mean, rstd) that
@@ -104,9 +112,17 @@ def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = Non
 
     def bw(g):
         g2 = _contig(g).reshape(-1, W.shape[1])
+        # x is an attention output [B, T, H * 64]: dx is its dO, and the same
+        # pass forms the attention backward's rowsum(dO * O)
+        rs = None
+        if x._rowdot is not None and x.requires_grad:
+            rs = dev.empty((X.shape[0] * x._rowdot * X.shape[1],), X.dtype)
         dx, dw, db = K.linear_bwd(X2, W, g2, need_dx=x.requires_grad, need_db=b is not None, dw_out=grad_out(w),
-                                  db_out=grad_out(b) if b is not None else None)
+                                  db_out=grad_out(b) if b is not None else None, rowdot=rs,
+                                  rowdot_t=X.shape[1] if rs is not None else 1)
         out = [dx.reshape(X.shape) if dx is not None else None, dw]
+        if rs is not None:
+            _ROWSUMS[out[0]] = rs
         if b is not None:
             out.append(db)
         if residual is not None:
@@ -165,13 +181,17 @@ def qkv_attention(qkv: Tensor, heads: int) -> Tensor:
     _, rmax, rsum = K.attn_fwd(t5[0], t5[1], t5[2], out=out.reshape(B, T, heads, D).transpose(0, 2, 1, 3))
 
     def bw(g):
+        drow = _ROWSUMS.pop(g, None)
         gq = dev.empty((B, T, C3), qkv.dtype)
         d5 = gq.reshape(B, T, 3, heads, D).transpose(2, 0, 3, 1, 4)
         gv = _contig(g).reshape(B, T, heads, D).transpose(0, 2, 1, 3)
         o = out.reshape(B, T, heads, D).transpose(0, 2, 1, 3)
-        K.attn_bwd(t5[0], t5[1], t5[2], o, gv, rmax, rsum, dq=d5[0], dk=d5[1], dv=d5[2])
+        K.attn_bwd(t5[0], t5[1], t5[2], o, gv, rmax, rsum, dq=d5[0], dk=d5[1], dv=d5[2], drow=drow)
         return (gq,)
-    return Tensor._make(out, (qkv,), bw)
+    t = Tensor._make(out, (qkv,), bw)
+    if D == 64 and qkv.dtype == np.float32:
+        t._rowdot = heads  # its gradient's producer may form rowsum(dO * O) per head
+    return t
 
 
 class Linear(Module):

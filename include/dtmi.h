@@ -333,6 +333,17 @@ int dtmi_linear_fwd_ln(int dtype, void* Y, void* H, void* mean, void* rstd, cons
  * backward of autograd.py:139-143 (pre = the saved pre-activation [M, K]). */
 int dtmi_linear_bwd_dx_gelu(int dtype, void* dX, const void* dY, const void* W, const void* pre, int64_t M, int64_t K,
                             int64_t N);
+/* dX = dY W^T (autograd.py:106) for the projection that reads the attention
+ * output X = o [M, K] (Block's self.proj(att), dtrain/nn.py:103-104), plus
+ * the rowsum(dO * O) term of the attention backward (autograd.py:242: the
+ * (dP * P).sum(-1) of the softmax backward) for each 64-wide head:
+ * rowdot[(b H + h) T + t] = sum_d dX[m, 64 h + d] X[m, 64 h + d], m = b T + t,
+ * H = K / 64 -- summed in the split-K pass that forms dX, else in a pass over
+ * it; the same bits as dtmi_attn_bwd's own row pass, so dtmi_attn_bwd_rowsum
+ * gives dtmi_attn_bwd's results. float32, X and dX contiguous and 16-byte
+ * aligned, K % 64 == 0, M % T == 0. */
+int dtmi_linear_bwd_dx_rowdot(int dtype, void* dX, const void* dY, const void* W, const void* X, void* rowdot,
+                              int64_t M, int64_t K, int64_t N, int64_t T);
 
 /* ------------------------------------------------------- causal attention
  * dtrain/autograd.py:226-247: o = softmax(q k^T * scale + causal mask) v over
@@ -352,6 +363,15 @@ int dtmi_attn_bwd(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double 
                   const int64_t* dO_strides, const void* rowmax, const void* rowsum, void* dq,
                   const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
                   const int64_t* dv_strides);
+/* dtmi_attn_bwd with rowsum(dO * O) [B, H, T] already formed (by
+ * dtmi_linear_bwd_dx_rowdot, in the pass that produced dO): the same results
+ * without the backward's own row pass over o and dO. */
+int dtmi_attn_bwd_rowsum(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, double scale, const void* q,
+                         const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+                         const int64_t* v_strides, const void* o, const int64_t* o_strides, const void* dO,
+                         const int64_t* dO_strides, const void* rowmax, const void* rowsum, const void* drow,
+                         void* dq, const int64_t* dq_strides, void* dk, const int64_t* dk_strides, void* dv,
+                         const int64_t* dv_strides);
 /* The backward's dQ pass reads the dS = P * (dP - rowsum(dO * O)) that its key
  * pass wrote to a pooled [B, H, T, T] workspace when that takes at most
  * `bytes` (default 4 GiB), and otherwise recomputes S, P and dP itself (the

@@ -144,3 +144,42 @@ def test_head_dimensions_beyond_64(dev, dt, shape):
     rng = np.random.default_rng(sum(shape) + 1)
     q, k, v, g = (rng.standard_normal(shape).astype(dt) for _ in range(4))
     _check(D, K, q, k, v, g, dt)
+
+
+@pytest.mark.parametrize("B,T,H,N", [(2, 64, 2, 96), (4, 1024, 12, 768)])
+def test_rowsum_formed_by_the_projection_gradient(dev, B, T, H, N):
+    """dtmi_linear_bwd_dx_rowdot (the projection that reads the attention
+    output O: dO = dY W^T, plus rowsum(dO * O) per 64-wide head, in the split-K
+    pass at the GPT-2-small shape and in a pass over dO at the small one) then
+    dtmi_attn_bwd_rowsum: dO bit-equal to dtmi_linear_bwd_dx's, the row sums
+    within float32 rounding of a float64 sum, and dq, dk, dv bit-equal to
+    dtmi_attn_bwd computing the row sums itself (dtrain/autograd.py:242,
+    nn.py:103-104)."""
+    D, K = _dev()
+    dt = np.float32
+    C = H * 64
+    rng = np.random.default_rng(B + T)
+    qkv = rng.standard_normal((B, T, 3, H, 64)).astype(dt)
+    w = (rng.standard_normal((C, N)) * 0.05).astype(dt)
+    dy = rng.standard_normal((B * T, N)).astype(dt)
+    dqkv = D.from_numpy(qkv)
+    t5 = dqkv.transpose(2, 0, 3, 1, 4)
+    obuf = D.empty((B, T, H, 64), dt)
+    _, rmax, rsum = K.attn_fwd(t5[0], t5[1], t5[2], out=obuf.transpose(0, 2, 1, 3))
+    x2 = obuf.reshape(B * T, C)
+    dw_ = D.from_numpy(w)
+    rs = D.empty((B * H * T,), dt)
+    do_fused, _, _ = K.linear_bwd(x2, dw_, D.from_numpy(dy), need_db=False, rowdot=rs, rowdot_t=T)
+    do_plain, _, _ = K.linear_bwd(x2, dw_, D.from_numpy(dy), need_db=False)
+    assert np.array_equal(do_fused.numpy().view(np.uint32), do_plain.numpy().view(np.uint32))
+    o64 = obuf.numpy().astype(np.float64).reshape(B, T, H, 64)
+    g64 = do_plain.numpy().astype(np.float64).reshape(B, T, H, 64)
+    ref = np.einsum("bthd,bthd->bht", o64, g64)
+    assert rel_err(rs.numpy().reshape(B, H, T), ref) <= 1e-6
+    g4 = do_plain.reshape(B, T, H, 64).transpose(0, 2, 1, 3)
+    o4 = obuf.transpose(0, 2, 1, 3)
+    a = [D.full((B, T, 3, H, 64), 3.0, dt) for _ in range(2)]
+    for buf, drow in zip(a, (None, rs)):
+        d5 = buf.transpose(2, 0, 3, 1, 4)
+        K.attn_bwd(t5[0], t5[1], t5[2], o4, g4, rmax, rsum, dq=d5[0], dk=d5[1], dv=d5[2], drow=drow)
+    assert np.array_equal(a[0].numpy().view(np.uint32), a[1].numpy().view(np.uint32))
