@@ -14,7 +14,10 @@ this build's layout, so either order gives dtrain's bits.
 
 `SimGroup` stands where dtrain's ProcessGroup stands for DDP and ZeroAdamW:
 `.rank` (the replica currently running), `.world`, `broadcast`, `barrier`,
-plus the fixed-order reduction itself.
+plus the fixed-order reduction itself. Its collectives (`allreduce`,
+`allreduce_async`, `reduce_scatter`, `all_gather`) take every rank's buffer
+at once -- one process holds them all -- and give each rank the bits dtrain's
+collective would leave in that rank's buffer.
 """
 from __future__ import annotations
 
@@ -76,11 +79,106 @@ class SimGroup:
     def barrier(self):
         _lib.sync()
 
+    # ------------------------------------------------ dtrain's collectives
+    def _ranks(self, arrays, name):
+        arrays = list(arrays)
+        if len(arrays) != self.world:
+            raise ValueError(f"{name}: need one array per rank ({self.world}), got {len(arrays)}")
+        a0 = arrays[0]
+        for a in arrays:
+            if a.shape != a0.shape or a.dtype != a0.dtype:
+                raise ValueError(f"{name}: every rank's array must have the same shape and dtype")
+            if not a.is_contiguous:
+                raise ValueError(f"{name} needs contiguous arrays")
+        return arrays
+
+    def _ordered_sum(self, arrays, firsts):
+        """[n] sum over the ranks' arrays, element i summed starting at rank
+        firsts(i) (see ring_segments); returns the sum as a new array."""
+        n = arrays[0].size
+        rows = dev.empty((self.world, max(n, 1)), arrays[0].dtype)
+        for r, a in enumerate(arrays):
+            if n:
+                K.copy_into(rows[r][:n], a.reshape(-1))
+        out = dev.empty((n,), arrays[0].dtype)
+        if n:
+            K.bucket_average(out, rows, self.world, 1.0, segments=firsts)
+        return out
+
+    def allreduce(self, arrays, algo: str = "ring"):
+        """dtrain/comm.py:292-307, ProcessGroup.allreduce, for all W ranks at
+        once: `arrays[r]` is rank r's contiguous array; afterwards every one
+        holds the sum over ranks in `algo`'s order -- ring: chunk c of
+        partition(n, W) summed starting at rank c, (x_c + x_{c+1}) + ... +
+        x_{c-1} (comm.py:342-372); direct: rank 0 first (comm.py:374-391).
+        Returns the list."""
+        if algo not in ("ring", "direct"):
+            raise ValueError(algo)
+        arrays = self._ranks(arrays, "allreduce")
+        if self.world == 1:
+            return arrays
+        n = arrays[0].size
+        segs = None
+        if algo == "ring":
+            b = partition(n, self.world)
+            segs = [(b[c], c) for c in range(self.world) if b[c] < b[c + 1]] or [(0, 0)]
+        total = self._ordered_sum(arrays, segs)
+        for a in arrays:
+            if n:
+                K.copy_into(a.reshape(-1), total)
+        return arrays
+
+    def allreduce_async(self, arrays, algo: str = "ring"):
+        """comm.py:397-401: the same as allreduce (ordered on the library
+        stream); the returned work's wait() returns once it has been issued."""
+        self.allreduce(arrays, algo)
+        return _Done()
+
+    def reduce_scatter(self, flats):
+        """comm.py:309-315 for all W ranks: afterwards partition r of flats[r]
+        holds the total of that partition, summed starting at rank r (the
+        ring's order with ownership rotated); returns the W partition views.
+        The other partitions keep their values (dtrain leaves partial sums
+        there, which nothing reads)."""
+        flats = self._ranks(flats, "reduce_scatter")
+        n = flats[0].size
+        b = partition(n, self.world)
+        views = [flats[r].reshape(-1)[b[r]:b[r + 1]] for r in range(self.world)]
+        if self.world == 1:
+            return views
+        segs = [(b[c], c) for c in range(self.world) if b[c] < b[c + 1]] or [(0, 0)]
+        total = self._ordered_sum(flats, segs)
+        for r in range(self.world):
+            if b[r] < b[r + 1]:
+                K.copy_into(views[r], total[b[r]:b[r + 1]])
+        return views
+
+    def all_gather(self, flats):
+        """comm.py:317-321 for all W ranks: partition r of flats[r] is copied
+        into every rank's flat. Returns the list."""
+        flats = self._ranks(flats, "all_gather")
+        b = partition(flats[0].size, self.world)
+        for r in range(self.world):
+            if b[r] == b[r + 1]:
+                continue
+            src = flats[r].reshape(-1)[b[r]:b[r + 1]]
+            for q in range(self.world):
+                if q != r:
+                    K.copy_into(flats[q].reshape(-1)[b[r]:b[r + 1]], src)
+        return flats
+
     def average(self, out: DeviceArray, rows: DeviceArray, partials: DeviceArray | None = None, segments=None):
         """out = (((rows[0] + rows[1]) + ...) + rows[W-1]) * (1.0 / W), or in
         the rank orders of `segments` ((start, first_rank) pairs, see
         ring_segments)."""
         K.bucket_average(out, rows, self.world, 1.0 / self.world, partials=partials, segments=segments)
+
+
+class _Done:
+    """dtrain's Work (comm.py:229-238) for a collective already issued."""
+
+    def wait(self):
+        return None
 
 
 def ring_segments(sizes, world: int):
