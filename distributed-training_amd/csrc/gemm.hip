@@ -16,11 +16,11 @@
 // once and advanced by one k-tile per load (rows past the matrix edge clamped
 // onto the last row), so the main loop has no index arithmetic and no
 // divergent branches; only a partial last k-tile is masked.
-//   gemm_dma_kernel (float32, 16-byte aligned operands -- every GPT-2 GEMM):
-//     the loads go straight into LDS (global_load_lds_dwordx4) through three
-//     stages, in swizzled layouts that keep the fragment reads conflict-free.
-//   gemm_kernel (float64, and float32 with unaligned operands): registers ->
-//     LDS, double-buffered.
+//   gemm_dma_kernel (16-byte aligned operands -- every GPT-2 GEMM, in float32
+//     and float64): the loads go straight into LDS (global_load_lds_dwordx4)
+//     through three stages, in swizzled layouts that keep the fragment reads
+//     conflict-free.
+//   gemm_kernel (unaligned operands): registers -> LDS, double-buffered.
 //   gemm_x6_kernel (float32 when dtmi_set_gemm_math selects the split-bf16
 //     arithmetic, aligned operands): each operand split exactly into three
 //     bf16 parts on the way into LDS, six partial products on the bf16 MFMA
@@ -544,33 +544,42 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// float32 with direct global -> LDS loads (global_load_lds_dwordx4: each lane
-// fetches 16 bytes that land at LDS base + 16 * lane, with no register
-// staging, no LDS store instructions and no wait before a store). Three LDS
-// stages: tile t's loads are issued two iterations before it is computed.
+// Direct global -> LDS loads (global_load_lds_dwordx4: each lane fetches 16
+// bytes that land at LDS base + 16 * lane, with no register staging, no LDS
+// store instructions and no wait before a store), float32 and float64 alike:
+// a k-tile is 64 bytes of k per row (16 floats or 8 doubles), VEC = 16 bytes
+// of elements (4 floats or 2 doubles) per vector. Three LDS stages: tile t's
+// loads are issued two iterations before it is computed.
 // LDS layouts (a 1 KB load instruction fills 1 KB contiguously, so conflicts
 // are avoided by choosing which global vector each lane fetches):
-//   KC  (k-contiguous operand, 128 rows x 16 k): 1 KB chunks of 16 rows; the
-//       4-float k-vector v of chunk row r sits in 16-byte slot
+//   KC  (k-contiguous operand, BMN rows x 64 bytes): 1 KB chunks of 16 rows;
+//       the 16-byte k-vector v of chunk row r sits in 16-byte slot
 //       4 r + (v ^ kc_swz(r)), so the 16-byte fragment reads of 16
 //       consecutive rows hit distinct banks;
-//   MNC (mn-contiguous operand, 16 k-rows x 128): k-row k holds its 32
-//       mn-vectors u at slots 32 k + (u ^ mnc_swz(k)), so the two lane groups
-//       (k and k + 4) of a fragment read hit different bank halves.
+//   MNC (mn-contiguous operand, k-rows of BMN elements): k-row k holds its
+//       mn-vectors u at slots u ^ mnc_swz(k), which flips 128 bytes between
+//       the k-rows that the two lane groups of a half-wave fragment read
+//       (k and k + 4 for float32, k and k + 2 for float64), so they hit
+//       different bank halves.
 constexpr int kDmaStages = 3;
 
 __device__ __forceinline__ int kc_swz(int r) { return ((r >> 1) + (r >> 3)) & 3; }
-__device__ __forceinline__ int mnc_swz(int k) { return ((k >> 2) & 1) << 3; }
+template <typename T>
+__device__ __forceinline__ int mnc_swz(int k) {
+  return ((k >> (MF<T>::VEC == 4 ? 2 : 1)) & 1) << 3;
+}
 
-// Float offset, within one BMN x 16 operand tile, of the 4-float vector of
-// (row/col mn, k-vector v) for KC, or of (k-row k, mn-vector u) for MNC.
+// Element offset, within one BMN x 64-byte operand tile, of the 16-byte
+// vector of (row/col mn, k-vector v) for KC, or of (k-row k, mn-vector u)
+// for MNC.
+template <typename T>
 __device__ __forceinline__ int kc_off(int mn, int v) {
   const int r = mn & 15;
-  return (mn >> 4) * 256 + (4 * r + (v ^ kc_swz(r))) * 4;
+  return (mn >> 4) * (1024 / (int)sizeof(T)) + (4 * r + (v ^ kc_swz(r))) * MF<T>::VEC;
 }
-template <int BMN>
+template <typename T, int BMN>
 __device__ __forceinline__ int mnc_off(int k, int u) {
-  return k * BMN + ((u ^ mnc_swz(k)) << 2);
+  return k * BMN + (u ^ mnc_swz<T>(k)) * MF<T>::VEC;
 }
 
 // The BMN / 64 load instructions (1 KB each) of each wave per operand tile:
@@ -578,20 +587,21 @@ __device__ __forceinline__ int mnc_off(int k, int u) {
 // scalar adds) and fixed per-lane 32-bit byte offsets, so issuing a tile
 // takes no vector instructions. Offsets are >= 0: clamped rows / columns
 // stay at or after the tile origin (the origin is inside the matrix, and
-// MN - 4 >= mn0 because MN and mn0 are multiples of 4).
-template <bool KCONTIG, int BMN>
+// MN - VEC >= mn0 because MN and mn0 are multiples of VEC).
+template <typename T, bool KCONTIG, int BMN>
 struct DmaSrc {
   static constexpr int NQ = BMN / 64;
-  const float* base;
+  const T* base;
   unsigned off[NQ];
   int64_t step;  // elements per k-tile
 };
 
-template <bool KCONTIG, int BMN>
-__device__ __forceinline__ void dma_init(DmaSrc<KCONTIG, BMN>& s, const float* __restrict__ P, int64_t ld,
+template <typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void dma_init(DmaSrc<T, KCONTIG, BMN>& s, const T* __restrict__ P, int64_t ld,
                                          int64_t mn0, int64_t MN, int64_t kbeg, int wave, int lane) {
-  constexpr int NQ = DmaSrc<KCONTIG, BMN>::NQ;
-  constexpr int RV = BMN / 4;  // mn-vectors per k-row (MNC)
+  constexpr int NQ = DmaSrc<T, KCONTIG, BMN>::NQ;
+  constexpr int VEC = MF<T>::VEC;
+  constexpr int RV = BMN / VEC;  // mn-vectors per k-row (MNC)
   s.base = KCONTIG ? P + mn0 * ld + kbeg : P + kbeg * ld + mn0;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
@@ -601,16 +611,16 @@ __device__ __forceinline__ void dma_init(DmaSrc<KCONTIG, BMN>& s, const float* _
       int64_t mn = mn0 + 16 * j + r;
       mn = mn < MN ? mn : MN - 1;
       const int v = (lane & 3) ^ kc_swz(r);
-      s.off[q] = (unsigned)(((mn - mn0) * ld + 4 * v) * 4);
+      s.off[q] = (unsigned)(((mn - mn0) * ld + VEC * v) * (int64_t)sizeof(T));
     } else {
-      const int k = j * (64 / RV) + lane / RV;
-      const int u = (lane % RV) ^ mnc_swz(k);
-      int64_t mn = mn0 + 4 * u;
-      mn = mn < MN ? mn : MN - 4;
-      s.off[q] = (unsigned)((k * ld + (mn - mn0)) * 4);
+      const int k = (64 * j + lane) / RV;
+      const int u = ((64 * j + lane) % RV) ^ mnc_swz<T>(k);
+      int64_t mn = mn0 + VEC * u;
+      mn = mn < MN ? mn : MN - VEC;
+      s.off[q] = (unsigned)((k * ld + (mn - mn0)) * (int64_t)sizeof(T));
     }
   }
-  s.step = KCONTIG ? 16 : 16 * ld;
+  s.step = KCONTIG ? 64 / (int)sizeof(T) : (64 / (int)sizeof(T)) * ld;
 }
 
 // Issue one operand tile: chunk q of this wave lands at LDS byte address
@@ -619,9 +629,9 @@ __device__ __forceinline__ void dma_init(DmaSrc<KCONTIG, BMN>& s, const float* _
 // The asm writes no SCC (an s_add here would clobber the carry of a 64-bit
 // scalar add the compiler may have split around it): the address is summed
 // outside and moved in with s_mov_b32.
-template <int LDS_OFF, bool KCONTIG, int BMN>
-__device__ __forceinline__ void dma_issue(DmaSrc<KCONTIG, BMN>& s, unsigned lds_wave) {
-  constexpr int NQ = DmaSrc<KCONTIG, BMN>::NQ;
+template <int LDS_OFF, typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void dma_issue(DmaSrc<T, KCONTIG, BMN>& s, unsigned lds_wave) {
+  constexpr int NQ = DmaSrc<T, KCONTIG, BMN>::NQ;
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     const unsigned dst = lds_wave + (unsigned)(LDS_OFF + 1024 * q);
@@ -645,39 +655,40 @@ struct IC {
 
 // The partial last k-tile through registers, stored in the same layouts
 // (k at or past kend as zeros).
-template <bool KCONTIG, int BMN>
-__device__ __forceinline__ void dma_tail_store(float* __restrict__ tile, const TileRegs<float, KCONTIG, BMN>& r,
-                                               int64_t k0, int64_t kend) {
-  using L = TileLayout<float, KCONTIG, BMN>;
-  constexpr int RV = BMN / 4;
+template <typename T, bool KCONTIG, int BMN>
+__device__ __forceinline__ void dma_tail_store(T* __restrict__ tile, const TileRegs<T, KCONTIG, BMN>& r, int64_t k0,
+                                               int64_t kend) {
+  using L = TileLayout<T, KCONTIG, BMN>;
+  constexpr int VEC = L::VEC;
+  constexpr int RV = BMN / VEC;
 #pragma unroll
   for (int i = 0; i < L::NVEC; ++i) {
     const int f = threadIdx.x + 256 * i;
     int off;
     int64_t k;
     if (KCONTIG) {
-      off = kc_off(f / 4, f % 4);
-      k = k0 + (f % 4) * 4;
+      off = kc_off<T>(f / 4, f % 4);
+      k = k0 + (f % 4) * VEC;
     } else {
-      off = mnc_off<BMN>(f / RV, f % RV);
+      off = mnc_off<T, BMN>(f / RV, f % RV);
       k = k0 + f / RV;
     }
-    *reinterpret_cast<MF<float>::vec_t*>(tile + off) = k < kend ? r.v[i] : MF<float>::vec_t(0);
+    *reinterpret_cast<typename MF<T>::vec_t*>(tile + off) = k < kend ? r.v[i] : typename MF<T>::vec_t(0);
   }
 }
 
-// Block tile BM x BN (128 or 256 each), 4 waves in a 2 x 2 grid of
-// (BM/2) x (BN/2) wave tiles.
-template <int BM, int BN, bool AKC, bool BKC>
+// Block tile BM x BN (128 or 256 each; 128 x 128 for float64), 4 waves in a
+// 2 x 2 grid of (BM/2) x (BN/2) wave tiles.
+template <typename T, int BM, int BN, bool AKC, bool BKC>
 __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(GemmArgs a) {
-  using MFT = MF<float>;
-  constexpr int BK = 16;
-  constexpr int MT = MFT::MT, VEC = MFT::VEC;
+  using MFT = MF<T>;
+  constexpr int BK = 64 / (int)sizeof(T);
+  constexpr int MT = MFT::MT, VEC = MFT::VEC, LV = VEC == 4 ? 2 : 1;  // VEC = 1 << LV
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / MT, TN = WN / MT, NCH = BK / kKC;
-  constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // floats per operand tile
+  constexpr int TILE_A = BM * BK, TILE_B = BN * BK;  // elements per operand tile
   constexpr int NST = kDmaStages;
-  __shared__ __attribute__((aligned(1024))) float lds[NST * (TILE_A + TILE_B)];
+  __shared__ __attribute__((aligned(1024))) T lds[NST * (TILE_A + TILE_B)];
 
   int tm, tn;
   tile_coords(a, tm, tn);
@@ -686,59 +697,61 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
   const int64_t batch = blockIdx.z;
   const int64_t kbeg = (int64_t)split * a.k_per_split;
   const int64_t kend = kbeg + a.k_per_split < a.K ? kbeg + a.k_per_split : a.K;
-  const float* A = (const float*)a.A + batch * a.sA;
-  const float* B = (const float*)a.B + batch * a.sB;
+  const T* A = (const T*)a.A + batch * a.sA;
+  const T* B = (const T*)a.B + batch * a.sB;
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g = lane / MT, c = lane % MT;
   const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
 
-  MFT::acc_t acc[TM][TN];
+  typename MFT::acc_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = MFT::acc_t(0);
+    for (int j = 0; j < TN; ++j) acc[i][j] = typename MFT::acc_t(0);
 
   const int ntiles = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
   const int nfull = kend > kbeg ? (int)((kend - kbeg) / BK) : 0;
-  DmaSrc<AKC, BM> sa;
-  DmaSrc<BKC, BN> sb;
-  dma_init<AKC, BM>(sa, A, a.lda, m0, a.M, kbeg, wave, lane);
-  dma_init<BKC, BN>(sb, B, a.ldb, n0, a.N, kbeg, wave, lane);
+  DmaSrc<T, AKC, BM> sa;
+  DmaSrc<T, BKC, BN> sb;
+  dma_init<T, AKC, BM>(sa, A, a.lda, m0, a.M, kbeg, wave, lane);
+  dma_init<T, BKC, BN>(sb, B, a.ldb, n0, a.N, kbeg, wave, lane);
   auto tileA = [&](int st) { return lds + st * (TILE_A + TILE_B); };
   auto tileB = [&](int st) { return lds + st * (TILE_A + TILE_B) + TILE_A; };
   // LDS byte address of this wave's first A chunk and first B chunk in stage
   // 0 (the low 32 bits of a generic LDS address are the LDS offset)
   const unsigned lds0 = (unsigned)(uintptr_t)lds;
-  const unsigned ldsA = __builtin_amdgcn_readfirstlane(lds0 + wave * DmaSrc<AKC, BM>::NQ * 1024u);
-  const unsigned ldsB = __builtin_amdgcn_readfirstlane(lds0 + TILE_A * 4 + wave * DmaSrc<BKC, BN>::NQ * 1024u);
-  constexpr int STAGE_BYTES = (TILE_A + TILE_B) * 4;
-  constexpr int NQT = DmaSrc<AKC, BM>::NQ + DmaSrc<BKC, BN>::NQ;  // loads per wave per k-tile
+  const unsigned ldsA = __builtin_amdgcn_readfirstlane(lds0 + wave * DmaSrc<T, AKC, BM>::NQ * 1024u);
+  const unsigned ldsB =
+      __builtin_amdgcn_readfirstlane(lds0 + TILE_A * (unsigned)sizeof(T) + wave * DmaSrc<T, BKC, BN>::NQ * 1024u);
+  constexpr int STAGE_BYTES = (TILE_A + TILE_B) * (int)sizeof(T);
+  constexpr int NQT = DmaSrc<T, AKC, BM>::NQ + DmaSrc<T, BKC, BN>::NQ;  // loads per wave per k-tile
 
   // Per-lane fragment offsets within a tile: KC fragment (rows base + c,
-  // k-vector 2 ch + g); MNC fragment element s (k-row 8 ch + 4 g + s,
-  // column base + c).
-  auto frag = [&](const float* __restrict__ t, bool kcontig, int bmn, int base, int ch) {
-    MFT::vec_t v;
+  // k-vector (8 / VEC) ch + g); MNC fragment element s (k-row
+  // 8 ch + VEC g + s, column base + c).
+  auto frag = [&](const T* __restrict__ t, bool kcontig, int bmn, int base, int ch) {
+    typename MFT::vec_t v;
     if (kcontig) {
-      v = *reinterpret_cast<const MFT::vec_t*>(t + kc_off(base + c, 2 * ch + g));
+      v = *reinterpret_cast<const typename MFT::vec_t*>(t + kc_off<T>(base + c, (kKC / VEC) * ch + g));
     } else {
       const int n = base + c;
 #pragma unroll
-      for (int s = 0; s < VEC; ++s)
-        v[s] = t[(bmn == 256 ? mnc_off<256>(8 * ch + 4 * g + s, n >> 2) : mnc_off<128>(8 * ch + 4 * g + s, n >> 2)) +
-                 (n & 3)];
+      for (int s = 0; s < VEC; ++s) {
+        const int k = kKC * ch + VEC * g + s;
+        v[s] = t[(bmn == 256 ? mnc_off<T, 256>(k, n >> LV) : mnc_off<T, 128>(k, n >> LV)) + (n & (VEC - 1))];
+      }
     }
     return v;
   };
   const bool take_colsum = a.colsum != nullptr && tm == 0 && (int)threadIdx.x < BN;
   double csum = 0.0;
   auto compute = [&](int st) {
-    const float* As = tileA(st);
-    const float* Bs = tileB(st);  // st is a constant in the main loop: immediate LDS offsets
+    const T* As = tileA(st);
+    const T* Bs = tileB(st);  // st is a constant in the main loop: immediate LDS offsets
 #pragma unroll
     for (int ch = 0; ch < NCH; ++ch) {
-      MFT::vec_t fa[TM], fb[TN];
+      typename MFT::vec_t fa[TM], fb[TN];
 #pragma unroll
       for (int i = 0; i < TM; ++i) fa[i] = frag(As, AKC, BM, wm0 + i * MT, ch);
 #pragma unroll
@@ -751,13 +764,13 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
           for (int j = 0; j < TN; ++j) acc[i][j] = MFT::mma(fa[i][s], fb[j][s], acc[i][j]);
     }
     if (take_colsum) {
-      // this thread's column of the B tile, its 16 values in k order, then
+      // this thread's column of the B tile, its BK values in k order, then
       // into the running float64 sum (k past kend was stored as zero)
       const int n = threadIdx.x;
-      float t = 0.f;
+      T t = T(0);
 #pragma unroll
       for (int k = 0; k < BK; ++k)
-        t = t + (BKC ? Bs[kc_off(n, k >> 2) + (k & 3)] : Bs[mnc_off<BN>(k, n >> 2) + (n & 3)]);
+        t = t + (BKC ? Bs[kc_off<T>(n, k >> LV) + (k & (VEC - 1))] : Bs[mnc_off<T, BN>(k, n >> LV) + (n & (VEC - 1))]);
       csum += (double)t;
     }
   };
@@ -794,22 +807,22 @@ __global__ void __launch_bounds__(256, (BM + BN > 384 ? 1 : 2)) gemm_dma_kernel(
   const int st = nfull % 3;  // stage of the partial tile, if any
   if (ntiles > nfull) {  // the partial last k-tile, through registers
     const int64_t k0 = kbeg + (int64_t)nfull * BK;
-    TilePtr<float, AKC, BM> pa;
-    TilePtr<float, BKC, BN> pb;
-    TileRegs<float, AKC, BM> ra;
-    TileRegs<float, BKC, BN> rb;
-    init_ptr<float, AKC, BM>(pa, A, a.lda, m0, a.M, k0);
-    init_ptr<float, BKC, BN>(pb, B, a.ldb, n0, a.N, k0);
-    load_tail<float, AKC, BM>(ra, pa, a.lda, k0, kend);
-    load_tail<float, BKC, BN>(rb, pb, a.ldb, k0, kend);
+    TilePtr<T, AKC, BM> pa;
+    TilePtr<T, BKC, BN> pb;
+    TileRegs<T, AKC, BM> ra;
+    TileRegs<T, BKC, BN> rb;
+    init_ptr<T, AKC, BM>(pa, A, a.lda, m0, a.M, k0);
+    init_ptr<T, BKC, BN>(pb, B, a.ldb, n0, a.N, k0);
+    load_tail<T, AKC, BM>(ra, pa, a.lda, k0, kend);
+    load_tail<T, BKC, BN>(rb, pb, a.ldb, k0, kend);
     __syncthreads();  // every wave is done with the stage being refilled
-    dma_tail_store<AKC, BM>(tileA(st), ra, k0, kend);
-    dma_tail_store<BKC, BN>(tileB(st), rb, k0, kend);
+    dma_tail_store<T, AKC, BM>(tileA(st), ra, k0, kend);
+    dma_tail_store<T, BKC, BN>(tileB(st), rb, k0, kend);
     __syncthreads();
     compute(st);
   }
-  if (take_colsum) finish_colsum<float>(a, csum, n0 + threadIdx.x, split);
-  write_acc<float, TM, TN, true>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
+  if (take_colsum) finish_colsum<T>(a, csum, n0 + threadIdx.x, split);
+  write_acc<T, TM, TN, true>(a, acc, m0 + wm0, n0 + wn0, g, c, split, batch);
 }
 
 // ---------------------------------------------------------------------------
@@ -1322,11 +1335,10 @@ __global__ void __launch_bounds__(256) splitk_ln_kernel(GemmArgs a, const T* __r
 
 template <typename T, int BM, int BN, bool AKC, bool BKC>
 static void launch_variant(const GemmArgs& a, dim3 grid, bool veca, bool vecb, bool dma) {
-  if constexpr (std::is_same<T, float>::value) {
-    if (dma) {
-      gemm_dma_kernel<BM, BN, AKC, BKC><<<grid, 256, 0, stream()>>>(a);
-      return;
-    }
+  if (dma) {
+    if constexpr (std::is_same<T, float>::value || (BM == 128 && BN == 128))
+      gemm_dma_kernel<T, BM, BN, AKC, BKC><<<grid, 256, 0, stream()>>>(a);
+    return;
   }
   if constexpr (BM != 128 || BN != 128) return;  // larger tiles: aligned float32 only (see gemm_impl)
   if (veca && vecb)
@@ -1451,14 +1463,15 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   const bool veca = aligned(A, 16) && lda % VEC == 0 && (batch == 1 || sA % VEC == 0) && (akc ? K % VEC == 0 : M % VEC == 0);
   const bool vecb = aligned(B, 16) && ldb % VEC == 0 && (batch == 1 || sB % VEC == 0) && (bkc ? K % VEC == 0 : N % VEC == 0);
   // The direct-to-LDS kernel addresses a tile with 32-bit byte offsets from
-  // its origin: leading dimensions below 2^22 elements keep them in range.
-  const bool dma = std::is_same<T, float>::value && veca && vecb && lda < (1 << 22) && ldb < (1 << 22);
+  // its origin: leading dimensions below 2^24 bytes keep them in range.
+  constexpr int64_t kDmaMaxLd = (1 << 24) / (int64_t)sizeof(T);
+  const bool dma = veca && vecb && lda < kDmaMaxLd && ldb < kDmaMaxLd;
   // split-bf16 products: aligned float32 operands (its column sums need an
   // n-contiguous B)
   const bool x6 = std::is_same<T, float>::value && veca && vecb && g_gemm_math == DTMI_GEMM_MATH_BF16X6 &&
                   !(a.colsum && bkc) && lda < (1 << 22) && ldb < (1 << 22);
   int bm = 128, bn = 128;
-  if (dma && !x6) pick_tile(M, N, K, batch, cus, bm, bn);
+  if (std::is_same<T, float>::value && dma && !x6) pick_tile(M, N, K, batch, cus, bm, bn);
   const int64_t tmn = cdiv(M, bm) * cdiv(N, bn);
   int splits = force_splits > 0 ? force_splits : choose_splits(tmn, batch, K, cus);
   a.tiles_m = (int)cdiv(M, bm);

@@ -226,6 +226,31 @@ def test_gemm_split_k_with_partial_last_tile(dev, dt, akc, bkc):
     assert bits_equal(outs[1], outs[2])
 
 
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("akc,bkc", [(True, False), (True, True), (False, False), (False, True)])
+def test_gemm_direct_lds_kernel_matches_register_staged_kernel_bitwise(dev, dt, akc, bkc):
+    """16-byte aligned operands take the direct-to-LDS kernel; the same values
+    one element off alignment take the register-staged kernel. Both feed the
+    MFMAs the same k order, so the products agree to the bit (128 x 128
+    block tiles, one split, ragged M and N, a partial last k-tile)."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(41)
+    M, N, K = 300, 260, 1000
+    a = rng.standard_normal((M, K) if akc else (K, M)).astype(dt)
+    b = rng.standard_normal((N, K) if bkc else (K, N)).astype(dt)
+    bias = D.from_numpy(rng.standard_normal(N).astype(dt))
+    db = D.from_numpy(b)
+    big = D.empty((a.size + 1,), dt)
+    a_off = big[1:1 + a.size].reshape(*a.shape)
+    a_off.assign(a)
+    assert a_off.ptr % 16 != 0
+    aligned_ = K_.gemm(D.from_numpy(a), db, a_kcontig=akc, b_kcontig=bkc, bias=bias, splits=1).numpy()
+    staged = K_.gemm(a_off, db, a_kcontig=akc, b_kcontig=bkc, bias=bias, splits=1).numpy()
+    ref = _gemm_ref(a.astype(np.float64), b.astype(np.float64), akc, bkc) + bias.numpy()
+    assert rel_err(aligned_, ref) <= TOL[dt]
+    assert bits_equal(aligned_, staged)
+
+
 @pytest.mark.parametrize("akc,bkc", [(True, False), (True, True), (False, False), (False, True)])
 def test_gemm_large_tile_ragged_edges_and_k_tail(dev, akc, bkc):
     """float32 shapes whose k range per block is long enough for the 256 x 128
