@@ -207,6 +207,10 @@ __device__ __forceinline__ void mma_lds_t_regs(typename AM<T>::acc_t (&out)[DP /
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ double ex2(double x) { return exp2(x); }
 
+// Largest excess (log2 units) of a score over the forward's reference max
+// before the reference moves: probabilities stay <= 2^8.
+constexpr float kLazyLog2 = 8.0f;
+
 // Column swizzle of the transposed LDS tiles: XOR of bits 2-3 of the column
 // with bits 4-5 of the row, so groups of 4 columns stay 16-byte aligned and a
 // wave's transposed stores (16 rows 4 apart, 4 columns) hit 64 distinct banks.
@@ -414,6 +418,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] = typename M::acc_t(0);
   T mrow = ninf, lrow = T(0);
+  constexpr bool LAZY = FAST && sizeof(T) == 4;
+  T mtop = ninf;  // LAZY: this lane's running max of its own scores
 
   const int qlast = (q0 + QB < Tn ? q0 + QB : Tn) - 1;
   const int nkb = qlast / KB + 1;
@@ -463,29 +469,57 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
         scores(std::true_type());
       else
         scores(std::false_type());
-      bmax = group_max(bmax);
-      const T mnew = fmax(mrow, bmax);
-      // aligned path: every query sees key 0 in the first tile, so the max is
-      // finite from then on
-      const bool live = FAST || mnew != ninf;
-      const T alpha = live ? ex2(mrow - mnew) : T(1);
-      T psum = T(0);
+      if constexpr (LAZY) {
+        // Lazy rescaling: the probabilities are taken against a reference
+        // max mrow (equal across the lane groups of a query column) that
+        // moves only when a score exceeds it by more than kLazyLog2, so
+        // p <= 2^kLazyLog2 and the output and sum are rescaled a few times
+        // per row instead of on almost every tile; no cross-lane step on the
+        // other tiles. The row sum stays a per-lane partial until the end.
+        // The first tile a wave computes holds key 0 for every query, so
+        // mrow is finite after it.
+        mtop = fmax(mtop, bmax);
+        if (__any(bmax > mrow + kLazyLog2)) {
+          const T mnew = fmax(mrow, group_max(bmax));
+          const T alpha = ex2(mrow - mnew);  // mrow = -inf on the first tile: 0
+          lrow *= alpha;
 #pragma unroll
-      for (int jt = 0; jt < KB / MT; ++jt)
-#pragma unroll
-        for (int i = 0; i < NACC; ++i) {
-          const T p = live ? ex2(sacc[jt][i] - mnew) : T(0);
-          sacc[jt][i] = p;
-          psum += p;
+          for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
+          mrow = mnew;
         }
-      psum = group_sum(psum);
-      lrow = lrow * alpha + psum;
-      mrow = mnew;
-      // rescale the output only when some lane's max moved (alpha == 1
-      // leaves it unchanged bit for bit)
-      if (__any(alpha != T(1))) {
 #pragma unroll
-        for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
+        for (int jt = 0; jt < KB / MT; ++jt)
+#pragma unroll
+          for (int i = 0; i < NACC; ++i) {
+            const T p = ex2(sacc[jt][i] - mrow);
+            sacc[jt][i] = p;
+            lrow += p;
+          }
+      } else {
+        bmax = group_max(bmax);
+        const T mnew = fmax(mrow, bmax);
+        // aligned path: every query sees key 0 in the first tile, so the max is
+        // finite from then on
+        const bool live = FAST || mnew != ninf;
+        const T alpha = live ? ex2(mrow - mnew) : T(1);
+        T psum = T(0);
+#pragma unroll
+        for (int jt = 0; jt < KB / MT; ++jt)
+#pragma unroll
+          for (int i = 0; i < NACC; ++i) {
+            const T p = live ? ex2(sacc[jt][i] - mnew) : T(0);
+            sacc[jt][i] = p;
+            psum += p;
+          }
+        psum = group_sum(psum);
+        lrow = lrow * alpha + psum;
+        mrow = mnew;
+        // rescale the output only when some lane's max moved (alpha == 1
+        // leaves it unchanged bit for bit)
+        if (__any(alpha != T(1))) {
+#pragma unroll
+          for (int dt = 0; dt < DP / MT; ++dt) oacc[dt] *= alpha;
+        }
       }
 #pragma unroll
       for (int jt = 0; jt < KB / MT; ++jt) mma_lds_t_regs<T, DP>(oacc, Vs, jt * MT, sacc[jt], g, c);
@@ -497,8 +531,18 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
     }
     __syncthreads();
   }
+  if constexpr (LAZY) {
+    // the row's sum against the reference max, then (after the output) the
+    // statistics against the true max
+    lrow = group_sum(lrow);
+    mtop = group_max(mtop);
+  }
   T* O = (T*)a.out + b * a.so.b + h * a.so.h;
   store_result<T, DP, QB>(lds, oacc, lrow > T(0) ? T(1) / lrow : T(0), O, a.so.t, q0, Tn, D, wave, g, c);
+  if constexpr (LAZY) {
+    lrow *= ex2(mrow - mtop);
+    mrow = mtop;
+  }
   if (g == 0 && qr < Tn) {
     ((T*)a.rowmax)[(int64_t)bh * Tn + qr] = mrow;
     ((T*)a.rowsum)[(int64_t)bh * Tn + qr] = lrow;
