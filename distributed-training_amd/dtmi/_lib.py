@@ -71,6 +71,8 @@ SIGNATURES: dict[str, list] = {
     "dtmi_softmax_bwd": [i32, vp, vp, vp, i64, i64],
     "dtmi_embedding_fwd": [i32, vp, vp, vp, i64, i64, i64],
     "dtmi_embedding_bwd": [i32, vp, vp, vp, vp, vp, i32, i64, i64, i32],
+    "dtmi_embedding_segments": [vp, i64, vp, vp, vp, vp],
+    "dtmi_embedding_bwd_segs": [i32, vp, vp, vp, vp, vp, vp, i64, i64, i64, i32],
     "dtmi_gemm": [i32, i32, i32, i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, i64, i64, vp, i32, i32],
     "dtmi_set_gemm_math": [i32],
     "dtmi_get_gemm_math": [vp],

@@ -333,9 +333,10 @@ class Indices:
         return Indices(np.where(self.host < 0, self.host + n, self.host))
 
     def segments(self):
+        """The stable sort of the indices by row, built on the device from
+        the uploaded ids once (kernels.embedding_segments)."""
         if self._segs is None:
-            perm, start, row = K.embedding_segments(self.host)
-            self._segs = (dev.from_numpy(perm), dev.from_numpy(start), dev.from_numpy(row))
+            self._segs = K.embedding_segments(self.dev)
         return self._segs
 
 

@@ -391,31 +391,31 @@ def embedding_fwd(weight: DeviceArray, idx_dev: DeviceArray, out_shape) -> Devic
     return out
 
 
-def embedding_segments(idx: np.ndarray):
-    """Stable sort of the host index array: (perm, seg_start, seg_row) int32 arrays
-    such that segment s lists, in increasing order, the positions holding row
-    seg_row[s] -- np.add.at's order of additions."""
-    flat = np.asarray(idx).reshape(-1).astype(np.int64)
-    perm = np.argsort(flat, kind="stable").astype(np.int32)
-    sv = flat[perm]
-    if sv.size:
-        starts = np.flatnonzero(np.r_[True, sv[1:] != sv[:-1]]).astype(np.int32)
-    else:
-        starts = np.zeros(0, np.int32)
-    seg_row = sv[starts].astype(np.int32) if sv.size else np.zeros(0, np.int32)
-    seg_start = np.r_[starts, np.int32(flat.size)].astype(np.int32)
-    return perm, seg_start, seg_row
+def embedding_segments(idx_dev: DeviceArray):
+    """Stable sort of the device index array (int64), on the device:
+    (perm, seg_start, seg_row, nseg) int32 device arrays such that segment
+    s < nseg lists perm[seg_start[s] .. seg_start[s+1]), in increasing
+    order, the positions holding row seg_row[s] -- np.add.at's order of
+    additions. nseg (one element) stays on the device."""
+    _contig(idx_dev)
+    if idx_dev.dtype != np.int64:
+        raise TypeError("embedding_segments: int64 indices expected")
+    n = idx_dev.size
+    perm, seg_row = empty((n,), np.int32), empty((n,), np.int32)
+    seg_start, nseg = empty((n + 1,), np.int32), empty((1,), np.int32)
+    _c("dtmi_embedding_segments", idx_dev.ptr if n else None, n, perm.ptr, seg_start.ptr, seg_row.ptr, nseg.ptr)
+    return perm, seg_start, seg_row, nseg
 
 
 def embedding_bwd(dout: DeviceArray, V: int, segs, out: DeviceArray | None = None) -> DeviceArray:
-    """segs: device int32 arrays (perm, seg_start, seg_row); the [V, C] table
+    """segs: the device arrays of embedding_segments; the [V, C] table
     gradient is written into `out` when given."""
     _contig(dout)
     C_ = dout.shape[-1]
-    perm, seg_start, seg_row = segs
+    perm, seg_start, seg_row, nseg = segs
     dw = _out_or_new(out, (V, C_), dout.dtype, "embedding_bwd")
-    _c("dtmi_embedding_bwd", _dt(dout), dw.ptr, dout.ptr, perm.ptr, seg_start.ptr, seg_row.ptr, seg_row.size, V,
-       C_, 1)
+    _c("dtmi_embedding_bwd_segs", _dt(dout), dw.ptr, dout.ptr, perm.ptr, seg_start.ptr, seg_row.ptr, nseg.ptr,
+       perm.size, V, C_, 1)
     return dw
 
 

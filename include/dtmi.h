@@ -270,6 +270,18 @@ int dtmi_embedding_fwd(int dtype, void* out, const void* weight, const int64_t* 
                        int64_t cols);
 int dtmi_embedding_bwd(int dtype, void* dweight, const void* dout, const int32_t* perm, const int32_t* seg_start,
                        const int32_t* seg_row, int nseg, int64_t vocab, int64_t cols, int zero_fill);
+/* The stable sort behind the backward, on the device (replaces the host-side
+ * np.argsort(idx, kind="stable") of the index array; dtrain's np.add.at order,
+ * dtrain/autograd.py:202). idx: n_idx int64 row ids in device memory; out, all
+ * device memory: perm[n_idx], seg_start[n_idx + 1], seg_row[n_idx] and
+ * nseg[1] (the segment count; seg_start[nseg] = n_idx). Deterministic. */
+int dtmi_embedding_segments(const int64_t* idx, int64_t n_idx, int32_t* perm, int32_t* seg_start, int32_t* seg_row,
+                            int32_t* nseg);
+/* dtmi_embedding_bwd with the segment count read on the device (the output of
+ * dtmi_embedding_segments over n_idx positions). */
+int dtmi_embedding_bwd_segs(int dtype, void* dweight, const void* dout, const int32_t* perm, const int32_t* seg_start,
+                            const int32_t* seg_row, const int32_t* nseg, int64_t n_idx, int64_t vocab, int64_t cols,
+                            int zero_fill);
 
 /* ------------------------------------------------------------ MFMA GEMM
  * C[b] = sum_k A(m,k) B(k,n) (+ bias[n]) (+ C[b] if accumulate), batched.

@@ -168,10 +168,41 @@ def test_embedding_forward_and_bit_exact_scatter_add(dev, dt, V, C, shape):
     didx = D.from_numpy(idx.astype(np.int64).reshape(-1))
     out = K.embedding_fwd(D.from_numpy(w), didx, shape)
     assert bits_equal(out.numpy(), w[idx])
-    perm, start, row = K.embedding_segments(idx)
-    segs = tuple(D.from_numpy(a) for a in (perm, start, row))
+    segs = K.embedding_segments(didx)
+    _check_segments(idx, segs)
     dw = K.embedding_bwd(D.from_numpy(g), V, segs)
     assert bits_equal(dw.numpy(), ops.embedding_bwd(g, (V, C), dt, idx))
+
+
+def _check_segments(idx, segs):
+    """The device sort equals NumPy's stable argsort; segment s covers the
+    positions of row[s] in increasing order (np.add.at's order)."""
+    flat = np.asarray(idx).reshape(-1)
+    perm, start, row, nseg = (x.numpy() for x in segs)
+    order = np.argsort(flat, kind="stable")
+    rows = np.unique(flat)
+    assert nseg[0] == rows.size
+    assert np.array_equal(perm, order)
+    assert np.array_equal(row[:rows.size], rows)
+    first = np.flatnonzero(np.r_[True, flat[order][1:] != flat[order][:-1]])[:rows.size]
+    assert np.array_equal(start[:rows.size + 1], np.r_[first, flat.size])
+
+
+@pytest.mark.parametrize("n,V", [(0, 5), (1, 3), (8191, 50304), (8192, 7), (8193, 50304), (20000, 64),
+                                 (65536, 50304), (100003, 1000)])
+def test_embedding_segments_on_device(dev, n, V):
+    """Chunk sorts of 8192 keys, merge passes (n above 8192, uneven last runs)
+    and the segment scan across 1024-key blocks, against NumPy's stable
+    argsort; then the table gradient bit-equal to np.add.at."""
+    D, K = _dev()
+    rng = np.random.default_rng(n + V)
+    idx = rng.integers(0, V, n)
+    segs = K.embedding_segments(D.from_numpy(idx.astype(np.int64)))
+    _check_segments(idx, segs)
+    if n:
+        g = rng.standard_normal((n, 8)).astype(np.float32)
+        dw = K.embedding_bwd(D.from_numpy(g), V, segs)
+        assert bits_equal(dw.numpy(), ops.embedding_bwd(g, (V, 8), np.float32, idx))
 
 
 def _gemm_ref(a, b, akc, bkc):

@@ -1,11 +1,9 @@
 """Host-side logic of the dtmi package that needs no GPU: DDP bucket layout,
-ZeRO partition, the learning-rate schedule, embedding segment construction and
-the parameter order/init of the model definition (checked without touching
-the device)."""
+ZeRO partition, the learning-rate schedule and the parameter order/init of
+the model definition (checked without touching the device)."""
 import numpy as np
 
 from dtmi.ddp import bucket_layout
-from dtmi.kernels import embedding_segments
 from dtmi.replicas import partition
 from dtmi.train import lr_at
 from oracle import model as OM
@@ -41,22 +39,6 @@ def test_lr_schedule_closed_form():
     assert abs(lr_at(100, lr, 4, 100) - 0.1 * lr) < 1e-18  # and ends at lr / 10
     mid = lr_at(52, lr, 4, 100)
     assert abs(mid - lr * (0.1 + 0.9 * 0.5)) < 1e-15
-
-
-def test_embedding_segments_reproduce_add_at_order():
-    rng = np.random.default_rng(0)
-    idx = rng.integers(0, 7, (5, 9))
-    perm, start, row = embedding_segments(idx)
-    flat = idx.reshape(-1)
-    assert start[0] == 0 and start[-1] == flat.size
-    seen = []
-    for s in range(row.size):
-        pos = perm[start[s]:start[s + 1]]
-        assert np.all(flat[pos] == row[s])
-        assert np.all(np.diff(pos) > 0)  # increasing position order == np.add.at order
-        seen.extend(pos.tolist())
-    assert sorted(seen) == list(range(flat.size))
-    assert list(row) == sorted(set(flat.tolist()))
 
 
 def test_model_parameter_order_matches_dtrain_names():
