@@ -566,23 +566,25 @@ __global__ void __launch_bounds__(256) attn_drow_kernel(AttnArgs a) {
   if (lane == 0) ((T*)a.drow)[row] = s;
 }
 
-// float32 rows of D = 64: 16 lanes per row, one 16-byte vector of O and dO
-// each, 16 rows per 256-thread block.
+// Rows of D = 64: 16 lanes per row, four consecutive elements of O and dO
+// each (one 16-byte vector in float32, two in float64), 16 rows per
+// 256-thread block.
+template <typename T>
 __global__ void __launch_bounds__(256) attn_drow64_kernel(AttnArgs a) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
+  typedef T v4 __attribute__((ext_vector_type(4)));
   const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int q = threadIdx.x & 15;
   const int64_t total = a.B * a.H * a.T;
-  float s = 0.f;
+  T s = T(0);
   if (row < total) {
     const int64_t t = row % a.T, bh = row / a.T, b = bh / a.H, h = bh % a.H;
-    const f4 o = *reinterpret_cast<const f4*>((const float*)a.o + b * a.so.b + h * a.so.h + t * a.so.t + 4 * q);
-    const f4 g = *reinterpret_cast<const f4*>((const float*)a.dO + b * a.sdo.b + h * a.sdo.h + t * a.sdo.t + 4 * q);
+    const v4 o = *reinterpret_cast<const v4*>((const T*)a.o + b * a.so.b + h * a.so.h + t * a.so.t + 4 * q);
+    const v4 g = *reinterpret_cast<const v4*>((const T*)a.dO + b * a.sdo.b + h * a.sdo.h + t * a.sdo.t + 4 * q);
     s = ((o[0] * g[0] + o[1] * g[1]) + o[2] * g[2]) + o[3] * g[3];
   }
 #pragma unroll
   for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
-  if (q == 0 && row < total) ((float*)a.drow)[row] = s;
+  if (q == 0 && row < total) ((T*)a.drow)[row] = s;
 }
 
 // ------------------------------------------------- backward A: dK and dV
@@ -1499,11 +1501,12 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
   {
     // causal-exact FLOP of the 5 backward GEMMs (S recompute, dV, dP, dQ, dK)
     TimedLaunch tl(DTMI_FAM_ATTN_BWD, 5.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
-    const bool drow64 = std::is_same<T, float>::value && a.D == 64 && aligned(a.o, 16) && aligned(a.dO, 16) &&
-                        strides_vec(a.so, 4) && strides_vec(a.sdo, 4);
+    constexpr int VE = 16 / (int)sizeof(T);  // elements per 16-byte vector
+    const bool drow64 = a.D == 64 && aligned(a.o, 16) && aligned(a.dO, 16) && strides_vec(a.so, VE) &&
+                        strides_vec(a.sdo, VE);
     if (drow_in) {
     } else if (drow64) {
-      attn_drow64_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, stream()>>>(a);
+      attn_drow64_kernel<T><<<(unsigned)cdiv(rows, 16), 256, 0, stream()>>>(a);
     } else {
       attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
     }
