@@ -1425,13 +1425,19 @@ static int choose_splits(int64_t tiles, int64_t batch, int64_t K, int64_t cus) {
 // gets a long k range (>= 1024) and the grid covers the CUs, else 128 x 128.
 // The larger tile moves 25 % fewer bytes per MFMA through the loads and LDS
 // but has half the blocks; on the GPT-2 shapes it wins for the long-K
-// products (dW, the vocabulary head's dX and dW) and loses on K = 768.
+// products (dW, the vocabulary head's dX and dW) and loses on K = 768. When
+// the larger tile needs a K split and the smaller one fills whole rounds
+// without one, the smaller one is taken: no partials, no sum pass.
 static void pick_tile(int64_t M, int64_t N, int64_t K, int64_t batch, int64_t cus, int& bm, int& bn) {
   bm = bn = 128;
   if (M < 256) return;
   const int64_t tiles = cdiv(M, 256) * cdiv(N, 128);
   const int sp = choose_splits(tiles, batch, K, cus);
   if (tiles * batch * sp >= cus && K / sp >= 1024) bm = 256;
+  if (bm == 256 && sp > 1) {
+    const int64_t t128 = cdiv(M, 128) * cdiv(N, 128);
+    if (choose_splits(t128, batch, K, cus) == 1 && t128 * batch % cus == 0) bm = 128;
+  }
 }
 
 template <typename T>
