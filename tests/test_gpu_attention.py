@@ -46,6 +46,17 @@ def test_attention_forward_backward(dev, dt, shape):
     _check(D, K, q, k, v, g, dt)
 
 
+@pytest.mark.parametrize("shape", [(1, 2, 16, 64), (2, 3, 208, 64), (3, 2, 512, 64)])
+def test_float64_backward_at_head_dim_64(dev, shape):
+    """float64, D = 64 on the aligned path (64-key blocks of 16 per wave, the
+    dQ pass reading dS; one tile, T not a multiple of 32 or of 64), against
+    the oracle at 1e-12."""
+    D, K = _dev()
+    rng = np.random.default_rng(sum(shape) + 64)
+    q, k, v, g = (rng.standard_normal(shape) for _ in range(4))
+    _check(D, K, q, k, v, g, np.float64)
+
+
 @pytest.mark.parametrize("T", [512, 640, 768, 896, 1024])
 def test_forward_over_many_key_tiles(dev, T):
     """T of 4 to 8 query blocks of 128 on the aligned float32 path, where the
