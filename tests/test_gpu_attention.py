@@ -57,7 +57,7 @@ def test_float64_backward_at_head_dim_64(dev, shape):
     _check(D, K, q, k, v, g, np.float64)
 
 
-@pytest.mark.parametrize("T", [512, 640, 768, 896, 1024])
+@pytest.mark.parametrize("T", [512, 640, 768, 896, 1024, 2048])
 def test_forward_over_many_key_tiles(dev, T):
     """T of 4 to 8 query blocks of 128 on the aligned float32 path, where the
     forward's reference max moves only when a score exceeds it by 2^8: oracle

@@ -282,6 +282,30 @@ def test_gemm_direct_lds_kernel_matches_register_staged_kernel_bitwise(dev, dt, 
     assert bits_equal(aligned_, staged)
 
 
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("akc,bkc", [(True, False), (False, True)])
+def test_batched_gemm_direct_lds_kernel_matches_register_staged_kernel_bitwise(dev, dt, akc, bkc):
+    """Batched products (batch strides of whole matrices, as the attention's
+    wide path uses them): the direct-to-LDS kernel on aligned operands and the
+    register-staged kernel on the same values off alignment give the same
+    bits, split into K ranges or not."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(43)
+    Bt, M, N, K = 3, 136, 200, 520
+    a = rng.standard_normal((Bt, M, K) if akc else (Bt, K, M)).astype(dt)
+    b = rng.standard_normal((Bt, N, K) if bkc else (Bt, K, N)).astype(dt)
+    db = D.from_numpy(b)
+    big = D.empty((a.size + 1,), dt)
+    a_off = big[1:1 + a.size].reshape(*a.shape)
+    a_off.assign(a)
+    ref = _gemm_ref(a.astype(np.float64), b.astype(np.float64), akc, bkc)
+    for splits in (1, 2):
+        aligned_ = K_.gemm(D.from_numpy(a), db, a_kcontig=akc, b_kcontig=bkc, splits=splits).numpy()
+        staged = K_.gemm(a_off, db, a_kcontig=akc, b_kcontig=bkc, splits=splits).numpy()
+        assert rel_err(aligned_, ref) <= TOL[dt]
+        assert bits_equal(aligned_, staged)
+
+
 @pytest.mark.parametrize("akc,bkc", [(True, False), (True, True), (False, False), (False, True)])
 def test_gemm_large_tile_ragged_edges_and_k_tail(dev, akc, bkc):
     """float32 shapes whose k range per block is long enough for the 256 x 128
