@@ -1384,6 +1384,13 @@ struct EpiArgs {
   void* aux = nullptr;
   void* colsum = nullptr;  // column sums of B (length N), unbatched
   int colsum_accumulate = 0;
+  // Split-K partials left for the consumer: when the chooser takes between 2
+  // and parts_max splits, the raw partials go to parts_out ([splits][M][N],
+  // unbatched, no bias or epilogue) with no sum pass and *parts_n = splits;
+  // otherwise C is written as usual and *parts_n = 1.
+  void* parts_out = nullptr;
+  int parts_max = 0;
+  int* parts_n = nullptr;
   // float32 row dots with X per 64-column group (see splitk_rowdot_kernel)
   const void* rowdot_x = nullptr;
   void* rowdot_out = nullptr;
@@ -1491,7 +1498,13 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
   a.k_per_split = kps;
   const size_t es = sizeof(T);
   void* ws = nullptr;
-  if (splits > 1) {
+  // the partials handed to the consumer (see EpiArgs::parts_out)
+  const bool to_parts = ep.parts_out && splits > 1 && splits <= ep.parts_max && batch == 1 && !bias &&
+                        !a.accumulate && a.epi == kEpiNone && !a.addend && !a.colsum && ldc == N;
+  if (ep.parts_n) *ep.parts_n = to_parts ? splits : 1;
+  if (to_parts) {
+    a.ws = ep.parts_out;
+  } else if (splits > 1) {
     const size_t main_bytes = (size_t)splits * batch * M * N * es;
     const size_t cs_bytes = a.colsum ? (size_t)splits * N * es : 0;
     int rc = pool_alloc(&ws, main_bytes + cs_bytes);
@@ -1528,7 +1541,7 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
     } else {
       launch_layout<T, 128, 128>(a, grid, akc, bkc, veca, vecb, dma);
     }
-    if (splits > 1 && !ln_fused) {
+    if (splits > 1 && !ln_fused && !to_parts) {
       int64_t total = batch * M * N;
       int rg = (int)(cdiv(total, 256 * 4) < 8192 ? cdiv(total, 256 * 4) : 8192);
       GemmArgs r = a;
@@ -1697,6 +1710,20 @@ DTMI_EXPORT int dtmi_linear_bwd_dx(int dtype, void* dX, const void* dY, const vo
   DTMI_REQUIRE_INIT();
   // dX[m, k] = sum_n dY[m, n] W[k, n]: A = dY (k-contiguous over n), B(n, k) = W[k, n] (k-contiguous)
   return gemm_dispatch(dtype, 1, 1, M, K, N, dY, N, 0, W, N, 0, dX, K, 0, 1, nullptr, accumulate, 0);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_linear_bwd_dx_parts(int dtype, void* parts, int max_parts, int* nparts, const void* dY,
+                                         const void* W, int64_t M, int64_t K, int64_t N) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_CHECK(parts && nparts && max_parts >= 1, "dtmi_linear_bwd_dx_parts: NULL parts / nparts or max_parts < 1");
+  EpiArgs ep;
+  ep.parts_out = parts;
+  ep.parts_max = max_parts;
+  ep.parts_n = nparts;
+  *nparts = 1;
+  return gemm_dispatch(dtype, 1, 1, M, K, N, dY, N, 0, W, N, 0, parts, K, 0, 1, nullptr, 0, 0, ep);
   DTMI_BODY_END
 }
 

@@ -43,6 +43,17 @@ __global__ void __launch_bounds__(256) ln_fwd_kernel(T* __restrict__ y, T* __res
   ln_row_fwd<T, NV, VW>(xv, cols, lane, w, b, eps, y + row * cols, mean_out + row, rstd_out + row);
 }
 
+// out = ((p_0 + p_1) + ...) + p_{n-1}, elementwise, parts `stride` apart.
+template <typename T>
+__global__ void __launch_bounds__(256) sum_parts_kernel(T* __restrict__ out, const T* __restrict__ parts,
+                                                         int64_t stride, int n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < stride; i += (int64_t)gridDim.x * 256) {
+    T v = parts[i];
+    for (int p = 1; p < n; ++p) v = v + parts[(int64_t)p * stride + i];
+    out[i] = v;
+  }
+}
+
 // Blocks needed for the deterministic column partials: a function of rows only.
 static int ln_bwd_blocks(int64_t rows) {
   int64_t b = cdiv(rows, 4 * 2);  // two rows per wave
@@ -50,13 +61,16 @@ static int ln_bwd_blocks(int64_t rows) {
   return (int)(b < 512 ? b : 512);
 }
 
-template <typename T, int NV, int VW>
+// NP > 1: dy is the in-order sum of NP split-K partials of the product that
+// made it, part p at dy + p * pstride (((p0 + p1) + ...), the sum pass's
+// order), summed here as the rows are loaded instead of in a pass of its own.
+template <typename T, int NV, int VW, int NP = 1>
 __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __restrict__ part_dw,
                                                       T* __restrict__ part_db, const T* __restrict__ dy,
                                                       const T* __restrict__ x, const T* __restrict__ w,
                                                       const T* __restrict__ mean, const T* __restrict__ rstd,
                                                       const T* __restrict__ addend, int64_t rows, int cols,
-                                                      int accumulate_dx) {
+                                                      int accumulate_dx, int64_t pstride = 0) {
   extern __shared__ unsigned char lds_raw[];
   T* lds = reinterpret_cast<T*>(lds_raw);  // [4 waves][2][NV*VW*64]
   const int lane = threadIdx.x & 63;
@@ -82,10 +96,11 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
   // is used instead (a second row set would spill). The arithmetic per row is
   // the same.
   constexpr bool PF = NV <= 8;
+  static_assert(NP == 1 || PF, "split-K partials: rows of up to 8 vectors per lane");
   // what dx adds to: the existing dx, or the addend (a row's own rows only,
   // so the next row's are read ahead of this row's store)
   const T* base = accumulate_dx ? dx : addend;
-  T gn[NV][VW], xn[NV][VW], an[NV][VW];
+  T gn[NP][NV][VW], xn[NV][VW], an[NV][VW];
   T mun = T(0), rsn = T(0);
   int64_t row = (int64_t)blockIdx.x * 4 + wave;
   auto load_row = [&](int64_t r) {
@@ -95,7 +110,8 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
     for (int j = 0; j < NV; ++j) {
       const int c = VW * lane + 64 * VW * j;
       if (c < cols) {
-        load_vec<T, VW>(gn[j], dy + r * cols + c);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) load_vec<T, VW>(gn[p][j], dy + p * pstride + r * cols + c);
         load_vec<T, VW>(xn[j], x + r * cols + c);
         if (base) load_vec<T, VW>(an[j], base + r * cols + c);
       }
@@ -112,7 +128,10 @@ __global__ void __launch_bounds__(256) ln_bwd_kernel(T* __restrict__ dx, T* __re
       for (int j = 0; j < NV; ++j)
 #pragma unroll
         for (int e = 0; e < VW; ++e) {
-          gv[j][e] = gn[j][e];
+          T v = gn[0][j][e];
+#pragma unroll
+          for (int p = 1; p < NP; ++p) v = v + gn[p][j][e];
+          gv[j][e] = v;
           xh[j][e] = xn[j][e];
           av[j][e] = an[j][e];
         }
@@ -308,6 +327,16 @@ struct LnDispatch {
     size_t lds = (size_t)4 * 2 * NV * VW * 64 * sizeof(T);
     ln_bwd_kernel<T, NV, VW><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, add, rows, cols, acc);
   }
+  // dy as two split-K partials (rows of up to 8 vectors per lane)
+  template <int NV>
+  static void bwd2(int grid, T* dx, T* pdw, T* pdb, const T* dy, int64_t pstride, const T* x, const T* w,
+                   const T* mu, const T* rs, const T* add, int64_t rows, int cols, int acc) {
+    if constexpr (NV <= 8) {
+      size_t lds = (size_t)4 * 2 * NV * VW * 64 * sizeof(T);
+      ln_bwd_kernel<T, NV, VW, 2><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, add, rows, cols, acc,
+                                                               pstride);
+    }
+  }
 };
 
 template <typename T>
@@ -349,13 +378,50 @@ static int ln_fwd(void* y, void* mean, void* rstd, const void* x, const void* w,
 template <typename T>
 static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, const void* w, const void* mean,
                   const void* rstd, const void* addend, int64_t rows, int64_t cols, int accumulate,
-                  void* scratch_ptr = nullptr, size_t scratch_bytes = 0) {
+                  void* scratch_ptr = nullptr, size_t scratch_bytes = 0, int nparts = 1) {
   constexpr int VWV = 16 / sizeof(T);
   bool vec = cols % VWV == 0 && aligned(x, 16) && aligned(dy, 16) && aligned(dx, 16) && aligned(w, 16) &&
              aligned(addend, 16);
   int vw = vec ? VWV : 1;
   const int nv = ln_pick_nv(cdiv(cols, 64LL * vw));
   const bool wide = nv < 0;  // longer rows than a wave holds
+  if (nparts > 1) {
+    // dy as split-K partials: summed in the kernel's loads (two partials,
+    // aligned rows of up to 8 vectors per lane), else by a sum pass first
+    const int64_t pstride = rows * cols;
+    if (nparts == 2 && vec && nv > 0 && nv <= 8 && (pstride * (int64_t)sizeof(T)) % 16 == 0) {
+      const int grid = ln_bwd_blocks(rows);
+      void* parts = nullptr;
+      int rc = pool_alloc(&parts, (size_t)2 * grid * cols * sizeof(T));
+      if (rc) return rc;
+      T* pdw = (T*)parts;
+      T* pdb = pdw + (size_t)grid * cols;
+      {
+        const double arrays = (addend || (accumulate & 1)) ? 5.0 : 4.0;
+        TimedLaunch tl(DTMI_FAM_LN_BWD, (double)rows * cols * arrays * sizeof(T));
+        const int c = (int)cols;
+        const int acc = (accumulate & 1) ? 1 : 0;
+#define CALLP(NV)                                                                                        \
+  LnDispatch<T, VWV>::template bwd2<NV>(grid, (T*)dx, pdw, pdb, (const T*)dy, pstride, (const T*)x, (const T*)w, \
+                                        (const T*)mean, (const T*)rstd, (const T*)addend, rows, c, acc)
+        LN_NV_SWITCH(nv, CALLP)
+#undef CALLP
+        launch_colreduce<T>((T*)dw, pdw, grid, cols, (accumulate & 2) ? 1 : 0, (T*)db, pdb);
+      }
+      hipError_t le = hipGetLastError();
+      pool_free(parts);
+      if (le != hipSuccess) return fail_hip(le, "ln_bwd kernels", __FILE__, __LINE__);
+      return DTMI_OK;
+    }
+    void* sum = nullptr;
+    int rc = pool_alloc(&sum, (size_t)pstride * sizeof(T));
+    if (rc) return rc;
+    const int64_t g = cdiv(pstride, 256LL) < 8192 ? cdiv(pstride, 256LL) : 8192;
+    sum_parts_kernel<T><<<(unsigned)g, 256, 0, stream()>>>((T*)sum, (const T*)dy, pstride, nparts);
+    rc = ln_bwd<T>(dx, dw, db, sum, x, w, mean, rstd, addend, rows, cols, accumulate);
+    pool_free(sum);
+    return rc;
+  }
   const int grid = wide ? ln_bwd_wide_blocks(rows, cols, sizeof(T)) : ln_bwd_blocks(rows);
   const size_t part_bytes = (size_t)2 * grid * cols * sizeof(T);
   void* parts = scratch_ptr;
@@ -457,6 +523,41 @@ DTMI_EXPORT int dtmi_layernorm_bwd(int dtype, void* dx, void* dw, void* db, cons
   DTMI_CHECK(dx && dy && x && w && mean && rstd, "dtmi_layernorm_bwd: NULL pointer");
   if (dtype == DTMI_F32) return ln_bwd<float>(dx, dw, db, dy, x, w, mean, rstd, nullptr, rows, cols, accumulate);
   return ln_bwd<double>(dx, dw, db, dy, x, w, mean, rstd, nullptr, rows, cols, accumulate);
+  DTMI_BODY_END
+}
+
+DTMI_EXPORT int dtmi_layernorm_bwd_parts(int dtype, void* dx, void* dw, void* db, const void* dy_parts, int nparts,
+                                         const void* x, const void* w, const void* mean, const void* rstd,
+                                         const void* dx_addend, int64_t rows, int64_t cols, int accumulate) {
+  DTMI_BODY_BEGIN
+  DTMI_REQUIRE_INIT();
+  DTMI_DTYPE_OK(dtype);
+  DTMI_CHECK(rows >= 0 && cols > 0 && cols < (1 << 30) && nparts >= 1 && nparts <= 64,
+             "dtmi_layernorm_bwd_parts: bad shape [%lld, %lld] or part count %d", (long long)rows, (long long)cols,
+             nparts);
+  DTMI_CHECK(dw && db, "dtmi_layernorm_bwd_parts: NULL dgamma/dbeta");
+  DTMI_CHECK(!(dx_addend && (accumulate & 1)), "dtmi_layernorm_bwd_parts: an addend and accumulate bit 0 together");
+  if (rows == 0) {
+    if (accumulate & 2) return DTMI_OK;
+    int rc = dtmi_fill(dtype, dw, 0.0, cols);
+    return rc ? rc : dtmi_fill(dtype, db, 0.0, cols);
+  }
+  DTMI_CHECK(dx && dy_parts && x && w && mean && rstd, "dtmi_layernorm_bwd_parts: NULL pointer");
+  {
+    // dx is written while other waves still read rows of the partials and
+    // the addend: the byte ranges must be disjoint
+    const size_t bytes = (size_t)rows * (size_t)cols * (dtype == DTMI_F32 ? 4 : 8);
+    const uintptr_t d0 = (uintptr_t)dx, p0 = (uintptr_t)dy_parts;
+    DTMI_CHECK(p0 + bytes * (size_t)nparts <= d0 || d0 + bytes <= p0, "dtmi_layernorm_bwd_parts: the partials overlap dx");
+    if (dx_addend) {
+      const uintptr_t a0 = (uintptr_t)dx_addend;
+      DTMI_CHECK(a0 + bytes <= d0 || d0 + bytes <= a0, "dtmi_layernorm_bwd_parts: the addend overlaps dx");
+    }
+  }
+  if (dtype == DTMI_F32)
+    return ln_bwd<float>(dx, dw, db, dy_parts, x, w, mean, rstd, dx_addend, rows, cols, accumulate, nullptr, 0,
+                         nparts);
+  return ln_bwd<double>(dx, dw, db, dy_parts, x, w, mean, rstd, dx_addend, rows, cols, accumulate, nullptr, 0, nparts);
   DTMI_BODY_END
 }
 

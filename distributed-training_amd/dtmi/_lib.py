@@ -63,6 +63,8 @@ SIGNATURES: dict[str, list] = {
     "dtmi_layernorm_fwd": [i32, vp, vp, vp, vp, vp, vp, i64, i64, f64],
     "dtmi_layernorm_bwd": [i32, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
     "dtmi_layernorm_bwd_add": [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
+    "dtmi_layernorm_bwd_parts": [i32, vp, vp, vp, vp, i32, vp, vp, vp, vp, vp, i64, i64, i32],
+    "dtmi_linear_bwd_dx_parts": [i32, vp, i32, C.POINTER(C.c_int), vp, vp, i64, i64, i64],
     "dtmi_layernorm_bwd_noalloc": [i32, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, i32],
     "dtmi_xent_fwd": [i32, vp, vp, vp, vp, vp, i64, i64],
     "dtmi_xent_bwd": [i32, vp, vp, vp, vp, vp, vp, f64, i64, i64],

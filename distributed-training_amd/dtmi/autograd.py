@@ -74,7 +74,7 @@ def _broadcast_to(g: DeviceArray, shape) -> DeviceArray:
 
 class Tensor:
     __slots__ = ("data", "grad", "requires_grad", "_parents", "_backward", "_hooks", "name", "grad_dest",
-                 "_dest_live", "_ln_pre", "_rowdot", "__weakref__")
+                 "_dest_live", "_ln_pre", "_rowdot", "_ln_out", "__weakref__")
 
     def __init__(self, data, requires_grad=False, _parents=(), _backward=None, name=None):
         self.data = data if isinstance(data, DeviceArray) else dev.asarray(np.asarray(data))
@@ -93,6 +93,10 @@ class Tensor:
         # (w, b, eps, y, mean, rstd); layer_norm(self, w, b, eps) takes it once.
         self._ln_pre = None
         self._rowdot = None
+        # the output of layer_norm: the backward of the product that reads it
+        # may hand its gradient over as split-K partials (kernels.SplitSum),
+        # which the LayerNorm backward adds as it loads them
+        self._ln_out = False
 
     # ------------------------------------------------------------ utilities
     @property
@@ -247,6 +251,8 @@ class Tensor:
                 if g is None:
                     continue
                 if node._backward is None:
+                    if isinstance(g, K.SplitSum):
+                        g = g.value()
                     if node.requires_grad:
                         node._dest_live = None
                         if node.grad is None:
@@ -270,6 +276,10 @@ class Tensor:
         # already has a pending gradient P, f(g, P) returns the parents'
         # gradients with P already added into parent i's (P + its own, the
         # order of the sum below), or None to decline.
+        # a gradient left as split-K partials goes on as it is only to a
+        # backward that takes it (the LayerNorm's); any other gets its value
+        if isinstance(g, K.SplitSum) and not getattr(node._backward, "takes_split_sum", False):
+            g = g.value()
         outs, summed = None, -1
         fuse = getattr(node._backward, "with_addend", None)
         if fuse is not None:
@@ -289,7 +299,8 @@ class Tensor:
             if j == summed or k not in grads:
                 grads[k] = pg
             else:
-                grads[k] = K.binary("add", grads[k], pg)
+                a = grads[k].value() if isinstance(grads[k], K.SplitSum) else grads[k]
+                grads[k] = K.binary("add", a, pg.value() if isinstance(pg, K.SplitSum) else pg)
 
 
 def grad_out(t: Tensor):
@@ -370,17 +381,22 @@ def layer_norm(x: Tensor, w: Tensor, b: Tensor, eps=1e-5) -> Tensor:
         y, mean, rstd = K.layernorm_fwd(xd, _contig(w.data), _contig(b.data), eps)
 
     def bw(g, dx_addend=None):
-        return K.layernorm_bwd(_contig(g), xd, _contig(w.data), mean, rstd, dw_out=grad_out(w), db_out=grad_out(b),
-                               dx_addend=dx_addend)
+        # g may be a kernels.SplitSum (the producer's split-K partials)
+        return K.layernorm_bwd(g if isinstance(g, K.SplitSum) else _contig(g), xd, _contig(w.data), mean, rstd,
+                               dw_out=grad_out(w), db_out=grad_out(b), dx_addend=dx_addend)
 
     def bw_add(g, pending):
         # x already has a pending gradient (the residual path): the kernel
         # writes pending + dx, the engine's own sum, in the same pass
-        if not pending.is_contiguous or pending.dtype != xd.dtype or pending.shape != xd.shape:
+        if isinstance(pending, K.SplitSum) or not pending.is_contiguous or pending.dtype != xd.dtype or \
+                pending.shape != xd.shape:
             return None
         return bw(g, dx_addend=pending)
     bw.with_addend = (0, bw_add)
-    return Tensor._make(y, (x, w, b), bw)
+    bw.takes_split_sum = True
+    t = Tensor._make(y, (x, w, b), bw)
+    t._ln_out = True
+    return t
 
 
 def causal_attention(q: Tensor, k: Tensor, v: Tensor) -> Tensor:

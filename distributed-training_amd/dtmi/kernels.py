@@ -291,11 +291,32 @@ def _out_or_new(out, shape, dtype, what):
     return out
 
 
-def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceArray, rstd: DeviceArray,
+class SplitSum:
+    """A gradient left as the split-K partials of the product that made it:
+    its value is ((parts[0] + parts[1]) + ...), elementwise, of shape `shape`
+    (the sum pass's order). layernorm_bwd takes it as it is and adds the parts
+    while it loads the rows; value() forms the array for anything else."""
+
+    __slots__ = ("parts", "n", "shape", "dtype")
+
+    def __init__(self, parts: DeviceArray, n: int, shape):
+        self.parts, self.n, self.shape, self.dtype = parts, int(n), tuple(shape), parts.dtype
+
+    def value(self) -> DeviceArray:
+        v = self.parts[0]
+        for i in range(1, self.n):
+            v = binary("add", v, self.parts[i])
+        return v.reshape(*self.shape)
+
+
+def layernorm_bwd(dy, x: DeviceArray, w: DeviceArray, mean: DeviceArray, rstd: DeviceArray,
                   dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None,
                   dx_addend: DeviceArray | None = None):
     """Returns (dx, dw, db); dw / db are written into dw_out / db_out when given.
-    With dx_addend, dx = dx_addend + the input gradient (a new array)."""
+    With dx_addend, dx = dx_addend + the input gradient (a new array). dy may
+    be a SplitSum: its partials are added in the same pass."""
+    if isinstance(dy, SplitSum):
+        return _layernorm_bwd_parts(dy, x, w, mean, rstd, dw_out, db_out, dx_addend)
     _contig(dy, x, w, mean, rstd)
     if dy.shape != x.shape:
         raise ValueError("layernorm_bwd: dy/x shape mismatch")
@@ -315,6 +336,26 @@ def layernorm_bwd(dy: DeviceArray, x: DeviceArray, w: DeviceArray, mean: DeviceA
             raise ValueError("layernorm_bwd: dx_addend must match x in shape and dtype")
         _c("dtmi_layernorm_bwd_add", _dt(dy, x, w, mean, rstd, dx_addend), dx.ptr, dw.ptr, db.ptr, dy.ptr, x.ptr,
            w.ptr, mean.ptr, rstd.ptr, dx_addend.ptr, rows, C_, 0)
+    return dx, dw, db
+
+
+def _layernorm_bwd_parts(dy: SplitSum, x, w, mean, rstd, dw_out, db_out, dx_addend):
+    _contig(dy.parts, x, w, mean, rstd)
+    if dy.shape != x.shape or dy.dtype != x.dtype:
+        raise ValueError("layernorm_bwd: dy/x shape mismatch")
+    C_ = x.shape[-1]
+    rows = x.size // C_
+    if mean.size != rows or rstd.size != rows:
+        raise ValueError("layernorm_bwd: bad row statistics")
+    dx = empty(x.shape, x.dtype)
+    dw = _out_or_new(dw_out, (C_,), x.dtype, "layernorm_bwd")
+    db = _out_or_new(db_out, (C_,), x.dtype, "layernorm_bwd")
+    if dx_addend is not None:
+        _contig(dx_addend)
+        if dx_addend.shape != x.shape or dx_addend.dtype != x.dtype:
+            raise ValueError("layernorm_bwd: dx_addend must match x in shape and dtype")
+    _c("dtmi_layernorm_bwd_parts", _dt(dy.parts, x, w, mean, rstd), dx.ptr, dw.ptr, db.ptr, dy.parts.ptr, dy.n, x.ptr,
+       w.ptr, mean.ptr, rstd.ptr, dx_addend.ptr if dx_addend is not None else None, rows, C_, 0)
     return dx, dw, db
 
 
@@ -514,13 +555,16 @@ def linear_fwd_ln(x2: DeviceArray, w: DeviceArray, b: DeviceArray | None, residu
 
 def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, need_db=True,
                dw_out: DeviceArray | None = None, db_out: DeviceArray | None = None,
-               gelu_pre: DeviceArray | None = None, rowdot: DeviceArray | None = None, rowdot_t: int = 1):
+               gelu_pre: DeviceArray | None = None, rowdot: DeviceArray | None = None, rowdot_t: int = 1,
+               dx_parts: int = 0):
     """Returns (dx, dw, db) for y = x @ w + b with x [M, K], w [K, N]; dw / db
     are written into dw_out / db_out when given. With gelu_pre (the [M, K]
     pre-activation whose GELU is x), dx is the gradient of that pre-activation.
     With rowdot (float32 [M / rowdot_t * K / 64 * rowdot_t]): also the per-64-
     column row dots of dx with x, laid out [B, K / 64, T] for rows m = b T + t
-    (the attention backward's rowsum(dO * O) when x is the attention output)."""
+    (the attention backward's rowsum(dO * O) when x is the attention output).
+    With dx_parts = n > 1, dx may come back as a SplitSum of up to n split-K
+    partials instead of summed (when the product is split in 2..n)."""
     _contig(x2, w, dy2)
     M, K = x2.shape
     N = w.shape[1]
@@ -529,7 +573,7 @@ def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, 
     dt = _dt(x2, w, dy2)
     dx = None
     if need_dx:
-        dx = empty((M, K), x2.dtype)
+        dx = empty((M, K), x2.dtype) if dx_parts <= 1 or gelu_pre is not None or rowdot is not None else None
         if gelu_pre is not None:
             _contig(gelu_pre)
             if gelu_pre.shape != (M, K):
@@ -540,6 +584,11 @@ def linear_bwd(x2: DeviceArray, w: DeviceArray, dy2: DeviceArray, need_dx=True, 
             if rowdot.dtype != x2.dtype or rowdot.size != M * (K // 64):
                 raise ValueError("linear_bwd: rowdot must hold M * K / 64 values of x's dtype")
             _c("dtmi_linear_bwd_dx_rowdot", dt, dx.ptr, dy2.ptr, w.ptr, x2.ptr, rowdot.ptr, M, K, N, int(rowdot_t))
+        elif dx_parts > 1:
+            parts = empty((int(dx_parts), M, K), x2.dtype)
+            n = C.c_int(1)
+            _c("dtmi_linear_bwd_dx_parts", dt, parts.ptr, int(dx_parts), C.byref(n), dy2.ptr, w.ptr, M, K, N)
+            dx = SplitSum(parts, n.value, (M, K)) if n.value > 1 else parts[0]
         else:
             _c("dtmi_linear_bwd_dx", dt, dx.ptr, dy2.ptr, w.ptr, M, K, N, 0)
     dw = _out_or_new(dw_out, (K, N), x2.dtype, "linear_bwd")

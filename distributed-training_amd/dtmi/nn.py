@@ -117,10 +117,12 @@ def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = Non
         rs = None
         if x._rowdot is not None and x.requires_grad:
             rs = dev.empty((X.shape[0] * x._rowdot * X.shape[1],), X.dtype)
+        # x is a LayerNorm output: its backward adds dx's split-K partials itself
+        parts = 2 if LN_SPLIT_SUM and x._ln_out and rs is None else 0
         dx, dw, db = K.linear_bwd(X2, W, g2, need_dx=x.requires_grad, need_db=b is not None, dw_out=grad_out(w),
                                   db_out=grad_out(b) if b is not None else None, rowdot=rs,
-                                  rowdot_t=X.shape[1] if rs is not None else 1)
-        out = [dx.reshape(X.shape) if dx is not None else None, dw]
+                                  rowdot_t=X.shape[1] if rs is not None else 1, dx_parts=parts)
+        out = [_shaped(dx, X.shape), dw]
         if rs is not None:
             _ROWSUMS[out[0]] = rs
         if b is not None:
@@ -132,6 +134,22 @@ def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = Non
     t = Tensor._make(y, tuple(parents), bw)
     t._ln_pre = pre
     return t
+
+
+# The qkv and fc products read LayerNorm outputs: their input gradient goes
+# to the LayerNorm backward as split-K partials (kernels.SplitSum) when the
+# product is split in two, and that backward adds them while it loads its
+# rows (the same bits as summing first). False sums them in a pass of their own.
+LN_SPLIT_SUM = True
+
+
+def _shaped(dx, shape):
+    """dx (an array or a kernels.SplitSum, or None) as a gradient of `shape`."""
+    if dx is None:
+        return None
+    if isinstance(dx, K.SplitSum):
+        return K.SplitSum(dx.parts, dx.n, shape)
+    return dx.reshape(shape)
 
 
 def mlp(x: Tensor, fc: "Linear", out: "Linear", residual: Tensor, ln: "LayerNorm | None" = None) -> Tensor:
@@ -154,8 +172,9 @@ def mlp(x: Tensor, fc: "Linear", out: "Linear", residual: Tensor, ln: "LayerNorm
         dh, dwo, dbo = K.linear_bwd(act, Wo, g2, need_dx=True, need_db=bo is not None, dw_out=grad_out(out.w),
                                     db_out=grad_out(bo) if bo is not None else None, gelu_pre=h)
         dx, dwf, dbf = K.linear_bwd(X2, Wf, dh, need_dx=x.requires_grad, need_db=bf is not None,
-                                    dw_out=grad_out(fc.w), db_out=grad_out(bf) if bf is not None else None)
-        res = [dx.reshape(X.shape) if dx is not None else None, dwf]
+                                    dw_out=grad_out(fc.w), db_out=grad_out(bf) if bf is not None else None,
+                                    dx_parts=2 if LN_SPLIT_SUM and x._ln_out else 0)
+        res = [_shaped(dx, X.shape), dwf]
         if bf is not None:
             res.append(dbf)
         res.append(dwo)

@@ -221,6 +221,15 @@ int dtmi_layernorm_bwd(int dtype, void* dx, void* dw, void* db, const void* dy, 
 int dtmi_layernorm_bwd_add(int dtype, void* dx, void* dw, void* db, const void* dy, const void* x, const void* w,
                            const void* mean, const void* rstd, const void* dx_addend, int64_t rows, int64_t cols,
                            int accumulate);
+/* dtmi_layernorm_bwd / _add with dy given as the nparts split-K partials of
+ * the product that made it (dy_parts: nparts contiguous [rows, cols] arrays,
+ * as dtmi_linear_bwd_dx_parts leaves them): dy = ((p0 + p1) + ...) in the
+ * split-K sum's order, added as the rows are loaded, so the results equal
+ * summing first and calling dtmi_layernorm_bwd(_add). dx_addend may be NULL;
+ * it and the partials must not overlap dx. dtrain/autograd.py:216-222. */
+int dtmi_layernorm_bwd_parts(int dtype, void* dx, void* dw, void* db, const void* dy_parts, int nparts, const void* x,
+                             const void* w, const void* mean, const void* rstd, const void* dx_addend, int64_t rows,
+                             int64_t cols, int accumulate);
 /* dtmi_layernorm_bwd that allocates nothing. No counterpart in dtrain: it is
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
@@ -356,6 +365,13 @@ int dtmi_linear_bwd_dx_gelu(int dtype, void* dX, const void* dY, const void* W, 
  * aligned, K % 64 == 0, M % T == 0. */
 int dtmi_linear_bwd_dx_rowdot(int dtype, void* dX, const void* dY, const void* W, const void* X, void* rowdot,
                               int64_t M, int64_t K, int64_t N, int64_t T);
+/* dtmi_linear_bwd_dx (dX = dY W^T, [M, K]) for a consumer that adds split-K
+ * partials itself: when the product is split in s, 2 <= s <= max_parts, the s
+ * raw partials are written to parts ([s][M][K]) and *nparts = s (a host
+ * pointer); otherwise the finished dX is written to parts[0] and *nparts = 1.
+ * parts holds max_parts * M * K elements. dtrain/autograd.py:106. */
+int dtmi_linear_bwd_dx_parts(int dtype, void* parts, int max_parts, int* nparts, const void* dY, const void* W,
+                             int64_t M, int64_t K, int64_t N);
 
 /* ------------------------------------------------------- causal attention
  * dtrain/autograd.py:226-247: o = softmax(q k^T * scale + causal mask) v over

@@ -155,3 +155,30 @@ def test_vocabulary_head_gemms_at_gpt2_small_shape(dev):
     gx, gw = ops.matmul_bwd(dy, h, w)
     assert rel_err(dx.numpy(), gx) <= 1e-5
     assert rel_err(dw.numpy(), gw) <= 1e-5
+
+
+def test_layernorm_backward_taking_split_k_partials_changes_no_bit(dev):
+    """8 x 1024 tokens at GPT-2 width (2 layers, vocabulary 65): the qkv and fc
+    input gradients split in two and handed to the LayerNorm backwards as
+    partials give every parameter gradient and the loss bit for bit as
+    summing the partials first."""
+    D, K, N, O, P, R, S = _api()
+    cfg = dict(vocab=65, ctx=1024, dim=768, heads=12, layers=2)
+    oc = OM.GPTConfig(dtype="float32", **cfg)
+    weights = OM.synthetic_init(oc, seed=7)
+    xs, ys = OM.synthetic_tokens(oc, batch=8, seed=7, replicas=1)
+    out = {}
+    for split in (True, False):
+        N.LN_SPLIT_SUM = split
+        try:
+            m = N.GPT(N.GPTConfig(dtype="float32", **cfg), seed=7)
+            m.load_numpy(weights)
+            m.zero_grad()
+            _, loss = m(xs[0], ys[0])
+            loss.backward()
+            out[split] = (loss.numpy(), [p.grad.numpy() for p in m.parameters()])
+        finally:
+            N.LN_SPLIT_SUM = True
+    assert bits_equal(out[True][0], out[False][0])
+    for a, b in zip(out[True][1], out[False][1]):
+        assert bits_equal(a, b)

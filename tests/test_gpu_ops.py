@@ -394,6 +394,57 @@ def test_linear_forward_backward_at_layernorm_linear_workload(dev, dt):
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("K,N", [(768, 2304), (768, 3072)])
+def test_layernorm_backward_adds_the_split_k_partials_of_dy(dev, dt, K, N):
+    """The qkv / fc input gradient ([8192, 768] = dY W^T over N = 2304 or
+    3072) left as split-K partials and summed inside the LayerNorm backward:
+    the same bits as summing first (dtmi_linear_bwd_dx) and then
+    dtmi_layernorm_bwd, with and without the residual addend; and the
+    partials' value equal to the summed product."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(K + N)
+    M = 8192
+    x = D.from_numpy(rng.standard_normal((M, K)).astype(dt))
+    lw = D.from_numpy((1 + 0.01 * rng.standard_normal(K)).astype(dt))
+    lb = D.from_numpy((0.01 * rng.standard_normal(K)).astype(dt))
+    W = D.from_numpy((rng.standard_normal((K, N)) * 0.02).astype(dt))
+    dY = D.from_numpy(rng.standard_normal((M, N)).astype(dt))
+    pend = D.from_numpy(rng.standard_normal((M, K)).astype(dt))
+    h, mean, rstd = K_.layernorm_fwd(x, lw, lb)
+    dh, _, _ = K_.linear_bwd(h, W, dY, need_db=False)
+    dsplit, _, _ = K_.linear_bwd(h, W, dY, need_db=False, dx_parts=2)
+    if dt == np.float32:
+        assert isinstance(dsplit, K_.SplitSum) and dsplit.n == 2
+    val = dsplit.value() if isinstance(dsplit, K_.SplitSum) else dsplit
+    assert bits_equal(val.numpy(), dh.numpy())
+    for addend in (None, pend):
+        ref = K_.layernorm_bwd(dh, x, lw, mean, rstd, dx_addend=addend)
+        got = K_.layernorm_bwd(dsplit, x, lw, mean, rstd, dx_addend=addend)
+        for r, g_ in zip(ref, got):
+            assert bits_equal(g_.numpy(), r.numpy())
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
+@pytest.mark.parametrize("rows,C,n", [(4096, 768, 3), (33, 1000, 2), (9, 5000, 2), (64, 768, 4)])
+def test_layernorm_backward_partials_outside_the_fused_load(dev, dt, rows, C, n):
+    """dtmi_layernorm_bwd_parts where the partials are summed by a pass of
+    their own first (more than two parts, unaligned rows, rows longer than 8
+    vectors per lane): the bits of summing in order and dtmi_layernorm_bwd."""
+    D, K_ = _dev()
+    rng = np.random.default_rng(rows + C + n)
+    x = D.from_numpy(rng.standard_normal((rows, C)).astype(dt))
+    lw = D.from_numpy((1 + 0.01 * rng.standard_normal(C)).astype(dt))
+    lb = D.from_numpy((0.01 * rng.standard_normal(C)).astype(dt))
+    parts = D.from_numpy(rng.standard_normal((n, rows, C)).astype(dt))
+    _, mean, rstd = K_.layernorm_fwd(x, lw, lb)
+    s = K_.SplitSum(parts, n, (rows, C))
+    ref = K_.layernorm_bwd(s.value(), x, lw, mean, rstd)
+    got = K_.layernorm_bwd(s, x, lw, mean, rstd)
+    for r, g_ in zip(ref, got):
+        assert bits_equal(g_.numpy(), r.numpy())
+
+
+@pytest.mark.parametrize("dt", [np.float64, np.float32])
 @pytest.mark.parametrize("M,K,N", [(1024, 256, 512), (256, 4096, 96), (300, 68, 132), (2048, 2048, 2048),
                                    (4096, 1024, 2048)])
 def test_fused_linear_epilogues_equal_the_unfused_ops(dev, dt, M, K, N):
