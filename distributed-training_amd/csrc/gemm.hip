@@ -1229,8 +1229,12 @@ __global__ void __launch_bounds__(256) splitk_rowdot_kernel(GemmArgs a, const fl
   float* C = (float*)a.C;
   for (int64_t iv = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; iv < nvec; iv += stride) {
     const int64_t idx = iv * 4;
+    // X and the first two partials in flight together
+    const f4 o = *reinterpret_cast<const f4*>(X + idx);
     f4 v = *reinterpret_cast<const f4*>(ws + idx);
-    int s = 1;
+    const f4 p1 = *reinterpret_cast<const f4*>(ws + total + idx);  // splits >= 2
+    v = v + p1;
+    int s = 2;
     for (; s + 3 < splits; s += 4) {
       f4 t[4];
 #pragma unroll
@@ -1240,7 +1244,6 @@ __global__ void __launch_bounds__(256) splitk_rowdot_kernel(GemmArgs a, const fl
     }
     for (; s < splits; ++s) v = v + *reinterpret_cast<const f4*>(ws + (int64_t)s * total + idx);
     *reinterpret_cast<f4*>(C + idx) = v;
-    const f4 o = *reinterpret_cast<const f4*>(X + idx);
     rowdot_group(((o[0] * v[0] + o[1] * v[1]) + o[2] * v[2]) + o[3] * v[3], idx, N, T, rowdot);
   }
 }
@@ -1263,8 +1266,9 @@ __global__ void __launch_bounds__(256) rowdot64_kernel(const float* __restrict__
 // output element is (((p_0 + p_1) + ...) + bias) then residual + that -- the
 // reduction kernel's and epilogue's order -- and the LayerNorm is the shared
 // row code of the LayerNorm kernel, so C, ln_out, mean and rstd are the bits
-// the separate kernels give. 16-byte aligned rows, unbatched.
-template <typename T, int NV, int VW>
+// the separate kernels give. 16-byte aligned rows, unbatched. S2: exactly
+// two partials (the common split), loaded with no stand-in re-reads.
+template <typename T, int NV, int VW, bool S2>
 __global__ void __launch_bounds__(256) splitk_ln_kernel(GemmArgs a, const T* __restrict__ ws, int splits,
                                                          T* __restrict__ hout, T* __restrict__ mean,
                                                          T* __restrict__ rstd, const T* __restrict__ lw,
@@ -1281,7 +1285,8 @@ __global__ void __launch_bounds__(256) splitk_ln_kernel(GemmArgs a, const T* __r
   // every load of the row is issued before the first add, from addresses
   // that are always valid (a missing split, bias or residual re-reads the
   // first partial and is then left out), so no load waits behind a branch
-  constexpr int SP = NV * VW <= 16 ? 4 : (NV * VW <= 32 ? 2 : 1);
+  constexpr int SP = S2 ? 2 : (NV * VW <= 16 ? 4 : (NV * VW <= 32 ? 2 : 1));
+  if (S2) splits = 2;
   T pv[SP][NV][VW], bv[NV][VW], rv[NV][VW];
   const T* bsrc = bias ? bias : ws;
   const T* rsrc = add ? add + row * a.ldc : ws + row * a.N;
@@ -1575,12 +1580,18 @@ static int gemm_impl(int akc, int bkc, int64_t M, int64_t N, int64_t K, const vo
     GemmArgs r = a;
     r.ws = nullptr;
     const unsigned lg = (unsigned)cdiv(M, 4);
-#define CALL_LN(NV)                                                                                          \
-  splitk_ln_kernel<T, NV, LVW><<<lg, 256, 0, stream()>>>(r, (const T*)ws, splits, (T*)ep.ln_out, (T*)ep.ln_mean, \
-                                                          (T*)ep.ln_rstd, (const T*)ep.ln_w, (const T*)ep.ln_b,   \
-                                                          (T)ep.ln_eps)
+#define CALL_LN_S(NV, S2)                                                                                      \
+  splitk_ln_kernel<T, NV, LVW, S2><<<lg, 256, 0, stream()>>>(r, (const T*)ws, splits, (T*)ep.ln_out,               \
+                                                              (T*)ep.ln_mean, (T*)ep.ln_rstd, (const T*)ep.ln_w, \
+                                                              (const T*)ep.ln_b, (T)ep.ln_eps)
+#define CALL_LN(NV)          \
+  if (splits == 2)           \
+    CALL_LN_S(NV, true);     \
+  else                       \
+    CALL_LN_S(NV, false)
     LN_NV_SWITCH(ln_nv, CALL_LN)
 #undef CALL_LN
+#undef CALL_LN_S
   }
   if constexpr (std::is_same<T, float>::value) {
     if (ep.rowdot_out && !rowdot_done) {
