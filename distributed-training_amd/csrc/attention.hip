@@ -89,7 +89,8 @@ struct AttnArgs {
   Strides3 sq, sk, sv, so, sdo, sdq, sdk, sdv;
   int64_t B, H, T, D;
   double scale;
-  int vec;  // 16-byte global access allowed for every operand
+  int vec;   // 16-byte global access allowed for every operand
+  int ovec;  // the results (out, or dq, dk and dv) too, with D a multiple of the vector
 };
 
 // Load NR rows [r0, r0 + NR) of a (T x D) matrix with row stride `rs` into LDS
@@ -346,18 +347,42 @@ __device__ __forceinline__ void mma_ldsT_regs(AM<float>::acc_t (&out)[DP / 32], 
 
 // Write a wave's MT x DP result (held transposed: lane column c = row of the
 // result, register rows = d) through LDS to global rows r0 + (0 .. NROWS).
+// ovec (D == DP, dst and rs 16-byte granular): whole vectors out of LDS and
+// to global memory; in float32 a lane's four consecutive rows i = 4a .. 4a+3
+// go to LDS as one vector too.
 template <typename T, int DP, int NROWS>
 __device__ __forceinline__ void store_result(T* __restrict__ lds, const typename AM<T>::acc_t (&acc)[DP / AM<T>::MT],
                                              T mul, T* __restrict__ dst, int64_t rs, int r0, int Tn, int D, int wave,
-                                             int g, int c) {
+                                             int g, int c, bool ovec) {
   using M = AM<T>;
-  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
+  typedef typename M::vec_t V;
+  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD, VEC = M::VEC;
   T* Ws = lds + wave * MT * LD;
+  if constexpr (sizeof(T) == 4) {
 #pragma unroll
-  for (int dt = 0; dt < DP / MT; ++dt)
+    for (int dt = 0; dt < DP / MT; ++dt)
 #pragma unroll
-    for (int i = 0; i < NACC; ++i) Ws[c * LD + dt * MT + M::row(i, g)] = acc[dt][i] * mul;
+      for (int a4 = 0; a4 < NACC / 4; ++a4) {
+        V x;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = acc[dt][4 * a4 + e] * mul;
+        *reinterpret_cast<V*>(Ws + c * LD + dt * MT + M::row(4 * a4, g)) = x;
+      }
+  } else {
+#pragma unroll
+    for (int dt = 0; dt < DP / MT; ++dt)
+#pragma unroll
+      for (int i = 0; i < NACC; ++i) Ws[c * LD + dt * MT + M::row(i, g)] = acc[dt][i] * mul;
+  }
   __syncthreads();
+  if (ovec) {
+    for (int f = threadIdx.x; f < NROWS * DP / VEC; f += 256) {
+      const int r = f / (DP / VEC), d = (f % (DP / VEC)) * VEC;
+      if (r0 + r < Tn)
+        *reinterpret_cast<V*>(dst + (int64_t)(r0 + r) * rs + d) = *reinterpret_cast<const V*>(lds + r * LD + d);
+    }
+    return;
+  }
   for (int f = threadIdx.x; f < NROWS * DP; f += 256) {
     const int r = f / DP, d = f % DP;
     if (r0 + r < Tn && d < D) dst[(int64_t)(r0 + r) * rs + d] = lds[r * LD + d];
@@ -538,7 +563,8 @@ __global__ void __launch_bounds__(256, 2) attn_fwd_kernel(AttnArgs a) {
     mtop = group_max(mtop);
   }
   T* O = (T*)a.out + b * a.so.b + h * a.so.h;
-  store_result<T, DP, QB>(lds, oacc, lrow > T(0) ? T(1) / lrow : T(0), O, a.so.t, q0, Tn, D, wave, g, c);
+  store_result<T, DP, QB>(lds, oacc, lrow > T(0) ? T(1) / lrow : T(0), O, a.so.t, q0, Tn, D, wave, g, c,
+                          a.ovec != 0 && D == DP);
   if constexpr (LAZY) {
     lrow *= ex2(mrow - mtop);
     mrow = mtop;
@@ -778,9 +804,10 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   }
   T* DK = (T*)a.dk + b * a.sdk.b + h * a.sdk.h;
   T* DV = (T*)a.dv + b * a.sdv.b + h * a.sdv.h;
-  store_result<T, DP, KBB>(lds, dk, (T)a.scale, DK, a.sdk.t, k0, Tn, D, wave, g, c);
+  const bool ovec = a.ovec != 0 && D == DP;
+  store_result<T, DP, KBB>(lds, dk, (T)a.scale, DK, a.sdk.t, k0, Tn, D, wave, g, c, ovec);
   __syncthreads();
-  store_result<T, DP, KBB>(lds, dv, T(1), DV, a.sdv.t, k0, Tn, D, wave, g, c);
+  store_result<T, DP, KBB>(lds, dv, T(1), DV, a.sdv.t, k0, Tn, D, wave, g, c, ovec);
 }
 
 // ------------------------- backward A, one key tile per block (float32)
@@ -801,7 +828,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
   constexpr int TILE = MT * LD;                 // 32 rows, row form
   constexpr int WAVE_LDS = 2 * TILE + 2 * MT;   // Q rows, dO rows, (max + log2 sum, rowsum(dO * O))
-  constexpr int RED = 2 * DP * (MT + 1);        // a wave's dK^T and dV^T for the final sum
+  constexpr int LDR = DP + 4;                   // row stride of the final sum's [key][d] rows
+  constexpr int RED = 2 * MT * LDR;             // a wave's dK and dV rows for the final sum
   constexpr int PER_WAVE = WAVE_LDS > RED ? WAVE_LDS : RED;
   constexpr int NV = MT * DP / 4 / 64;          // 16-byte vectors per lane per tile and operand
   // four wave regions, then the block's V rows (shared: the B operand of dP)
@@ -936,32 +964,52 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
     if (more) put();
     wave_sync();
   }
-  // partial dK^T / dV^T of the four waves, added in wave order
+  // partial dK / dV of the four waves as [key][d] rows (a lane's registers
+  // 4a .. 4a+3 are four consecutive d of its key: one 16-byte write), added
+  // in wave order, four d at a time
   __syncthreads();
   float* R = lds + wave * PER_WAVE;
 #pragma unroll
   for (int dt = 0; dt < DP / MT; ++dt)
 #pragma unroll
-    for (int i = 0; i < NACC; ++i) {
-      const int d = dt * MT + M::row(i, g);
-      R[d * (MT + 1) + c] = dk[dt][i];
-      R[DP * (MT + 1) + d * (MT + 1) + c] = dv[dt][i];
+    for (int a4 = 0; a4 < NACC / 4; ++a4) {
+      const int o = c * LDR + dt * MT + M::row(4 * a4, g);
+      V4 xk, xv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xk[e] = dk[dt][4 * a4 + e];
+        xv[e] = dv[dt][4 * a4 + e];
+      }
+      *reinterpret_cast<V4*>(R + o) = xk;
+      *reinterpret_cast<V4*>(R + MT * LDR + o) = xv;
     }
   __syncthreads();
   float* DK = (float*)a.dk + b * a.sdk.b + h * a.sdk.h;
   float* DV = (float*)a.dv + b * a.sdv.b + h * a.sdv.h;
   const float scale = (float)a.scale;
-  for (int f = threadIdx.x; f < MT * DP; f += 256) {
-    const int key = f / DP, d = f % DP;
-    const int o = d * (MT + 1) + key;
-    float sk = lds[o], sv = lds[DP * (MT + 1) + o];
+  const bool ovec = a.ovec != 0;
+  for (int f = threadIdx.x; f < MT * DP / 4; f += 256) {
+    const int key = f / (DP / 4), d = (f % (DP / 4)) * 4;
+    const int o = key * LDR + d;
+    V4 sk = *reinterpret_cast<const V4*>(lds + o), sv = *reinterpret_cast<const V4*>(lds + MT * LDR + o);
 #pragma unroll
     for (int w = 1; w < 4; ++w) {
-      sk += lds[w * PER_WAVE + o];
-      sv += lds[w * PER_WAVE + DP * (MT + 1) + o];
+      sk += *reinterpret_cast<const V4*>(lds + w * PER_WAVE + o);
+      sv += *reinterpret_cast<const V4*>(lds + w * PER_WAVE + MT * LDR + o);
     }
-    DK[(int64_t)(k0 + key) * a.sdk.t + d] = sk * scale;
-    DV[(int64_t)(k0 + key) * a.sdv.t + d] = sv;
+    sk *= scale;
+    float* pk = DK + (int64_t)(k0 + key) * a.sdk.t + d;
+    float* pv = DV + (int64_t)(k0 + key) * a.sdv.t + d;
+    if (ovec) {
+      *reinterpret_cast<V4*>(pk) = sk;
+      *reinterpret_cast<V4*>(pv) = sv;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pk[e] = sk[e];
+        pv[e] = sv[e];
+      }
+    }
   }
 }
 
@@ -1072,7 +1120,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
     __syncthreads();
   }
   T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h;
-  store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c);
+  store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c, a.ovec != 0 && D == DP);
 }
 
 // dQ from the dS workspace, one query tile per block (float32): the block's
@@ -1087,7 +1135,8 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q1_kernel(AttnArgs a) {
   typedef M::vec_t V4;
   constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
   constexpr int TILE = MT * LD;
-  constexpr int RED = DP * (MT + 1);
+  constexpr int LDR = DP + 4;  // row stride of the final sum's [query][d] rows
+  constexpr int RED = MT * LDR;
   constexpr int PER_WAVE = TILE > RED ? TILE : RED;
   constexpr int NV = MT * DP / 4 / 64;
   __shared__ __attribute__((aligned(16))) float lds[4 * PER_WAVE];
@@ -1160,22 +1209,36 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q1_kernel(AttnArgs a) {
     wave_sync();
     dsr = dsn;
   }
+  // the four waves' partial dQ as [query][d] rows, added in wave order
   __syncthreads();
   float* R = lds + wave * PER_WAVE;
 #pragma unroll
   for (int dt = 0; dt < DP / MT; ++dt)
 #pragma unroll
-    for (int i = 0; i < NACC; ++i) R[(dt * MT + M::row(i, g)) * (MT + 1) + c] = dq[dt][i];
+    for (int a4 = 0; a4 < NACC / 4; ++a4) {
+      V4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = dq[dt][4 * a4 + e];
+      *reinterpret_cast<V4*>(R + c * LDR + dt * MT + M::row(4 * a4, g)) = x;
+    }
   __syncthreads();
   float* DQ = (float*)a.dq + b * a.sdq.b + h * a.sdq.h;
   const float scale = (float)a.scale;
-  for (int f = threadIdx.x; f < MT * DP; f += 256) {
-    const int q = f / DP, d = f % DP;
-    const int o = d * (MT + 1) + q;
-    float sq = lds[o];
+  const bool ovec = a.ovec != 0;
+  for (int f = threadIdx.x; f < MT * DP / 4; f += 256) {
+    const int q = f / (DP / 4), d = (f % (DP / 4)) * 4;
+    const int o = q * LDR + d;
+    V4 sq = *reinterpret_cast<const V4*>(lds + o);
 #pragma unroll
-    for (int w = 1; w < 4; ++w) sq += lds[w * PER_WAVE + o];
-    DQ[(int64_t)(q0 + q) * a.sdq.t + d] = sq * scale;
+    for (int w = 1; w < 4; ++w) sq += *reinterpret_cast<const V4*>(lds + w * PER_WAVE + o);
+    sq *= scale;
+    float* pq = DQ + (int64_t)(q0 + q) * a.sdq.t + d;
+    if (ovec) {
+      *reinterpret_cast<V4*>(pq) = sq;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pq[e] = sq[e];
+    }
   }
 }
 
@@ -1264,7 +1327,7 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
     __syncthreads();
   }
   T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h;
-  store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c);
+  store_result<T, DP, QB>(lds, dq, (T)a.scale, DQ, a.sdq.t, q0, Tn, D, wave, g, c, a.ovec != 0 && D == DP);
 }
 
 // ------------------------------------------- head dimensions beyond 64
@@ -1576,6 +1639,7 @@ DTMI_EXPORT int dtmi_attn_fwd(int dtype, int64_t B, int64_t H, int64_t T, int64_
            strides_vec(a.sk, vecn) && strides_vec(a.sv, vecn))
               ? 1
               : 0;
+  a.ovec = (D % vecn == 0 && aligned(o, 16) && strides_vec(a.so, vecn)) ? 1 : 0;
   if (dtype == DTMI_F32) return attn_fwd_impl<float>(a);
   return attn_fwd_impl<double>(a);
   DTMI_BODY_END
@@ -1624,6 +1688,10 @@ static int attn_bwd_entry(int dtype, int64_t B, int64_t H, int64_t T, int64_t D,
            strides_vec(a.sdo, vecn))
               ? 1
               : 0;
+  a.ovec = (D % vecn == 0 && aligned(dq, 16) && aligned(dk, 16) && aligned(dv, 16) && strides_vec(a.sdq, vecn) &&
+            strides_vec(a.sdk, vecn) && strides_vec(a.sdv, vecn))
+               ? 1
+               : 0;
   if (dtype == DTMI_F32) return attn_bwd_impl<float>(a, drow);
   return attn_bwd_impl<double>(a, drow);
 }
