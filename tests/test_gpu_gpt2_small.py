@@ -182,3 +182,42 @@ def test_layernorm_backward_taking_split_k_partials_changes_no_bit(dev):
     assert bits_equal(out[True][0], out[False][0])
     for a, b in zip(out[True][1], out[False][1]):
         assert bits_equal(a, b)
+
+
+def test_split_k_partials_reaching_a_layernorm_output_read_twice(dev, monkeypatch):
+    """A LayerNorm output read by two Linears at GPT-2 width (8192 x 768 rows;
+    the qkv- and fc-shaped products split their input gradients in two): each
+    product hands its dX over as split-K partials, the backward engine forms
+    their values to add the two gradients in its own order, and the LayerNorm
+    backward then takes a plain dy. Every gradient, the leaf input's
+    included, is bit for bit the path that sums the partials inside the
+    products."""
+    D, K, N, O, P, R, S = _api()
+    from dtmi.autograd import Tensor
+    rng = np.random.default_rng(11)
+    M, C = 8192, 768
+    hx = rng.standard_normal((M, C)).astype(np.float32)
+    c1 = rng.standard_normal((M, 3 * C)).astype(np.float32)
+    c2 = rng.standard_normal((M, 4 * C)).astype(np.float32)
+    formed = []
+    value = K.SplitSum.value
+    monkeypatch.setattr(K.SplitSum, "value", lambda self: formed.append(self.n) or value(self))
+    out = {}
+    for split in (True, False):
+        N.LN_SPLIT_SUM = split
+        try:
+            wr = np.random.default_rng(12)
+            ln, l1, l2 = N.LayerNorm(C), N.Linear(C, 3 * C, wr), N.Linear(C, 4 * C, wr)
+            x = Tensor(D.from_numpy(hx), requires_grad=True)
+            h = ln(x)
+            loss = (l1(h) * Tensor(D.from_numpy(c1))).sum() + (l2(h) * Tensor(D.from_numpy(c2))).sum()
+            loss.backward()
+            out[split] = [t.grad.numpy() for t in (x, ln.w, ln.b, l1.w, l1.b, l2.w, l2.b)]
+        finally:
+            N.LN_SPLIT_SUM = True
+        if split:
+            assert formed == [2, 2]  # both products split, both partial sets formed once
+            formed.clear()
+    assert not formed
+    for a, b in zip(out[True], out[False]):
+        assert bits_equal(a, b)
