@@ -375,7 +375,9 @@ int dtmi_linear_bwd_dx_parts(int dtype, void* parts, int max_parts, int* nparts,
 
 /* ------------------------------------------------------- causal attention
  * dtrain/autograd.py:226-247: o = softmax(q k^T * scale + causal mask) v over
- * (B, H, T, D), D <= 64 contiguous; each *_strides argument points at three
+ * (B, H, T, D), the head dimension D contiguous (up to 64 in the fused MFMA
+ * kernels; above 64 through materialised scores and batched GEMMs, one batch
+ * element at a time); each *_strides argument points at three
  * element strides (b, h, t) of that operand, so q/k/v/o/dq/dk/dv may be views
  * into fused [B, T, 3, H, D] / [B, T, H, D] buffers. The forward writes o and
  * the per-row softmax statistics (contiguous [B, H, T]): rowmax = log2(e) *
