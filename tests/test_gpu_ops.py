@@ -93,6 +93,35 @@ def test_layernorm_backward_rejects_an_addend_overlapping_dx(dev):
     _lib.sync()
 
 
+def test_layernorm_backward_parts_rejects_overlaps_and_part_counts(dev):
+    """dtmi_layernorm_bwd_parts refuses, before any launch, partials or an
+    addend that share bytes with dx and part counts outside 1..64; disjoint
+    neighbours in one buffer are fine."""
+    import ctypes
+    from dtmi import _lib
+    D, K = _dev()
+    rows, C, n = 8, 64, 2
+    x = D.from_numpy(np.random.default_rng(1).standard_normal((rows, C)).astype(np.float32))
+    w, b = D.full((C,), 1.0, np.float32), D.zeros((C,), np.float32)
+    _, mean, rstd = K.layernorm_fwd(x, w, b)
+    e = rows * C
+    buf = D.full((5 * e,), 0.25, np.float32)
+    dw, db = D.empty((C,), np.float32), D.empty((C,), np.float32)
+
+    def call(dx_off, parts_off, nparts=n, add_off=None):
+        add = ctypes.c_void_p(buf.ptr + 4 * add_off) if add_off is not None else None
+        return _lib.lib().dtmi_layernorm_bwd_parts(
+            _lib.F32, ctypes.c_void_p(buf.ptr + 4 * dx_off), dw.ptr, db.ptr, ctypes.c_void_p(buf.ptr + 4 * parts_off),
+            nparts, x.ptr, w.ptr, mean.ptr, rstd.ptr, add, rows, C, 0)
+    # dx inside the partials, straddling their end, or at their start
+    for dx_off, parts_off in ((e, 0), (2 * e - 1, 0), (0, 0), (e, 1)):
+        assert call(dx_off, parts_off) == 1, (dx_off, parts_off)  # DTMI_ERR_INVALID
+    assert call(4 * e, 0, add_off=4 * e + 3) == 1  # addend overlapping dx
+    assert call(4 * e, 0, nparts=0) == 1 and call(4 * e, 0, nparts=65) == 1
+    assert call(2 * e, 0) == 0 and call(0, e) == 0 and call(4 * e, 0, add_off=2 * e) == 0
+    _lib.sync()
+
+
 @pytest.mark.parametrize("shape", [(40, 3000), (1100, 4096)])
 def test_layernorm_long_float32_rows(dev, shape):
     """float32 rows of 12 and 16 vectors per lane: the backward loads each
