@@ -210,8 +210,11 @@ TimedLaunch::TimedLaunch(int fam, double w) : family(fam), work(w), slot(-1) {
   if (!g_timing || fam < 0) return;  // family -1: never timed (creates no events)
   if (g_pending.size() > 4096) drain_pending(false);
   PendingTiming t{fam, w, nullptr, nullptr};
-  if (hipEventCreate(&t.a) != hipSuccess) return;
-  if (hipEventCreate(&t.b) != hipSuccess) {
+  // timing-only events: no system-scope cache writeback and invalidate when
+  // recorded, which would otherwise add to the bracketed launch and leave the
+  // next kernel with a cold L2
+  if (hipEventCreateWithFlags(&t.a, hipEventDisableSystemFence) != hipSuccess) return;
+  if (hipEventCreateWithFlags(&t.b, hipEventDisableSystemFence) != hipSuccess) {
     (void)hipEventDestroy(t.a);
     return;
   }
