@@ -327,12 +327,20 @@ struct LnDispatch {
     size_t lds = (size_t)4 * 2 * NV * VW * 64 * sizeof(T);
     ln_bwd_kernel<T, NV, VW><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, add, rows, cols, acc);
   }
-  // dy as two split-K partials (rows of up to 8 vectors per lane)
+  // dy as two split-K partials (rows of up to 8 vectors per lane) or four
+  // (up to 4 vectors per lane)
   template <int NV>
-  static void bwd2(int grid, T* dx, T* pdw, T* pdb, const T* dy, int64_t pstride, const T* x, const T* w,
+  static void bwd2(int grid, int np, T* dx, T* pdw, T* pdb, const T* dy, int64_t pstride, const T* x, const T* w,
                    const T* mu, const T* rs, const T* add, int64_t rows, int cols, int acc) {
+    size_t lds = (size_t)4 * 2 * NV * VW * 64 * sizeof(T);
+    if constexpr (NV <= 4) {
+      if (np == 4) {
+        ln_bwd_kernel<T, NV, VW, 4><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, add, rows, cols,
+                                                                 acc, pstride);
+        return;
+      }
+    }
     if constexpr (NV <= 8) {
-      size_t lds = (size_t)4 * 2 * NV * VW * 64 * sizeof(T);
       ln_bwd_kernel<T, NV, VW, 2><<<grid, 256, lds, stream()>>>(dx, pdw, pdb, dy, x, w, mu, rs, add, rows, cols, acc,
                                                                pstride);
     }
@@ -386,10 +394,12 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
   const int nv = ln_pick_nv(cdiv(cols, 64LL * vw));
   const bool wide = nv < 0;  // longer rows than a wave holds
   if (nparts > 1) {
-    // dy as split-K partials: summed in the kernel's loads (two partials,
-    // aligned rows of up to 8 vectors per lane), else by a sum pass first
+    // dy as split-K partials: summed in the kernel's loads (two partials on
+    // aligned rows of up to 8 vectors per lane, four on rows of up to 4),
+    // else by a sum pass first
     const int64_t pstride = rows * cols;
-    if (nparts == 2 && vec && nv > 0 && nv <= 8 && (pstride * (int64_t)sizeof(T)) % 16 == 0) {
+    if (((nparts == 2 && nv <= 8) || (nparts == 4 && nv <= 4)) && vec && nv > 0 &&
+        (pstride * (int64_t)sizeof(T)) % 16 == 0) {
       const int grid = ln_bwd_blocks(rows);
       void* parts = nullptr;
       int rc = pool_alloc(&parts, (size_t)2 * grid * cols * sizeof(T));
@@ -397,13 +407,13 @@ static int ln_bwd(void* dx, void* dw, void* db, const void* dy, const void* x, c
       T* pdw = (T*)parts;
       T* pdb = pdw + (size_t)grid * cols;
       {
-        const double arrays = (addend || (accumulate & 1)) ? 5.0 : 4.0;
+        const double arrays = nparts + ((addend || (accumulate & 1)) ? 3.0 : 2.0);
         TimedLaunch tl(DTMI_FAM_LN_BWD, (double)rows * cols * arrays * sizeof(T));
         const int c = (int)cols;
         const int acc = (accumulate & 1) ? 1 : 0;
 #define CALLP(NV)                                                                                        \
-  LnDispatch<T, VWV>::template bwd2<NV>(grid, (T*)dx, pdw, pdb, (const T*)dy, pstride, (const T*)x, (const T*)w, \
-                                        (const T*)mean, (const T*)rstd, (const T*)addend, rows, c, acc)
+  LnDispatch<T, VWV>::template bwd2<NV>(grid, nparts, (T*)dx, pdw, pdb, (const T*)dy, pstride, (const T*)x,      \
+                                        (const T*)w, (const T*)mean, (const T*)rstd, (const T*)addend, rows, c, acc)
         LN_NV_SWITCH(nv, CALLP)
 #undef CALLP
         launch_colreduce<T>((T*)dw, pdw, grid, cols, (accumulate & 2) ? 1 : 0, (T*)db, pdb);
@@ -548,7 +558,8 @@ DTMI_EXPORT int dtmi_layernorm_bwd_parts(int dtype, void* dx, void* dw, void* db
     // the addend: the byte ranges must be disjoint
     const size_t bytes = (size_t)rows * (size_t)cols * (dtype == DTMI_F32 ? 4 : 8);
     const uintptr_t d0 = (uintptr_t)dx, p0 = (uintptr_t)dy_parts;
-    DTMI_CHECK(p0 + bytes * (size_t)nparts <= d0 || d0 + bytes <= p0, "dtmi_layernorm_bwd_parts: the partials overlap dx");
+    DTMI_CHECK(p0 + bytes * (size_t)nparts <= d0 || d0 + bytes <= p0,
+               "dtmi_layernorm_bwd_parts: the partials overlap dx");
     if (dx_addend) {
       const uintptr_t a0 = (uintptr_t)dx_addend;
       DTMI_CHECK(a0 + bytes <= d0 || d0 + bytes <= a0, "dtmi_layernorm_bwd_parts: the addend overlaps dx");

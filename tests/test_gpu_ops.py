@@ -423,13 +423,14 @@ def test_linear_forward_backward_at_layernorm_linear_workload(dev, dt):
 
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
-@pytest.mark.parametrize("K,N", [(768, 2304), (768, 3072)])
-def test_layernorm_backward_adds_the_split_k_partials_of_dy(dev, dt, K, N):
-    """The qkv / fc input gradient ([8192, 768] = dY W^T over N = 2304 or
-    3072) left as split-K partials and summed inside the LayerNorm backward:
-    the same bits as summing first (dtmi_linear_bwd_dx) and then
-    dtmi_layernorm_bwd, with and without the residual addend; and the
-    partials' value equal to the summed product."""
+@pytest.mark.parametrize("K,N,parts", [(768, 2304, 2), (768, 3072, 2), (768, 50304, 4)])
+def test_layernorm_backward_adds_the_split_k_partials_of_dy(dev, dt, K, N, parts):
+    """The qkv / fc / vocabulary-head input gradient ([8192, 768] = dY W^T
+    over N = 2304, 3072 or 50304) left as split-K partials (two, or four for
+    the head) and summed inside the LayerNorm backward: the same bits as
+    summing first (dtmi_linear_bwd_dx) and then dtmi_layernorm_bwd, with and
+    without the residual addend; and the partials' value equal to the summed
+    product."""
     D, K_ = _dev()
     rng = np.random.default_rng(K + N)
     M = 8192
@@ -441,9 +442,9 @@ def test_layernorm_backward_adds_the_split_k_partials_of_dy(dev, dt, K, N):
     pend = D.from_numpy(rng.standard_normal((M, K)).astype(dt))
     h, mean, rstd = K_.layernorm_fwd(x, lw, lb)
     dh, _, _ = K_.linear_bwd(h, W, dY, need_db=False)
-    dsplit, _, _ = K_.linear_bwd(h, W, dY, need_db=False, dx_parts=2)
+    dsplit, _, _ = K_.linear_bwd(h, W, dY, need_db=False, dx_parts=parts)
     if dt == np.float32:
-        assert isinstance(dsplit, K_.SplitSum) and dsplit.n == 2
+        assert isinstance(dsplit, K_.SplitSum) and dsplit.n == parts
     val = dsplit.value() if isinstance(dsplit, K_.SplitSum) else dsplit
     assert bits_equal(val.numpy(), dh.numpy())
     for addend in (None, pend):
