@@ -76,13 +76,14 @@ def _median(xs):
 def cpu_baseline(weights, xs, ys, seq: int):
     """The oracle (NumPy restatement of dtrain) on the host cores, on a bounded
     sample of the same step:
-      - forward+backward of one replica's first `seq` sequences: 1 warm-up,
-        then the median of 3 runs, with the BLAS thread count the machine is
-        configured for, and once more with 1 thread;
-      - the 4-replica bucket average, global norm, clip and AdamW over all
-        163,109,376 parameters, timed once;
-      - tokens/s extrapolated to the full step (4 x 8 sequences of
-        forward+backward, one optimizer pass);
+      - forward+backward of one replica's first `seq` sequences (default: the
+        replica's whole batch, 8 x 1024 tokens): 1 warm-up, then 1 timed run,
+        with the BLAS thread count the machine is configured for; and one
+        sequence with 1 thread (1 warm-up, 1 timed);
+      - the 4-replica bucket average (ring order), global norm, clip and
+        AdamW over all 163,109,376 parameters: median of 3;
+      - tokens/s extrapolated to the full step over the 4 replicas (and over
+        the 8 / seq sequence groups when seq < 8), plus one optimizer pass;
       - dtrain's own published benchmark configuration (float32, dim 128, 4
         layers, 4 heads, ctx 64, batch 8, vocabulary 65) with 1 thread: median
         of 3 full steps after 1 warm-up, beside dtrain's 2,577 tokens/s
@@ -95,31 +96,43 @@ def cpu_baseline(weights, xs, ys, seq: int):
     c = OM.GPTConfig(**CFG)
     P = {k: v.copy() for k, v in weights.items()}
     info = _cpu_info()
-    x, y = xs[0][:seq], ys[0][:seq]
 
-    def fb():
+    def fb(nseq):
         t0 = time.perf_counter()
-        _, g = OM.loss_and_grads(P, c, x, y)
+        _, g = OM.loss_and_grads(P, c, xs[0][:nseq], ys[0][:nseq])
         return time.perf_counter() - t0, g
 
-    _, g = fb()  # warm-up
-    runs = [fb()[0] for _ in range(3)]
-    t_fb = _median(runs)
+    def note(msg):
+        print(f"[cpu baseline] {msg}", file=sys.stderr, flush=True)
+
+    t_warm, _ = fb(seq)
+    note(f"warm-up forward+backward of {seq} x {CFG['ctx']} tokens: {t_warm:.1f} s")
+    t_fb, g = fb(seq)
+    note(f"timed forward+backward: {t_fb:.1f} s")
     with threadpool_limits(limits=1):
-        t_fb1, _ = fb()
+        fb(1)
+        t_fb1, _ = fb(1)
+    note(f"1 sequence on 1 thread: {t_fb1:.1f} s")
     names = list(P)
     glist = [g[k] for k in names]
-    t1 = time.perf_counter()
-    avg = ddp_average([glist] * WORLD, 4, 1.0, "ring")
-    sq = OO.global_sq_norm(avg)
-    s = OO.clip_scale(sq, CLIP)
+    del g
     opt = OO.AdamW([P[k] for k in names], lr=LR, betas=BETAS, eps=EPS, weight_decay=WD)
-    opt.step([v * s for v in avg])
-    t_opt = time.perf_counter() - t1
-    del avg, glist, g
+    t_opts = []
+    for _ in range(3):
+        t1 = time.perf_counter()
+        avg = ddp_average([glist] * WORLD, 4, 1.0, "ring")
+        sq = OO.global_sq_norm(avg)
+        s = OO.clip_scale(sq, CLIP)
+        opt.step([v * s for v in avg])
+        t_opts.append(time.perf_counter() - t1)
+        del avg
+    t_opt = _median(t_opts)
+    note(f"average + clip + AdamW: {', '.join(f'{t:.2f}' for t in t_opts)} s")
+    del glist
     tokens_step = WORLD * BATCH * CFG["ctx"]
     per_step = (WORLD * BATCH / seq) * t_fb + t_opt
-    per_step1 = (WORLD * BATCH / seq) * t_fb1 + t_opt
+    per_step1 = (WORLD * BATCH) * t_fb1 + t_opt
+    extrap = "the 4 replicas" if seq == BATCH else f"4 replicas x {BATCH // seq if BATCH % seq == 0 else BATCH / seq} groups"
 
     # dtrain's published configuration, 1 thread
     rc = OM.GPTConfig(vocab=65, ctx=64, dim=128, heads=4, layers=4, dtype="float32")
@@ -137,11 +150,11 @@ def cpu_baseline(weights, xs, ys, seq: int):
     return {"value": round(tokens_step / per_step, 2), "unit": "tokens/s", "cores": info["blas_threads"],
             "kind": "port", **info,
             "value_1_thread": round(tokens_step / per_step1, 2),
-            "sample": (f"oracle (NumPy) forward+backward of 1 replica x {seq} x {CFG['ctx']} tokens: median of 3 "
-                       f"after 1 warm-up {t_fb:.2f} s ({', '.join(f'{r:.2f}' for r in runs)}), 1 thread {t_fb1:.2f} s; "
-                       f"4-replica bucket average (ring order), clip and AdamW over 163,109,376 params once "
-                       f"({t_opt:.2f} s); extrapolated to the full 4 x 8 x 1024-token step "
-                       f"({per_step:.1f} s, 1 thread {per_step1:.1f} s)"),
+            "sample": (f"oracle (NumPy) forward+backward of 1 replica's {seq} x {CFG['ctx']} tokens: 1 timed run "
+                       f"after 1 warm-up, {t_fb:.2f} s (warm-up {t_warm:.2f} s); 4-replica bucket average (ring "
+                       f"order), clip and AdamW over 163,109,376 params, median of 3, {t_opt:.2f} s; extrapolated "
+                       f"over {extrap} to the 4 x 8 x 1024-token step: {per_step:.1f} s. 1 thread: 1 x "
+                       f"{CFG['ctx']} tokens {t_fb1:.2f} s, extrapolated over 32 sequences: {per_step1:.1f} s"),
             "reference_config_1_thread": {
                 "value": round(ref_tps, 1), "unit": "tokens/s",
                 "config": "float32 GPT, dim 128, 4 layers, 4 heads, ctx 64, batch 8, vocab 65 (dtrain's benchmark)",
@@ -157,7 +170,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seq", type=int, default=1, help="sequences in the CPU baseline sample")
+    ap.add_argument("--cpu-seq", type=int, default=8,
+                    help="sequences of one replica in the CPU baseline sample (8: the whole replica batch)")
     ap.add_argument("--seed", type=int, default=5)
     ap.add_argument("--workload", default="gpt2",
                     choices=["gpt2", "ln_linear", "attention", "bucket_adamw", "chargpt", "copy"],
@@ -461,16 +475,22 @@ def micro_attention(a):
 
 def micro_bucket_adamw(a):
     """124,439,808-element fixed-order 4-replica average (+ fused sum of squares),
-    clip and AdamW over the full buffer, then AdamW on the 1/4 shard."""
-    from dtmi import device as D, kernels as K
-    n, W = 124_439_808, 4
+    clip and AdamW over the full buffer, then AdamW on the 1/4 shard. Beside
+    it, the same average through DDP's 1 MiB buckets: the merged launches
+    DDP.finish issues, and its norm pass."""
+    from dtmi import ddp as P, device as D, kernels as K, replicas as R
+    from dtmi.workload import N_BUCKET_WORKLOAD, BucketParams
+    n, W = N_BUCKET_WORKLOAD, 4
     dt = np.dtype(a.dtype)
     rng = np.random.default_rng(4)
     p = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)).astype(dt)
     reps = (rng.standard_normal((W, n), dtype=np.float32) * np.float32(1e-3)).astype(dt)
     m = np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-4)).astype(dt)
     v = np.abs(rng.standard_normal(n, dtype=np.float32) * np.float32(1e-4)).astype(dt)
-    dp_, dm_, dv_, dr_ = D.from_numpy(p), D.from_numpy(m), D.from_numpy(v), D.from_numpy(reps)
+    bmodel = BucketParams(D.zeros((n,), dt))
+    ddp = P.DDP(bmodel, R.SimGroup(W), bucket_mb=1.0, algo="direct")
+    ddp.grads.rows.assign(reps)
+    dp_, dm_, dv_, dr_ = D.from_numpy(p), D.from_numpy(m), D.from_numpy(v), ddp.grads.rows
     del reps
     g_ = D.empty((n,), dt)
     nb = K.average_blocks(n, dt)
@@ -488,6 +508,9 @@ def micro_bucket_adamw(a):
     dtm, fams = _timed(a, step, ["bucket_avg", "adamw", "sumsq"])
     an, ams, awork = fams["adamw"]
     bn, bms, bwork = fams["bucket_avg"]
+    _, dfams = _timed(a, lambda: bmodel.hand_over(ddp), ["bucket_avg", "sumsq"])
+    dn, dms, dwork = dfams["bucket_avg"]
+    sn, sms, swork = dfams["sumsq"]
     total_bytes = awork + bwork
     total_ms = ams + bms
     ach = awork / (ams * 1e-3)
@@ -517,6 +540,10 @@ def micro_bucket_adamw(a):
                  {"bound": "hbm", "kernel": "adamw_flat_kernel", "achieved": round(ach / 1e9, 1), "peak": 8000.0,
                   "unit": "GB/s", "frac": round(ach / 8e12, 4), "traffic": None}, cpu,
                  {"bucket_average": {"GB/s": round(bwork / (bms * 1e-3) / 1e9, 1), "ms": round(bms / max(bn, 1), 4)},
+                  "bucket_average_ddp_1mib": {
+                      "GB/s": round(dwork / (dms * 1e-3) / 1e9, 1), "ms": round(dms / a.steps, 4),
+                      "launches": dn // a.steps, "buckets": len(ddp.buckets),
+                      "norm_pass": {"GB/s": round(swork / (sms * 1e-3) / 1e9, 1), "ms": round(sms / a.steps, 4)}},
                   "adamw": {"GB/s": round(ach / 1e9, 1), "ms": round(ams / max(an, 1), 4)}})
 
 

@@ -339,6 +339,18 @@ def layernorm_bwd(dy, x: DeviceArray, w: DeviceArray, mean: DeviceArray, rstd: D
     return dx, dw, db
 
 
+def ln_fusable_parts(dtype, cols: int) -> int:
+    """How many split-K partials of dy the LayerNorm backward adds inside its
+    row loads for rows of `cols` elements (16-byte aligned rows): four when a
+    row is at most 4 vectors per lane, two up to 8, else none (a separate sum
+    pass would run, so the product should sum its partials itself)."""
+    vw = 16 // np.dtype(dtype).itemsize
+    if cols % vw:
+        return 0
+    per_lane = -(-cols // (64 * vw))
+    return 4 if per_lane <= 4 else 2 if per_lane <= 8 else 0
+
+
 def _layernorm_bwd_parts(dy: SplitSum, x, w, mean, rstd, dw_out, db_out, dx_addend):
     _contig(dy.parts, x, w, mean, rstd)
     if dy.shape != x.shape or dy.dtype != x.dtype:

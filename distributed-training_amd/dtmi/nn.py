@@ -117,9 +117,10 @@ def linear(x: Tensor, w: Tensor, b: Tensor | None, residual: Tensor | None = Non
         rs = None
         if x._rowdot is not None and x.requires_grad:
             rs = dev.empty((X.shape[0] * x._rowdot * X.shape[1],), X.dtype)
-        # x is a LayerNorm output: its backward adds dx's split-K partials itself
-        # (up to four: the vocabulary head's dX splits four ways)
-        parts = 4 if LN_SPLIT_SUM and x._ln_out and rs is None else 0
+        # x is a LayerNorm output: its backward adds dx's split-K partials
+        # itself, as many as it takes for this row width (float32 rows of 768:
+        # four, which the vocabulary head's dX splits into)
+        parts = K.ln_fusable_parts(X.dtype, X.shape[-1]) if LN_SPLIT_SUM and x._ln_out and rs is None else 0
         dx, dw, db = K.linear_bwd(X2, W, g2, need_dx=x.requires_grad, need_db=b is not None, dw_out=grad_out(w),
                                   db_out=grad_out(b) if b is not None else None, rowdot=rs,
                                   rowdot_t=X.shape[1] if rs is not None else 1, dx_parts=parts)

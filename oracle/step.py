@@ -18,18 +18,21 @@ from .ddp import ddp_average
 from .optim import AdamW, clip_scale, global_sq_norm
 
 
-def single_step(P, c, batches, opt: AdamW, clip=1.0, emulate_world=1):
-    """batches: list (one per virtual rank) of (x, y). Returns (loss, grad_norm, grads)."""
+def single_step(P, c, batches, opt: AdamW, clip=1.0, emulate_world=1, accum=1):
+    """batches: list (one per virtual rank) of (x, y); with accum > 1, of accum
+    (x, y) pairs each. Micro-steps outer, virtual ranks inner (train.py:132-145).
+    Returns (loss, grad_norm, grads)."""
     names = list(P.keys())
-    n_micro = emulate_world
+    n_micro = accum * emulate_world
     grads = {k: None for k in names}
     loss_sum = 0.0
-    for vr in range(emulate_world):
-        x, y = batches[vr]
-        loss, g = model.loss_and_grads(P, c, x, y, loss_scale=1.0 / n_micro)
-        for k in names:
-            grads[k] = g[k] if grads[k] is None else grads[k] + g[k]
-        loss_sum += float(loss) / n_micro
+    for micro in range(accum):
+        for vr in range(emulate_world):
+            x, y = batches[vr] if accum == 1 else batches[vr][micro]
+            loss, g = model.loss_and_grads(P, c, x, y, loss_scale=1.0 / n_micro)
+            for k in names:
+                grads[k] = g[k] if grads[k] is None else grads[k] + g[k]
+            loss_sum += float(loss) / n_micro
     glist = [grads[k] for k in names]
     sq = global_sq_norm(glist)
     gnorm = float(np.sqrt(sq))

@@ -10,6 +10,7 @@ import pytest
 
 from dtmi import checkpoint, data
 from dtmi import train as T
+from oracle import model as OM, optim as OO, step as OS
 
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
@@ -98,3 +99,52 @@ def test_driver_flags_match_dtrain():
     d = T.parse([])
     assert (d.batch, d.ctx, d.dim, d.heads, d.layers, d.lr, d.wd, d.clip, d.bucket_mb, d.algo) == \
         (8, 64, 128, 4, 4, 1e-3, 0.1, 1.0, 1.0, "ring")
+
+
+# dtrain's training driver run (tests/golden/make_golden_driver.py): --mode single
+# --emulate-world 2 --accum 2 --steps 6 with the tiny float64 flags of dtrain's
+# tests/test_training.py:15-16
+DRIVER = dict(steps=6, world=2, accum=2, batch=2, ctx=16, dim=16, heads=2, layers=2, lr=3e-3, warmup=2, wd=0.1,
+              clip=1.0, seed=0)
+
+
+def test_schedule_and_batches_reproduce_dtrain_driver_run():
+    """dtmi.train.lr_at and dtmi.data.rank_batch, driven as dtrain's main loop
+    drives them (train.py:118-159: lr_at(step), rank_batch(step, micro, ...,
+    vr, W), micro-steps outer), with the oracle's arithmetic for the steps:
+    every logged lr is identical, and loss, grad_norm and the final
+    parameters are dtrain's bit for bit."""
+    g = np.load(GOLDEN / "dtrain_driver_run.npz")
+    a = DRIVER
+    d = data.CharData(g["corpus"].tobytes().decode())
+    c = OM.GPTConfig(vocab=d.vocab, ctx=a["ctx"], dim=a["dim"], heads=a["heads"], layers=a["layers"],
+                     dtype="float64")
+    P = OM.dtrain_init(c, seed=a["seed"])
+    opt = OO.AdamW(list(P.values()), lr=a["lr"], weight_decay=a["wd"])
+    for step in range(a["steps"]):
+        lr = T.lr_at(step, a["lr"], a["warmup"], a["steps"])
+        assert lr == g["log/lr"][step]
+        opt.lr = lr
+        batches = [[data.rank_batch(d.train, step, micro, a["batch"], a["ctx"], a["seed"], vr, a["world"])
+                    for micro in range(a["accum"])] for vr in range(a["world"])]
+        loss, gnorm, _ = OS.single_step(P, c, batches, opt, clip=a["clip"], emulate_world=a["world"],
+                                        accum=a["accum"])
+        assert loss == g["log/loss"][step]
+        assert gnorm == g["log/grad_norm"][step]
+    for k, v in P.items():
+        np.testing.assert_array_equal(v, g[f"param/{k}"])
+
+
+def test_reads_the_checkpoint_of_a_dtrain_driver_run():
+    """dtrain's driver stopped after step 3 (--stop-after 3 --ckpt-every 3):
+    its checkpoint holds the parameters it saved at that point, AdamW's step
+    count 3 and one m and v per parameter (train.py:170-180)."""
+    g = np.load(GOLDEN / "dtrain_driver_run.npz")
+    d = checkpoint.latest(str(GOLDEN / "dtrain_driver_ckpt"))
+    assert d.endswith("step_000003")
+    step, st = checkpoint.load(d, 0, 1)
+    names = [k[len("part_param/"):] for k in g.files if k.startswith("part_param/")]
+    assert step == 3 and int(st["t"]) == 3
+    np.testing.assert_array_equal(st["params"], np.concatenate([g[f"part_param/{k}"].reshape(-1) for k in names]))
+    assert sorted(k for k in st if k[0] in "mv") == sorted([f"m{i}" for i in range(len(names))] +
+                                                          [f"v{i}" for i in range(len(names))])

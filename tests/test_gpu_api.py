@@ -421,28 +421,50 @@ class _Params:
         return self.ps
 
 
+# launch grouping of the bucket averages: dtmi.ddp.DDP's defaults (every bucket
+# of these tiny models in one launch at finish()), a launch per bucket as each
+# completes (MERGE_BYTES 1), and runs cut by the rank-order segment limit
+MERGE = {"default": None, "per_bucket": (1, 16), "segment_limit": (1 << 30, 8)}
+
+
+@pytest.mark.parametrize("merge", sorted(MERGE))
 @pytest.mark.parametrize("world", [3, 4])
 @pytest.mark.parametrize("dt", ["float64", "float32"])
 @pytest.mark.parametrize("algo", ["ring", "direct"])
-def test_ddp_average_matches_dtrain_fixture(dev, golden, world, dt, algo):
+def test_ddp_average_matches_dtrain_fixture(dev, golden, monkeypatch, world, dt, algo, merge):
     """dtrain's DDP over its TCP ring / direct all-reduce (3 and 4 ranks, 256-byte
     buckets, gradients over 16 decades) bit for bit: the simulated replicas'
-    gradients go through the grad-ready hooks and finish()."""
+    gradients go through the grad-ready hooks and finish(), with the bucket
+    averages launched in each of the groupings DDP can make."""
     A, N, O, P, Z, R, S_ = _api()
     from dtmi import device as D
+    if MERGE[merge] is not None:
+        monkeypatch.setattr(P.DDP, "MERGE_BYTES", MERGE[merge][0])
+        monkeypatch.setattr(P.DDP, "MAX_SEGS", MERGE[merge][1])
     G = golden("dtrain_ddp_reduce.npz")
     n = len(SHAPES_DDP)
     m = _Params(A, [G[f"w{world}/{dt}/p0/{i}"] for i in range(n)])
     pg = R.SimGroup(world)
     ddp = P.DDP(m, pg, bucket_mb=256 / (1 << 20), overlap=True, algo=algo)
     assert len(ddp.buckets) > 2
+    launches = []
+    average = pg.average
+    pg.average = lambda out, rows, **kw: (launches.append((len(kw.get("segments") or ()), ddp._sync)),
+                                          average(out, rows, **kw))
     for r in range(world):
         with pg.replica(r):
             for i in reversed(range(n)):
                 p = m.ps[i]
                 p.grad = D.from_numpy(G[f"w{world}/{dt}/g{r}/{i}"])
                 ddp._on_grad(p)
+        if r == world - 1 and merge == "per_bucket":
+            # every bucket was averaged inside the last replica's hooks
+            assert len(launches) == len(ddp.buckets)
     ddp.finish()
+    if algo == "direct" and merge != "per_bucket":
+        assert len(launches) == 1  # one rank order: every bucket in one launch
+    if algo == "ring" and merge == "segment_limit":
+        assert len(launches) > 1  # 3-6 segments per bucket, at most 8 per launch
     for i, p in enumerate(m.ps):
         assert bits_equal(p.grad.numpy(), G[f"w{world}/{dt}/ddp_{algo}/{i}"]), i
 

@@ -98,3 +98,75 @@ def test_corrupt_checkpoint_is_rejected(dev, tmp_path, corpus):
     shard.write_bytes(bytes(b))
     with pytest.raises(ValueError, match="checksum mismatch"):
         train(tmp_path, "r", corpus, "ddp", 2, extra=["--steps", "4", "--ckpt-dir", str(ck), "--resume"])
+
+
+# ---------------------------------------------- against a run of dtrain's driver
+DRIVER = ["--mode", "single", "--emulate-world", "2", "--accum", "2", "--steps", "6"]
+
+
+@pytest.fixture(scope="module")
+def dtrain_run(golden, tmp_path_factory):
+    """dtrain's own driver (dtrain/train.py:72-190) on the corpus of its tests,
+    with DRIVER and the tiny float64 flags (tests/golden/make_golden_driver.py):
+    per-step log, final parameters, and the checkpoint its run stopped after
+    step 3 wrote."""
+    g = golden("dtrain_driver_run.npz")
+    p = tmp_path_factory.mktemp("dtrain") / "corpus.txt"
+    p.write_bytes(g["corpus"].tobytes())
+    params = {k[len("param/"):]: g[k] for k in g.files if k.startswith("param/")}
+    log = {k: g[f"log/{k}"] for k in ("lr", "loss", "grad_norm")}
+    return str(p), params, log
+
+
+def _check_log(lines, ref, steps):
+    """lr identical; loss and gradient norm within 1e-12 (relative) of dtrain's
+    log lines for the given 1-based steps."""
+    assert [d["step"] for d in lines] == list(steps)
+    for d in lines:
+        i = d["step"] - 1
+        assert d["lr"] == ref["lr"][i], d["step"]
+        assert abs(d["loss"] - ref["loss"][i]) <= 1e-12 * abs(ref["loss"][i]), d["step"]
+        assert abs(d["grad_norm"] - ref["grad_norm"][i]) <= 1e-12 * ref["grad_norm"][i], d["step"]
+
+
+def test_driver_matches_a_dtrain_driver_run(dev, tmp_path, dtrain_run):
+    """dtmi.train.main with dtrain's flags against dtrain's main on the same
+    corpus: every step's lr (warm-up then cosine) identical, loss and gradient
+    norm within 1e-12, final parameters within 1e-10 (dtrain's own bar for
+    runs that sum in different orders, tests/test_training.py:48-51)."""
+    corpus, ref_params, ref_log = dtrain_run
+    params, log = train(tmp_path, "single", corpus, "single", extra=DRIVER)
+    _check_log(log, ref_log, range(1, 7))
+    assert_close(params, ref_params, 1e-10)
+
+
+def test_ddp_driver_matches_a_dtrain_driver_run(dev, tmp_path, dtrain_run):
+    """2 simulated ranks x 2 micro-steps against dtrain's single process
+    emulating 2 ranks with 2 micro-steps (dtrain's
+    test_gradient_accumulation_matches_larger_batch, with dtrain's run as the
+    reference): the losses within 1e-12, parameters within 1e-10."""
+    corpus, ref_params, ref_log = dtrain_run
+    params, log = train(tmp_path, "ddp", corpus, "ddp", 2, extra=["--accum", "2", "--steps", "6"])
+    for d in log:
+        i = d["step"] - 1
+        assert d["lr"] == ref_log["lr"][i]
+        assert abs(d["loss"] - ref_log["loss"][i]) <= 1e-12 * abs(ref_log["loss"][i])
+    assert_close(params, ref_params, 1e-10)
+
+
+def test_resume_from_a_checkpoint_dtrain_wrote_during_training(dev, tmp_path, dtrain_run, capsys):
+    """dtmi.train.main --resume from the checkpoint dtrain's driver wrote at
+    step 3 (dtrain/checkpoint.py:40-88, train.py:98-112): steps 4-6 log
+    dtrain's lr, loss and gradient norm, and the final parameters are within
+    1e-10 of dtrain's uninterrupted run."""
+    import shutil
+    corpus, ref_params, ref_log = dtrain_run
+    ck = tmp_path / "ck"
+    shutil.copytree(Path(__file__).resolve().parent / "golden" / "dtrain_driver_ckpt", ck)
+    params, log = train(tmp_path, "resumed", corpus, "single",
+                        extra=[*DRIVER, "--ckpt-dir", str(ck), "--ckpt-every", "3", "--resume"])
+    assert "resumed from step 3" in capsys.readouterr().err
+    _check_log(log, ref_log, range(4, 7))
+    assert_close(params, ref_params, 1e-10)
+    # and it wrote its own step-6 checkpoint in the same format
+    assert (ck / "LATEST").read_text() == "step_000006"

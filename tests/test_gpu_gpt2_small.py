@@ -5,10 +5,13 @@ on, and the kernels at the shapes only that configuration reaches:
 - the whole training step (dtrain/train.py:128-159 with --mode ddp): 4
   simulated replicas of one 1024-token sequence each through forward and
   backward, every replica's 149 gradient tensors and loss against the oracle
-  (dtrain/nn.py:131-139, autograd.py), the bucketed fixed-order average
-  bit-exact on the device's own replica gradients (ddp.py:84-110), the global
-  norm and clip (train.py:155-158), and AdamW bit-exact on the averaged
-  gradients (optim.py:21-33);
+  (dtrain/nn.py:131-139, autograd.py), the bucketed average bit-exact on the
+  device's own replica gradients in both of dtrain's all-reduce orders (ring
+  and direct; ddp.py:84-110, comm.py:292-303, 342-391), the global norm and
+  clip (train.py:155-158), and AdamW bit-exact on the averaged gradients
+  (optim.py:21-33);
+- one replica at the benchmark's 8 x 1024 tokens, forward and backward
+  against the oracle;
 - causal attention at (B, H, T, D) = (2, 12, 1024, 64) (autograd.py:226-247);
 - cross entropy over 8192 x 50304 logits (autograd.py:250-266);
 - the vocabulary head's forward, dX and dW at M = 8192, K/N = 50304
@@ -35,11 +38,22 @@ def _api():
     return D, K, N, O, P, R, S
 
 
-def test_gpt2_small_ddp_step_matches_oracle(dev):
-    """One step of the headline workload at 1 sequence per replica: loss and
-    gradients of every replica within 1e-5 of the oracle, the 4-replica average
-    bit-exact to the fixed rank order of the device's replica rows, norm and
-    clip factor within 1e-5, AdamW bit-exact on the averaged gradients."""
+def _split_rows(rows, names, shapes, offs):
+    """A [W, n] gradient buffer back into per-replica lists of parameter arrays."""
+    return [[rows[r, offs[i]:offs[i + 1]].reshape(shapes[k]) for i, k in enumerate(names)]
+            for r in range(rows.shape[0])]
+
+
+@pytest.mark.parametrize("algo", ["direct", "ring"])
+def test_gpt2_small_ddp_step_matches_oracle(dev, algo):
+    """One step of the headline workload at 1 sequence per replica, with each
+    of dtrain's all-reduce orders (`--algo ring` is what the benchmark runs):
+    loss and gradients of every replica within 1e-5 of the oracle; the
+    51-bucket average (merged launches of adjacent buckets, up to 16 rank-order
+    segments each) bit-exact to dtrain's DDP.finish restated over the device's
+    own replica rows (ddp.py:84-110 with comm.py:292-303, 342-372 for ring,
+    374-391 for direct); norm and clip factor within 1e-5; AdamW bit-exact on
+    the averaged gradients."""
     D, K, N, O, P, R, S = _api()
     W = 4
     oc = OM.GPTConfig(dtype="float32", **GPT2)
@@ -50,16 +64,32 @@ def test_gpt2_small_ddp_step_matches_oracle(dev):
     names = [n for n, _ in m.named_parameters()]
     assert len(names) == 149
     pg = R.SimGroup(W)
-    ddp = P.DDP(m, pg, bucket_mb=1.0, overlap=True, algo="direct")
+    ddp = P.DDP(m, pg, bucket_mb=1.0, overlap=True, algo=algo)
     assert len(ddp.buckets) == 51
+    launches = []
+    average = pg.average
+    pg.average = lambda out, rows, **kw: (launches.append(kw.get("segments")), average(out, rows, **kw))
     lr = 3e-4
     opt = O.AdamW([p.data for p in m.parameters()], lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
     res = S.step_ddp(m, ddp, opt, [[(xs[r], ys[r])] for r in range(W)], clip=1.0)
     rows = ddp.grads.rows.numpy()  # [W, n]: every replica's gradients, forward order
     avg_dev = ddp.avg.numpy()[:ddp.grads.n]
     p_dev = m.flat.numpy()
+    # adjacent buckets share launches; the ring order gives several segments per launch
+    assert 1 < len(launches) < 51
+    if algo == "ring":
+        assert max(len(s) for s in launches) > 4
 
+    shapes = {k: weights[k].shape for k in names}
     offs = np.cumsum([0] + [weights[k].size for k in names])
+    # the average of the device's own replica gradients: bit-exact to dtrain's
+    # bucketed all-reduce in the chosen order, times 1/W
+    dev_avg_ref = ddp_average(_split_rows(rows, names, shapes, offs), 4, 1.0, algo=algo)
+    assert bits_equal(avg_dev, np.concatenate([a.reshape(-1) for a in dev_avg_ref]))
+    del dev_avg_ref
+    if algo == "ring":  # the ring order is not the rank order: some bits must differ
+        assert not bits_equal(avg_dev, fixed_order_sum(list(rows)) * np.float32(0.25))
+
     losses, replica_grads = [], []
     for r in range(W):
         loss, G = OM.loss_and_grads(weights, oc, xs[r], ys[r])
@@ -72,10 +102,8 @@ def test_gpt2_small_ddp_step_matches_oracle(dev):
     ref_loss = sum(losses) / W
     assert abs(res.loss - ref_loss) <= 1e-5 * abs(ref_loss)
 
-    # the average of the device's own replica gradients: bit-exact
-    assert bits_equal(avg_dev, fixed_order_sum(list(rows)) * np.float32(0.25))
-    # and within tolerance of the oracle's average of its own gradients
-    ref_avg = ddp_average(replica_grads, 4, 1.0)
+    # within tolerance of the oracle's average of its own gradients
+    ref_avg = ddp_average(replica_grads, 4, 1.0, algo=algo)
     del replica_grads
     for i, k in enumerate(names):
         assert rel_err(avg_dev[offs[i]:offs[i + 1]], ref_avg[i].reshape(-1)) <= 1e-5, k
@@ -90,6 +118,30 @@ def test_gpt2_small_ddp_step_matches_oracle(dev):
     opt_ref = OO.AdamW([p_ref], lr=lr, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
     opt_ref.step([avg_dev * s])
     assert bits_equal(p_dev, p_ref)
+
+
+def test_gpt2_small_replica_at_8_sequences_matches_oracle(dev):
+    """One replica at the benchmark's batch (8 x 1024 tokens, so every Linear
+    runs at M = 8192 with the tile and split-K choices of the benchmark):
+    forward and backward through the model, loss and all 149 gradients within
+    1e-5 of the oracle."""
+    D, K, N, O, P, R, S = _api()
+    oc = OM.GPTConfig(dtype="float32", **GPT2)
+    weights = OM.synthetic_init(oc, seed=5)
+    xs, ys = OM.synthetic_tokens(oc, batch=8, seed=5, replicas=1)
+    m = N.GPT(N.GPTConfig(dtype="float32", **GPT2), seed=5)
+    m.load_numpy(weights)
+    m.zero_grad()
+    _, loss = m(xs[0], ys[0])
+    loss.backward()
+    got_loss = float(loss.numpy())
+    got = {k: p.grad.numpy() for k, p in m.named_parameters()}
+    del m, loss
+    ref_loss, G = OM.loss_and_grads(weights, oc, xs[0], ys[0])
+    assert abs(got_loss - float(ref_loss)) <= 1e-5 * abs(float(ref_loss))
+    assert len(got) == 149
+    for k, g in got.items():
+        assert rel_err(g, G[k]) <= 1e-5, k
 
 
 @pytest.mark.parametrize("dt,B", [(np.float32, 2), (np.float64, 1)])

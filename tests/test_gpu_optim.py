@@ -249,6 +249,51 @@ def test_bucket_average_and_adamw_at_124m_params(dev, dt):
     assert bits_equal(p_sh, p[:sh])
 
 
+@pytest.mark.parametrize("dt,algo", [(np.float32, "direct"), (np.float64, "direct"), (np.float32, "ring")])
+def test_bucket_average_at_124m_params_through_ddp_buckets(dev, dt, algo):
+    """The 124,439,808-element, 4-replica average through DDP's 1 MiB bucket
+    layout (dtrain/ddp.py:46-56: 474 full buckets and a remainder in float32,
+    949 and a remainder in float64) and the merged launches DDP.finish issues
+    (ddp.py:84-110): bit-exact to dtrain's bucketed all-reduce in rank order
+    ("direct", the workload's fixed order 0..3) or in its ring order, times
+    1/4; the norm it leaves within 1e-14 of an extended-precision sum."""
+    from dtmi import ddp as P, device as D, replicas as R
+    from dtmi.workload import N_BUCKET_WORKLOAD, BucketParams
+    from oracle.ddp import ddp_average
+    n, W = N_BUCKET_WORKLOAD, 4
+    rng = np.random.default_rng(4)
+    reps = rng.standard_normal((W, n), dtype=dt) * dt(1e-3)
+    model = BucketParams(D.zeros((n,), dt))
+    per = (1 << 20) // np.dtype(dt).itemsize
+    assert model.sizes[1:] == [per] * (n // per) and model.sizes[0] == n % per
+    pg = R.SimGroup(W)
+    ddp = P.DDP(model, pg, bucket_mb=1.0, algo=algo)
+    assert len(ddp.buckets) == n // per + 1
+    ddp.grads.rows.assign(reps)
+    launches = []
+    average = pg.average
+    pg.average = lambda out, rows, **kw: (launches.append(rows.shape[1]), average(out, rows, **kw))
+    model.hand_over(ddp)
+    assert sum(launches) == n and len(launches) < len(ddp.buckets) // 3
+    got = ddp.avg.numpy()[:n]
+    if algo == "direct":
+        ref = fixed_order_sum(list(reps))
+        ref *= dt(0.25)
+    else:
+        sizes = model.sizes
+        offs = np.cumsum([0] + sizes)
+        ref = np.concatenate(ddp_average([[reps[r, offs[i]:offs[i + 1]] for i in range(len(sizes))]
+                                          for r in range(W)], np.dtype(dt).itemsize, 1.0, algo="ring"))
+    assert bits_equal(got, ref)
+    for i in (0, len(model.ps) // 2, len(model.ps) - 1):  # the grads are the averaged buffer's slices
+        off = sum(model.sizes[:i])
+        assert bits_equal(model.ps[i].grad.numpy(), ref[off:off + model.sizes[i]])
+    del reps
+    r64 = ref.astype(np.float64)
+    exact = float(np.sum(np.square(r64).astype(np.longdouble)))
+    assert abs(float(ddp.grad_sq.numpy()[0]) - exact) <= 1e-14 * exact
+
+
 def _ring_ref(reps, segs, dt):
     W, n = reps.shape
     starts = [s for s, _ in segs] + [n]

@@ -120,3 +120,19 @@ def test_benchmark_inputs_equal_the_oracles():
             assert np.array_equal(u, v)
     gpt2 = GPTConfig(vocab=50304, ctx=1024, dim=768, heads=12, layers=12)
     assert sum(int(np.prod(s)) for _, s in Wk.param_spec(gpt2)) == 163_109_376
+
+
+def test_split_k_partials_offered_to_the_layernorm_backward():
+    """The product reading a LayerNorm output leaves at most as many split-K
+    partials of dx as the LayerNorm backward adds in its row loads (four
+    for rows of up to 4 16-byte vectors per lane, two up to 8, else none)."""
+    from dtmi.kernels import ln_fusable_parts
+    assert ln_fusable_parts(np.float32, 768) == 4  # GPT-2: 3 vectors per lane
+    assert ln_fusable_parts(np.float32, 1024) == 4
+    assert ln_fusable_parts(np.float32, 1028) == 2
+    assert ln_fusable_parts(np.float32, 2048) == 2
+    assert ln_fusable_parts(np.float32, 2052) == 0
+    assert ln_fusable_parts(np.float32, 770) == 0  # rows not in 16-byte vectors
+    assert ln_fusable_parts(np.float64, 768) == 2  # 6 vectors per lane
+    assert ln_fusable_parts(np.float64, 512) == 4
+    assert ln_fusable_parts(np.float64, 1025) == 0
