@@ -467,8 +467,8 @@ def micro_attention(a):
     return _line("causal attention backward throughput (5 GEMMs, causal-exact FLOP) at B16 H12 T256 D64",
                  round(ach / 1e12, 2), "TFLOP/s", a, 1e3 * dtm / a.steps,
                  {"workload": f"causal self-attention backward B=16 H=12 T=256 D=64 {a.dtype}"},
-                 {"bound": "mfma", "kernel": ("attn_drow64 + attn_bwd_kv1 + attn_bwd_q1 (aligned float32), attn_drow + attn_bwd_kv + "
-                             "attn_bwd_q_ds otherwise"), "achieved": round(ach / 1e12, 2),
+                 {"bound": "mfma", "kernel": ("attn_drow64 + attn_bwd_kvp + attn_bwd_qp (aligned float32), attn_drow64 + "
+                             "attn_bwd_kv + attn_bwd_q_ds (float64)"), "achieved": round(ach / 1e12, 2),
                   "peak": _mfma_peak(a.dtype) / 1e12, "unit": "TFLOP/s",
                   "frac": round(ach / _mfma_peak(a.dtype), 4), "traffic": None}, cpu)
 

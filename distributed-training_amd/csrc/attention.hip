@@ -25,12 +25,15 @@
 // registers) and writing dS = P * (dP - rowsum(dO * O)) to a [B, H, T, T]
 // workspace; kernel B owns queries and accumulates dQ = dS K from it (when
 // the workspace would exceed its bound, kernel B recomputes dS instead).
-// Float32 with D = 64 and T a multiple of 32 uses one 32-key (32-query) tile
-// per block, whose four waves split the tile's query (key) range and add
-// their partial sums in wave order at the end; otherwise a block owns 128
-// keys (queries), one 32-wide tile per wave, and the float32 kernel A keeps
-// its query and dO tiles also transposed in LDS so the dK / dV MFMAs read
-// them with 16-byte vectors. Results are deterministic.
+// Float32 with D = 64 and T a multiple of 32 works on 16 x 16 tiles with
+// paired ranges: key tile j and its mirror nt - 1 - j (nt + 1 tile pairs
+// between them) split over two waves in the key pass, query tile i and its
+// mirror over a pair of waves in the dQ pass, so every wave carries the same
+// work whatever the sequence length, and dS lives in causal tiles only.
+// Otherwise a block owns 128 keys (queries), one 32-wide (16-wide in
+// float64) tile per wave, and the float32 kernel A keeps its query and dO
+// tiles also transposed in LDS so the dK / dV MFMAs read them with 16-byte
+// vectors. Results are deterministic.
 #include <cmath>
 
 #include "bufrsrc.h"
@@ -810,209 +813,6 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   store_result<T, DP, KBB>(lds, dv, T(1), DV, a.sdv.t, k0, Tn, D, wave, g, c, ovec);
 }
 
-// ------------------------- backward A, one key tile per block (float32)
-// One block owns MT = 32 keys of one (batch, head); its four waves take the
-// query tiles that see those keys in turn (wave w: tiles kt + w, kt + w + 4,
-// ...), each with its own LDS copy of its tile's Q and dO rows and row
-// statistics. The waves never wait for each other inside the loop, and no
-// wave carries more than a quarter of its key tile's query range, so short
-// sequences still spread over the whole chip and a long one ends without a
-// single-wave tail. Each wave prefetches its next tile into registers while
-// it computes the current one. The four partial dK / dV are added in wave
-// order at the end. Aligned path only: D = DP = 64, T a multiple of 32,
-// 16-byte access, the dS workspace present.
-template <int DP>
-__global__ void __launch_bounds__(256, 2) attn_bwd_kv1_kernel(AttnArgs a) {
-  using M = AM<float>;
-  typedef M::vec_t V4;
-  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
-  constexpr int TILE = MT * LD;                 // 32 rows, row form
-  constexpr int WAVE_LDS = 2 * TILE + 2 * MT;   // Q rows, dO rows, (max + log2 sum, rowsum(dO * O))
-  constexpr int LDR = DP + 4;                   // row stride of the final sum's [key][d] rows
-  constexpr int RED = 2 * MT * LDR;             // a wave's dK and dV rows for the final sum
-  constexpr int PER_WAVE = WAVE_LDS > RED ? WAVE_LDS : RED;
-  constexpr int NV = MT * DP / 4 / 64;          // 16-byte vectors per lane per tile and operand
-  // four wave regions, then the block's V rows (shared: the B operand of dP)
-  __shared__ __attribute__((aligned(16))) float lds[4 * PER_WAVE + TILE];
-
-  int kt, bh;  // kt: the block's key tile; 0 sees the most query tiles
-  causal_block(kt, bh);
-  const int64_t b = bh / a.H, h = bh % a.H;
-  const int Tn = (int)a.T;
-  const int nt = Tn / MT;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane / MT, c = lane % MT;
-  const int k0 = kt * MT;
-  const int kj = k0 + c;  // this lane's key (column)
-  const float* Q = (const float*)a.q + b * a.sq.b + h * a.sq.h;
-  const float* K = (const float*)a.k + b * a.sk.b + h * a.sk.h;
-  const float* Vv = (const float*)a.v + b * a.sv.b + h * a.sv.h;
-  const float* G = (const float*)a.dO + b * a.sdo.b + h * a.sdo.h;
-  const float* RM = (const float*)a.rowmax + (int64_t)bh * Tn;
-  const float* RS = (const float*)a.rowsum + (int64_t)bh * Tn;
-  const float* DR = (const float*)a.drow + (int64_t)bh * Tn;
-  float* DS = (float*)a.ds + (int64_t)bh * Tn * Tn;
-  const float sl2 = (float)(a.scale * 1.4426950408889634);
-  // buffer resources over this (batch, head)'s rows; byte offsets below
-  const Rsrc rQ = make_rsrc(Q, (uint64_t)Tn * a.sq.t * 4), rG = make_rsrc(G, (uint64_t)Tn * a.sdo.t * 4);
-  const Rsrc rM = make_rsrc(RM, (uint64_t)Tn * 4), rL = make_rsrc(RS, (uint64_t)Tn * 4),
-             rD = make_rsrc(DR, (uint64_t)Tn * 4);
-  const Rsrc rS = make_rsrc(DS, (uint64_t)Tn * Tn * 4);
-  const uint32_t ds_lane = (uint32_t)(4 * g * Tn + kj) * 4u;  // dS of row 4g, column kj
-
-  float* W = lds + wave * PER_WAVE;
-  float* Qs = W;
-  float* Gs = W + TILE;
-  float* ST = W + 2 * TILE;  // [0, MT): max + log2 sum; [MT, 2 MT): rowsum(dO * O)
-
-  M::vec_t kf[DP / 8];
-  load_frag_rows<float, DP>(kf, K, a.sk.t, kj, Tn, DP, g, true);
-  float* Vs = lds + 4 * PER_WAVE;
-  // the block's V rows: this thread's vectors go to registers first, and to
-  // LDS only after the first tile's loads are issued too, so the prologue
-  // waits for global memory once
-  constexpr int VN = MT * DP / 4 / 256;
-  static_assert(VN * 256 == MT * DP / 4, "V rows: whole vectors per thread");
-  V4 vrow[VN];
-#pragma unroll
-  for (int i = 0; i < VN; ++i) {
-    const int f = threadIdx.x + 256 * i, r = f / (DP / 4), d = (f % (DP / 4)) * 4;
-    vrow[i] = *reinterpret_cast<const V4*>(Vv + (int64_t)(k0 + r) * a.sv.t + d);
-  }
-  M::acc_t dk[DP / MT], dv[DP / MT];
-#pragma unroll
-  for (int dt = 0; dt < DP / MT; ++dt) dk[dt] = dv[dt] = M::acc_t(0);
-
-  // this lane's share of a tile: vector v covers row 4 v + lane / 16, columns 4 (lane % 16) ..
-  const int lrow = lane >> 4, lcol = (lane & 15) * 4;
-  V4 rq[NV], rg[NV];
-  float rm = 0.f, rl = 1.f, rd = 0.f;
-  const uint32_t vq = (uint32_t)(lrow * a.sq.t + lcol) * 4u, vg = (uint32_t)(lrow * a.sdo.t + lcol) * 4u;
-  const uint32_t vs = (uint32_t)(lane & (MT - 1)) * 4u;
-  auto fetch = [&](int qs) {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      rq[v] = buf_load4(rQ, vq, (uint32_t)((qs + 4 * v) * a.sq.t) * 4u);
-      rg[v] = buf_load4(rG, vg, (uint32_t)((qs + 4 * v) * a.sdo.t) * 4u);
-    }
-    rm = buf_load1(rM, vs, (uint32_t)qs * 4u);
-    rl = buf_load1(rL, vs, (uint32_t)qs * 4u);
-    rd = buf_load1(rD, vs, (uint32_t)qs * 4u);
-  };
-  auto put = [&]() {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) {
-      const int r = 4 * v + lrow;
-      *reinterpret_cast<V4*>(Qs + r * LD + lcol) = rq[v];
-      *reinterpret_cast<V4*>(Gs + r * LD + lcol) = rg[v];
-    }
-    if (lane < MT) {
-      ST[lane] = rm + log2(rl);
-      ST[MT + lane] = rd;
-    }
-  };
-  // the wave's LDS is its own: a wave-level barrier orders its writes and reads
-  auto wave_sync = [] {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  };
-
-  int qt = kt + wave;
-  if (qt < nt) fetch(qt * MT);
-#pragma unroll
-  for (int i = 0; i < VN; ++i) {
-    const int f = threadIdx.x + 256 * i, r = f / (DP / 4), d = (f % (DP / 4)) * 4;
-    *reinterpret_cast<V4*>(Vs + r * LD + d) = vrow[i];
-  }
-  if (qt < nt) put();
-  __syncthreads();  // V rows and every wave's first tile in place
-  for (; qt < nt; qt += 4) {
-    const int qs = qt * MT;
-    const bool more = qt + 4 < nt;
-    if (more) fetch(qs + 4 * MT);
-    M::acc_t s = mma_rows_frag<float, DP>(M::acc_t(0), Qs, 0, kf, g, c);
-    M::acc_t dp = mma_rows_rows<float, DP>(M::acc_t(0), Gs, Vs, g, c);
-    const int lim = kj - qs - 4 * g;  // row qs + 4g + x sees key kj iff x >= lim
-    auto probs = [&](auto maskc) {
-      constexpr bool MASK = decltype(maskc)::value;
-#pragma unroll
-      for (int a4 = 0; a4 < NACC / 4; ++a4) {
-        const int r0 = 8 * a4 + 4 * g;
-        const V4 ml4 = *reinterpret_cast<const V4*>(&ST[r0]);
-        const V4 d4 = *reinterpret_cast<const V4*>(&ST[MT + r0]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 4 * a4 + e;
-          float p = ex2(__builtin_fmaf(s[i], sl2, -ml4[e]));
-          if constexpr (MASK) p = 8 * a4 + e >= lim ? p : 0.f;
-          s[i] = p;
-          const float v = p * (dp[i] - d4[e]);
-          dp[i] = v;
-          buf_store1(v, rS, ds_lane, (uint32_t)((qs + 8 * a4 + e) * Tn) * 4u);  // dS[qs + 8a + 4g + e][kj]
-        }
-      }
-    };
-    if (qt == kt)
-      probs(std::true_type());
-    else
-      probs(std::false_type());
-    // dV^T += dO^T P ; dK^T += Q^T dS
-    mma_lds_t_regs<float, DP>(dv, Gs, 0, s, g, c);
-    mma_lds_t_regs<float, DP>(dk, Qs, 0, dp, g, c);
-    wave_sync();
-    if (more) put();
-    wave_sync();
-  }
-  // partial dK / dV of the four waves as [key][d] rows (a lane's registers
-  // 4a .. 4a+3 are four consecutive d of its key: one 16-byte write), added
-  // in wave order, four d at a time
-  __syncthreads();
-  float* R = lds + wave * PER_WAVE;
-#pragma unroll
-  for (int dt = 0; dt < DP / MT; ++dt)
-#pragma unroll
-    for (int a4 = 0; a4 < NACC / 4; ++a4) {
-      const int o = c * LDR + dt * MT + M::row(4 * a4, g);
-      V4 xk, xv;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        xk[e] = dk[dt][4 * a4 + e];
-        xv[e] = dv[dt][4 * a4 + e];
-      }
-      *reinterpret_cast<V4*>(R + o) = xk;
-      *reinterpret_cast<V4*>(R + MT * LDR + o) = xv;
-    }
-  __syncthreads();
-  float* DK = (float*)a.dk + b * a.sdk.b + h * a.sdk.h;
-  float* DV = (float*)a.dv + b * a.sdv.b + h * a.sdv.h;
-  const float scale = (float)a.scale;
-  const bool ovec = a.ovec != 0;
-  for (int f = threadIdx.x; f < MT * DP / 4; f += 256) {
-    const int key = f / (DP / 4), d = (f % (DP / 4)) * 4;
-    const int o = key * LDR + d;
-    V4 sk = *reinterpret_cast<const V4*>(lds + o), sv = *reinterpret_cast<const V4*>(lds + MT * LDR + o);
-#pragma unroll
-    for (int w = 1; w < 4; ++w) {
-      sk += *reinterpret_cast<const V4*>(lds + w * PER_WAVE + o);
-      sv += *reinterpret_cast<const V4*>(lds + w * PER_WAVE + MT * LDR + o);
-    }
-    sk *= scale;
-    float* pk = DK + (int64_t)(k0 + key) * a.sdk.t + d;
-    float* pv = DV + (int64_t)(k0 + key) * a.sdv.t + d;
-    if (ovec) {
-      *reinterpret_cast<V4*>(pk) = sk;
-      *reinterpret_cast<V4*>(pv) = sv;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pk[e] = sk[e];
-        pv[e] = sv[e];
-      }
-    }
-  }
-}
-
 // ------------------------------------------------------- backward B: dQ
 // dQ from the dS the key-block pass wrote: dQ^T += K^T dS^T over the key
 // tiles up to the block's last query, with dS read straight into the MFMA B
@@ -1129,119 +929,6 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
 // prefetching the next tile's K rows and dS entries into registers; the four
 // partial dQ are added in wave order at the end. Aligned path only (D = DP =
 // 64, T a multiple of 32, 16-byte access).
-template <int DP>
-__global__ void __launch_bounds__(256, 2) attn_bwd_q1_kernel(AttnArgs a) {
-  using M = AM<float>;
-  typedef M::vec_t V4;
-  constexpr int MT = M::MT, NACC = M::NACC, LD = DP + M::PAD;
-  constexpr int TILE = MT * LD;
-  constexpr int LDR = DP + 4;  // row stride of the final sum's [query][d] rows
-  constexpr int RED = MT * LDR;
-  constexpr int PER_WAVE = TILE > RED ? TILE : RED;
-  constexpr int NV = MT * DP / 4 / 64;
-  __shared__ __attribute__((aligned(16))) float lds[4 * PER_WAVE];
-
-  int rank, bh;  // rank 0: the last query tile, which sees every key tile
-  causal_block(rank, bh);
-  const int64_t b = bh / a.H, h = bh % a.H;
-  const int Tn = (int)a.T;
-  const int nt = Tn / MT;
-  const int qt = nt - 1 - rank;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int g = lane / MT, c = lane % MT;
-  const int q0 = qt * MT;
-  const int qr = q0 + c;  // this lane's query (column)
-  const float* K = (const float*)a.k + b * a.sk.b + h * a.sk.h;
-  const float* DS = (const float*)a.ds + (int64_t)bh * Tn * Tn;
-  const Rsrc rK = make_rsrc(K, (uint64_t)Tn * a.sk.t * 4), rS = make_rsrc(DS, (uint64_t)Tn * Tn * 4);
-  float* Ks = lds + wave * PER_WAVE;
-  const int lrow = lane >> 4, lcol = (lane & 15) * 4;
-  const uint32_t vk = (uint32_t)(lrow * a.sk.t + lcol) * 4u;
-  const uint32_t vd = (uint32_t)(qr * Tn + 4 * g) * 4u;  // dS[qr][4g]
-  V4 rk[NV];
-  M::acc_t dsn;
-  auto fetch = [&](int kt) {
-    const int j0 = kt * MT;
-#pragma unroll
-    for (int v = 0; v < NV; ++v) rk[v] = buf_load4(rK, vk, (uint32_t)((j0 + 4 * v) * a.sk.t) * 4u);
-    // lane (c, g), register 4 a + e: dS[qr][j0 + 8 a + 4 g + e]
-#pragma unroll
-    for (int a4 = 0; a4 < NACC / 4; ++a4) {
-      const V4 x = buf_load4(rS, vd, (uint32_t)(j0 + 8 * a4) * 4u);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) dsn[4 * a4 + e] = x[e];
-    }
-  };
-  auto put = [&]() {
-#pragma unroll
-    for (int v = 0; v < NV; ++v) *reinterpret_cast<V4*>(Ks + (4 * v + lrow) * LD + lcol) = rk[v];
-  };
-  auto wave_sync = [] {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  };
-  M::acc_t dq[DP / MT];
-#pragma unroll
-  for (int dt = 0; dt < DP / MT; ++dt) dq[dt] = M::acc_t(0);
-  int kt = wave;
-  M::acc_t dsr = M::acc_t(0);
-  if (kt <= qt) {
-    fetch(kt);
-    put();
-    dsr = dsn;
-  }
-  wave_sync();
-  for (; kt <= qt; kt += 4) {
-    const bool more = kt + 4 <= qt;
-    if (more) fetch(kt + 4);
-    if (kt == qt) {  // the diagonal tile: entries above it were never written
-      const int lim = c - 4 * g;  // key 8a + 4g + e <= query c
-#pragma unroll
-      for (int a4 = 0; a4 < NACC / 4; ++a4)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dsr[4 * a4 + e] = 8 * a4 + e <= lim ? dsr[4 * a4 + e] : 0.f;
-    }
-    // dQ^T += K^T dS^T
-    mma_lds_t_regs<float, DP>(dq, Ks, 0, dsr, g, c);
-    wave_sync();
-    if (more) put();
-    wave_sync();
-    dsr = dsn;
-  }
-  // the four waves' partial dQ as [query][d] rows, added in wave order
-  __syncthreads();
-  float* R = lds + wave * PER_WAVE;
-#pragma unroll
-  for (int dt = 0; dt < DP / MT; ++dt)
-#pragma unroll
-    for (int a4 = 0; a4 < NACC / 4; ++a4) {
-      V4 x;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x[e] = dq[dt][4 * a4 + e];
-      *reinterpret_cast<V4*>(R + c * LDR + dt * MT + M::row(4 * a4, g)) = x;
-    }
-  __syncthreads();
-  float* DQ = (float*)a.dq + b * a.sdq.b + h * a.sdq.h;
-  const float scale = (float)a.scale;
-  const bool ovec = a.ovec != 0;
-  for (int f = threadIdx.x; f < MT * DP / 4; f += 256) {
-    const int q = f / (DP / 4), d = (f % (DP / 4)) * 4;
-    const int o = q * LDR + d;
-    V4 sq = *reinterpret_cast<const V4*>(lds + o);
-#pragma unroll
-    for (int w = 1; w < 4; ++w) sq += *reinterpret_cast<const V4*>(lds + w * PER_WAVE + o);
-    sq *= scale;
-    float* pq = DQ + (int64_t)(q0 + q) * a.sdq.t + d;
-    if (ovec) {
-      *reinterpret_cast<V4*>(pq) = sq;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) pq[e] = sq[e];
-    }
-  }
-}
-
 template <typename T, int DP, bool FAST>
 __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
   using M = AM<T>;
@@ -1338,6 +1025,444 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
 // dS = P * (dP - rowsum(dP * P)) * scale, dQ = dS K, dK = dS^T Q -- dtrain's
 // products (autograd.py:226-246), one batch element at a time. One block per
 // row for the row passes, fixed reduction order.
+// ----------------------------- backward on 16 x 16 tiles over paired ranges
+// MFMA 16 x 16 x 4 in both dtypes: lane (g, c), g = lane / 16, supplies
+// column c (B operand) or row c (A operand) at k-slot g, and holds column c,
+// rows row(i, g) (i = 0..3) of the 16 x 16 result.
+template <typename T>
+struct A16;
+template <>
+struct A16<float> {
+  typedef float acc_t __attribute__((ext_vector_type(4)));
+  typedef float vec_t __attribute__((ext_vector_type(4)));
+  static constexpr int VEC = 4;
+  static __device__ __forceinline__ acc_t mma(float a, float b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int i, int g) { return 4 * g + i; }
+};
+template <>
+struct A16<double> {
+  typedef double acc_t __attribute__((ext_vector_type(4)));
+  typedef double vec_t __attribute__((ext_vector_type(2)));
+  static constexpr int VEC = 2;
+  static __device__ __forceinline__ acc_t mma(double a, double b, acc_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ int row(int i, int g) { return g + 4 * i; }
+};
+
+template <typename VT>
+__device__ __forceinline__ VT buf_load_v(Rsrc r, uint32_t voff, uint32_t soff) {
+  static_assert(sizeof(VT) == 16, "16-byte vectors");
+  return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ float buf_load_s(Rsrc r, uint32_t voff, uint32_t soff, float) {
+  return buf_load1(r, voff, soff);
+}
+__device__ __forceinline__ double buf_load_s(Rsrc r, uint32_t voff, uint32_t soff, double) {
+  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
+}
+
+// dK (times the softmax scale) and dV of 16 keys from the key pass's
+// accumulators: lane (g, c), tile t, register i holds key k0 + c,
+// d = 4 row(i, g) + t.
+template <typename T>
+__device__ __forceinline__ void store_kv16(const AttnArgs& a, int64_t b, int64_t h, int k0,
+                                           const typename A16<T>::acc_t (&dk)[4],
+                                           const typename A16<T>::acc_t (&dv)[4], int g, int c) {
+  using M = A16<T>;
+  T* DK = (T*)a.dk + b * a.sdk.b + h * a.sdk.h + (int64_t)(k0 + c) * a.sdk.t;
+  T* DV = (T*)a.dv + b * a.sdv.b + h * a.sdv.h + (int64_t)(k0 + c) * a.sdv.t;
+  const T scale = (T)a.scale;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int d = 4 * M::row(i, g);
+    const typename M::acc_t xk = {dk[0][i] * scale, dk[1][i] * scale, dk[2][i] * scale, dk[3][i] * scale};
+    const typename M::acc_t xv = {dv[0][i], dv[1][i], dv[2][i], dv[3][i]};
+    if (a.ovec) {
+#pragma unroll
+      for (int v = 0; v < 4 / M::VEC; ++v) {
+        typename M::vec_t yk, yv;
+#pragma unroll
+        for (int e = 0; e < M::VEC; ++e) {
+          yk[e] = xk[M::VEC * v + e];
+          yv[e] = xv[M::VEC * v + e];
+        }
+        *reinterpret_cast<typename M::vec_t*>(DK + d + M::VEC * v) = yk;
+        *reinterpret_cast<typename M::vec_t*>(DV + d + M::VEC * v) = yv;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        DK[d + t] = xk[t];
+        DV[d + t] = xv[t];
+      }
+    }
+  }
+}
+
+// dQ (times the softmax scale) of 16 queries from the dQ pass's accumulators:
+// lane (g, c), tile t, register i holds row q0 + row(i, g), d = 4 c + t.
+template <typename T>
+__device__ __forceinline__ void store_q16(const AttnArgs& a, int64_t b, int64_t h, int q0,
+                                          const typename A16<T>::acc_t (&dq)[4], int g, int c) {
+  using M = A16<T>;
+  T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h + 4 * c;
+  const T scale = (T)a.scale;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    T* row = DQ + (int64_t)(q0 + M::row(i, g)) * a.sdq.t;
+    const typename M::acc_t x = {dq[0][i] * scale, dq[1][i] * scale, dq[2][i] * scale, dq[3][i] * scale};
+    if (a.ovec) {
+#pragma unroll
+      for (int v = 0; v < 4 / M::VEC; ++v) {
+        typename M::vec_t y;
+#pragma unroll
+        for (int e = 0; e < M::VEC; ++e) y[e] = x[M::VEC * v + e];
+        *reinterpret_cast<typename M::vec_t*>(row + M::VEC * v) = y;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) row[t] = x[t];
+    }
+  }
+}
+
+// dS of the paired-range backward: per (batch, head) the causal 16 x 16
+// tiles (query tile qt >= key tile j) back to back, tile (qt, j) at index
+// qt (qt + 1) / 2 + j, each [query][kpos(key)]. kpos puts the four keys that
+// the dQ pass's lane group g multiplies in MFMA steps 0..3 (keys row(s, g))
+// at 4g .. 4g + 3, so that each lane reads its dS row as 16-byte vectors.
+__host__ __device__ inline int64_t ds16_tiles(int64_t nt) { return nt * (nt + 1) / 2; }
+template <typename T>
+__device__ __forceinline__ int ds16_kpos(int key) {
+  return sizeof(T) == 4 ? key : 4 * (key & 3) + (key >> 2);  // inverse of row(s, g) = 4g + s / g + 4s
+}
+
+// Key pass. Block (bh, p), two waves, for the key tiles j = p and
+// j' = nt - 1 - p of 16 keys (nt = T / 16 tiles, even): key tile j is seen by
+// the nt - p query tiles p .. nt - 1, key tile j' by p + 1, nt + 1 tile pairs
+// in all. Wave 0 takes key tile j with query tiles p .. p + nt/2 - 1; wave 1
+// the rest of key tile j (query tiles p + nt/2 .. nt - 1), then all of key
+// tile j'. Every wave thus carries nt/2 or nt/2 + 1 tile pairs whatever p, and
+// one two-way sum (key tile j's partial dK and dV, wave 0's first) remains.
+// Each lane holds its key's K and V slices in registers; the query tiles'
+// Q and dO rows pass through the wave's own LDS, the next one prefetched into
+// registers. For each tile pair: S = Q K^T and dP = dO V^T, P recomputed from
+// the forward's row max and sum, dS = P * (dP - rowsum(dO * O)) written to the
+// workspace, dV^T += dO^T P and dK^T += Q^T dS.
+// Aligned path only: D = 64, T a multiple of 32, 16-byte access.
+template <typename T>
+__global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kernel(AttnArgs a) {
+  using M = A16<T>;
+  typedef typename M::vec_t VT;
+  typedef typename M::acc_t AT;
+  constexpr int MT = 16, DP = 64, VEC = M::VEC;
+  constexpr int LD = DP + VEC;                 // padded LDS row
+  constexpr int TILE = MT * LD;
+  constexpr int WAVE_LDS = 2 * TILE + 3 * MT;  // Q rows, dO rows, 3 statistics per row
+  constexpr int NV = MT * DP / VEC / 64;       // 16-byte vectors per lane per tile and operand
+  constexpr int RPV = 64 * VEC / DP;           // rows covered by one vector index
+  constexpr int NF = 16 / VEC;                 // vectors of a lane's 16-element K / V slice
+  constexpr int STASH = 2 * 4 * 4 * 64;        // wave 1's partial dK, dV of key tile j, register order
+  __shared__ __attribute__((aligned(16))) T lds[2 * WAVE_LDS + STASH];
+
+  const int bh = blockIdx.x, p = blockIdx.y;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int Tn = (int)a.T, nt = Tn / MT, half = nt / 2;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int kp = ds16_kpos<T>(c);  // this lane's key's place in a dS row
+  const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
+  const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+  const T* Vv = (const T*)a.v + b * a.sv.b + h * a.sv.h;
+  const T* G = (const T*)a.dO + b * a.sdo.b + h * a.sdo.h;
+  const T* RM = (const T*)a.rowmax + (int64_t)bh * Tn;
+  const T* RS = (const T*)a.rowsum + (int64_t)bh * Tn;
+  const T* DR = (const T*)a.drow + (int64_t)bh * Tn;
+  T* DS = (T*)a.ds + (int64_t)bh * ds16_tiles(nt) * (MT * MT);
+  const T sl2 = (T)(a.scale * 1.4426950408889634);
+  constexpr uint32_t S = sizeof(T);
+  const Rsrc rQ = make_rsrc(Q, (uint64_t)Tn * a.sq.t * S), rG = make_rsrc(G, (uint64_t)Tn * a.sdo.t * S);
+  const Rsrc rK = make_rsrc(K, (uint64_t)Tn * a.sk.t * S), rV = make_rsrc(Vv, (uint64_t)Tn * a.sv.t * S);
+  const Rsrc rM = make_rsrc(RM, (uint64_t)Tn * S), rL = make_rsrc(RS, (uint64_t)Tn * S),
+             rD = make_rsrc(DR, (uint64_t)Tn * S);
+  const Rsrc rS = make_rsrc(DS, (uint64_t)ds16_tiles(nt) * MT * MT * S);
+
+  T* Qs = lds + wave * WAVE_LDS;
+  T* Gs = Qs + TILE;
+  T* ST = Qs + 2 * TILE;  // [0, 16): max term, [16, 32): 1 / sum (float64), [32, 48): rowsum(dO * O)
+  T* stash = lds + 2 * WAVE_LDS;
+
+  // this lane's share of a tile's loads: vector v is row RPV v + lrow, columns lcol ..
+  const int lrow = lane / (DP / VEC), lcol = (lane % (DP / VEC)) * VEC;
+  const uint32_t vq = (uint32_t)(lrow * a.sq.t + lcol) * S, vg = (uint32_t)(lrow * a.sdo.t + lcol) * S;
+  const uint32_t vs = (uint32_t)c * S;
+  VT rq[NV], rg[NV];
+  T rm = T(0), rl = T(1), rd = T(0);
+  auto fetch = [&](int qs) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      rq[v] = buf_load_v<VT>(rQ, vq, (uint32_t)((qs + RPV * v) * a.sq.t) * S);
+      rg[v] = buf_load_v<VT>(rG, vg, (uint32_t)((qs + RPV * v) * a.sdo.t) * S);
+    }
+    rm = buf_load_s(rM, vs, (uint32_t)qs * S, T(0));
+    rl = buf_load_s(rL, vs, (uint32_t)qs * S, T(0));
+    rd = buf_load_s(rD, vs, (uint32_t)qs * S, T(0));
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int r = RPV * v + lrow;
+      *reinterpret_cast<VT*>(Qs + r * LD + lcol) = rq[v];
+      *reinterpret_cast<VT*>(Gs + r * LD + lcol) = rg[v];
+    }
+    if (lane < MT) {
+      if constexpr (sizeof(T) == 4) {
+        ST[lane] = rm + log2(rl);
+      } else {
+        ST[lane] = rm;
+        ST[MT + lane] = T(1) / rl;
+      }
+      ST[2 * MT + lane] = rd;
+    }
+  };
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+
+  AT dk[4], dv[4];
+  const int nseg = wave == 0 ? 1 : 2;
+  for (int seg = 0; seg < nseg; ++seg) {
+    const int j = seg == 0 ? p : nt - 1 - p;
+    const int qa = seg == 1 ? j : (wave == 0 ? p : p + half);
+    const int qb = wave == 0 ? p + half - 1 : nt - 1;
+    const int k0 = j * MT;
+    // this lane's key k0 + c: elements 16 g .. 16 g + 15 of its K and V rows
+    VT kf[NF], vf[NF];
+    const uint32_t kl = (uint32_t)((k0 + c) * a.sk.t + 16 * g) * S, vl = (uint32_t)((k0 + c) * a.sv.t + 16 * g) * S;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      kf[f] = buf_load_v<VT>(rK, kl, (uint32_t)(16 * f));
+      vf[f] = buf_load_v<VT>(rV, vl, (uint32_t)(16 * f));
+    }
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) dk[dt] = dv[dt] = AT(0);
+    fetch(qa * MT);
+    put();
+    drain_vm();  // K and V slices in: the loop's waits then cover only its own prefetch
+    wave_sync();
+    for (int qt = qa; qt <= qb; ++qt) {
+      const int qs = qt * MT;
+      const bool more = qt < qb;
+      if (more) fetch(qs + MT);
+      // S(r, key) and dP(r, key): rows r = the tile's queries, column c = this lane's key
+      AT s = AT(0), dp = AT(0);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const VT x = *reinterpret_cast<const VT*>(Qs + c * LD + 16 * g + VEC * f);
+        const VT y = *reinterpret_cast<const VT*>(Gs + c * LD + 16 * g + VEC * f);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          s = M::mma(x[e], kf[f][e], s);
+          dp = M::mma(y[e], vf[f][e], dp);
+        }
+      }
+      auto probs = [&](auto maskc) {
+        constexpr bool MASK = decltype(maskc)::value;  // the diagonal tile
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = M::row(i, g);
+          T pr;
+          if constexpr (sizeof(T) == 4)
+            pr = ex2(__builtin_fmaf(s[i], sl2, -ST[r]));
+          else
+            pr = ex2(s[i] * sl2 - ST[r]) * ST[MT + r];
+          if constexpr (MASK) pr = c > r ? T(0) : pr;  // key above the query: masked
+          s[i] = pr;
+          dp[i] = pr * (dp[i] - ST[2 * MT + r]);
+        }
+      };
+      if (qt == j)
+        probs(std::true_type());
+      else
+        probs(std::false_type());
+      // dS tile (qt, j), [query][kpos(key)]: queries row(i, g), this lane's key
+      const uint32_t tb = (uint32_t)((qt * (qt + 1) / 2 + j) * (MT * MT)) * S;
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) buf_store1(dp[i], rS, (uint32_t)(M::row(i, g) * MT + kp) * S, tb);
+      } else {
+        // float64: plain stores (a 64-bit buffer store of a vector element
+        // was lowered to four stores of one register)
+        T* dst = DS + (int64_t)(qt * (qt + 1) / 2 + j) * (MT * MT) + kp;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[M::row(i, g) * MT] = dp[i];
+      }
+      // dV^T += dO^T P ; dK^T += Q^T dS: result tile t, row r is d = 4 r + t,
+      // column = this lane's key, so a lane's A operands are dO and Q rows
+      // row(i, g), d = 4c .. 4c + 3 (16-byte reads)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = M::row(i, g);
+        VT gv[4 / VEC], qv[4 / VEC];
+#pragma unroll
+        for (int v = 0; v < 4 / VEC; ++v) {
+          gv[v] = *reinterpret_cast<const VT*>(Gs + r * LD + 4 * c + VEC * v);
+          qv[v] = *reinterpret_cast<const VT*>(Qs + r * LD + 4 * c + VEC * v);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          dv[t] = M::mma(gv[t / VEC][t % VEC], s[i], dv[t]);
+          dk[t] = M::mma(qv[t / VEC][t % VEC], dp[i], dk[t]);
+        }
+      }
+      wave_sync();
+      if (more) put();
+      wave_sync();
+    }
+    if (wave == 1) {
+      if (seg == 0) {  // key tile j's later query tiles: handed to wave 0
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            stash[(dt * 4 + i) * 64 + lane] = dk[dt][i];
+            stash[(16 + dt * 4 + i) * 64 + lane] = dv[dt][i];
+          }
+      } else {
+        store_kv16<T>(a, b, h, k0, dk, dv, g, c);
+      }
+    }
+  }
+  __syncthreads();  // wave 1's partial of key tile j is in the stash
+  if (wave == 0) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dk[dt][i] += stash[(dt * 4 + i) * 64 + lane];
+        dv[dt][i] += stash[(16 + dt * 4 + i) * 64 + lane];
+      }
+    store_kv16<T>(a, b, h, p * MT, dk, dv, g, c);
+  }
+}
+
+// dQ pass. Block (bh, bq) has eight waves for four pairs of query tiles:
+// wave w < 4 takes tile i = 4 bq + w, wave w + 4 its mirror i' = nt - 1 - i
+// (i < nt / 2). The two see i + 1 and nt - i key tiles, nt + 1 in all, and
+// waves w and w + 4 share a SIMD, so every SIMD carries the same work. The
+// block's waves walk the key tiles together, two per step (j = 2 it, 2 it + 1,
+// up to nt - 1 - 4 bq), the step's K tiles staged in LDS once for all eight;
+// a wave adds dS(q, j) K_j for the key tiles its query tile q sees. The next
+// step's K and dS tiles are loaded at the top of a step and consumed at the
+// next one. Output column c of the MFMA result tile t is d = 4 c + t, so that
+// a lane's B operands (a K row, d = 4c .. 4c + 3, from LDS), its A operands (a
+// dS row, stored [query][kpos(key)]) and its dQ rows are 16-byte vectors.
+template <typename T>
+__global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
+  using M = A16<T>;
+  typedef typename M::vec_t VT;
+  typedef typename M::acc_t AT;
+  constexpr int MT = 16, DP = 64, VEC = M::VEC;
+  constexpr int LD = DP + VEC;
+  constexpr int KT = 2;                         // key tiles per step
+  constexpr int STEP = KT * MT * LD;            // one step's K rows in LDS
+  constexpr int NTH = 512;
+  constexpr int KV = KT * MT * DP / VEC / NTH;  // K vectors per thread per step
+  constexpr int SL = 4 / VEC;                   // vectors of a lane's dS row per tile
+  static_assert(KV * NTH * VEC == KT * MT * DP, "K rows: whole vectors per thread");
+  __shared__ __attribute__((aligned(16))) T lds[2 * STEP];
+
+  const int bh = blockIdx.x, bq = blockIdx.y;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int Tn = (int)a.T, nt = Tn / MT, half = nt / 2;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, c = lane & 15;
+  const int i0 = 4 * bq + (wave & 3);
+  const bool live = i0 < half;
+  const int qt = wave < 4 ? i0 : nt - 1 - i0;  // this wave's query tile
+  const int jend = nt - 1 - 4 * bq;            // the block's last key tile (the longest mirror tile)
+  const int nstep = jend / KT + 1;
+  constexpr uint32_t S = sizeof(T);
+  const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
+  const T* DS = (const T*)a.ds + (int64_t)bh * ds16_tiles(nt) * (MT * MT);
+  const Rsrc rK = make_rsrc(K, (uint64_t)Tn * a.sk.t * S);
+  const Rsrc rS = make_rsrc(DS, (uint64_t)ds16_tiles(nt) * MT * MT * S);
+
+  int kro[KV], kco[KV];
+#pragma unroll
+  for (int v = 0; v < KV; ++v) {
+    const int f = (int)threadIdx.x + NTH * v;
+    kro[v] = f / (DP / VEC);
+    kco[v] = (f % (DP / VEC)) * VEC;
+  }
+  const uint32_t svo = (uint32_t)(c * MT + 4 * g) * S;  // dS row c, kpos 4g .. 4g + 3
+  // tiles clamped to ones that exist, so every step issues the same loads (a
+  // non-live wave reads the block's longest tile)
+  const int rq = live ? qt : jend;
+  VT rk[KV], nx[KT][SL], xs[KT][SL];
+  auto fetch = [&](int it) {
+    const int j0 = KT * it;
+    // rows past the last key tile (odd tile counts) read the last tile again
+#pragma unroll
+    for (int v = 0; v < KV; ++v) {
+      const int row = j0 * MT + kro[v];
+      const int rowc = row < (jend + 1) * MT ? row : jend * MT + (kro[v] % MT);
+      rk[v] = buf_load_v<VT>(rK, (uint32_t)kco[v] * S, (uint32_t)(rowc * a.sk.t) * S);
+    }
+#pragma unroll
+    for (int u = 0; u < KT; ++u) {
+      const int j = j0 + u;
+      const uint32_t tb = (uint32_t)((rq * (rq + 1) / 2 + (j < rq ? j : rq)) * (MT * MT)) * S;
+#pragma unroll
+      for (int v = 0; v < SL; ++v) nx[u][v] = buf_load_v<VT>(rS, svo, tb + 16 * v);
+    }
+  };
+  auto put = [&](T* Ks) {
+#pragma unroll
+    for (int v = 0; v < KV; ++v) *reinterpret_cast<VT*>(Ks + kro[v] * LD + kco[v]) = rk[v];
+#pragma unroll
+    for (int u = 0; u < KT; ++u)
+#pragma unroll
+      for (int v = 0; v < SL; ++v) xs[u][v] = nx[u][v];
+  };
+  AT dq[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) dq[t] = AT(0);
+  fetch(0);
+  put(lds);
+  __syncthreads();
+  for (int it = 0; it < nstep; ++it) {
+    const T* Ks = lds + (it & 1) * STEP;
+    const bool more = it + 1 < nstep;
+    if (more) fetch(it + 1);
+#pragma unroll
+    for (int u = 0; u < KT; ++u) {
+      const int j = KT * it + u;
+      if (live && j <= qt) {
+        // dQ(r, d = 4c + t) += sum over the tile's keys of dS(r, key) K(key, d)
+        VT kv[4][4 / VEC];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int v = 0; v < 4 / VEC; ++v)
+            kv[q][v] = *reinterpret_cast<const VT*>(Ks + (u * MT + M::row(q, g)) * LD + 4 * c + VEC * v);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) dq[t] = M::mma(xs[u][q / VEC][q % VEC], kv[q][t / VEC][t % VEC], dq[t]);
+      }
+    }
+    if (more) put(lds + ((it + 1) & 1) * STEP);
+    __syncthreads();
+  }
+  if (live) store_q16<T>(a, b, h, qt * MT, dq, g, c);
+}
+
 template <typename T>
 __device__ __forceinline__ T block_reduce_256(T x, T* red, bool is_max) {
 #pragma unroll
@@ -1550,10 +1675,16 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
   int rc = drow_in ? 0 : pool_alloc(&drow, (size_t)rows * sizeof(T));
   if (rc) return rc;
   a.drow = drow_in ? const_cast<void*>(drow_in) : drow;
-  // dS for the dQ pass: B*H*T*T elements, up to g_max_ds_bytes; beyond that
-  // the dQ pass recomputes S, P and dP itself.
+  // float32, D = 64, T a multiple of 32, 16-byte access: the paired-range
+  // kernels on 16 x 16 tiles, with dS in causal tiles (float64 keeps the
+  // 64-key blocks: its key pass needs twice the registers)
+  const bool pair16 = std::is_same<T, float>::value && a.vec && a.D == 64 && a.T % 32 == 0;
+  // dS for the dQ pass: B*H*T*T elements (the causal tiles only on the
+  // paired-range path), up to g_max_ds_bytes; beyond that the dQ pass
+  // recomputes S, P and dP itself.
   a.ds = nullptr;
-  const double ds_bytes = (double)a.B * a.H * a.T * a.T * sizeof(T);
+  const double ds_bytes = pair16 ? (double)a.B * a.H * (double)ds16_tiles(a.T / 16) * 256.0 * sizeof(T)
+                                 : (double)a.B * a.H * a.T * a.T * sizeof(T);
   if (ds_bytes <= (double)g_max_ds_bytes) {
     rc = pool_alloc(&a.ds, (size_t)ds_bytes);
     if (rc) {
@@ -1574,24 +1705,23 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
       attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
     }
     dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
-    // float32, D = 64, T a multiple of 32: one key (query) tile per block with
-    // independent waves; otherwise 128-key (128-query) blocks
-    const bool kv1 = std::is_same<T, float>::value && a.ds && a.vec && a.D == 64 && a.T % 32 == 0;
-    if (kv1) {
-      dim3 g1((unsigned)(a.T / 32), (unsigned)(a.B * a.H));
-      attn_bwd_kv1_kernel<64><<<g1, 256, 0, stream()>>>(a);
-    } else if (a.ds) {
-      DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
-    } else {  // the aligned key-block pass writes dS unconditionally
-      DP_SWITCH_F(dp, attn_bwd_kv_kernel, T, grid, false)
-    }
-    if (kv1) {
-      dim3 g1((unsigned)(a.T / 32), (unsigned)(a.B * a.H));
-      attn_bwd_q1_kernel<64><<<g1, 256, 0, stream()>>>(a);
-    } else if (a.ds) {
-      DP_SWITCH(dp, attn_bwd_q_ds_kernel, T, grid)
+    if (pair16 && a.ds) {
+      const unsigned pairs = (unsigned)(a.T / 32);
+      attn_bwd_kvp_kernel<T><<<dim3((unsigned)(a.B * a.H), pairs), 128, 0, stream()>>>(a);
+      attn_bwd_qp_kernel<T><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, 4)), 512, 0, stream()>>>(a);
     } else {
-      DP_SWITCH(dp, attn_bwd_q_kernel, T, grid)
+      // 128-key (128-query) blocks; the dQ pass reads dS, or recomputes it
+      // above the workspace bound
+      if (a.ds) {
+        DP_SWITCH(dp, attn_bwd_kv_kernel, T, grid)
+      } else {  // the aligned key-block pass writes dS unconditionally
+        DP_SWITCH_F(dp, attn_bwd_kv_kernel, T, grid, false)
+      }
+      if (a.ds) {
+        DP_SWITCH(dp, attn_bwd_q_ds_kernel, T, grid)
+      } else {
+        DP_SWITCH(dp, attn_bwd_q_kernel, T, grid)
+      }
     }
   }
   hipError_t le = hipGetLastError();
