@@ -15,9 +15,11 @@ dtrain/ddp.py on one GPU. Same constructor, attributes and step protocol:
 * `no_sync()` skips all of this for gradient-accumulation micro-steps;
 * `finish()` zero-fills missing gradients (ddp.py:88-94), reduces what is left,
   and points every `param.grad` at its slice of the averaged gradients
-  (ddp.py:104-110). The average is
-  (((g_0 + g_1) + g_2) + ... + g_{W-1}) * (1.0 / W), dtrain's `--algo direct`
-  order (comm.py:374-391), bit-exact to NumPy. `grad_sq` (a 1-element
+  (ddp.py:104-110). The average is the rank-order sum times (1.0 / W), in
+  the order of dtrain's all-reduce for `algo`: "ring" (its default: chunk c
+  of partition(n, W) of a bucket's buffer summed starting at rank c,
+  comm.py:292-303, 342-372) or "direct" ((((g_0 + g_1) + g_2) + ...),
+  comm.py:374-391), bit-exact to NumPy either way. `grad_sq` (a 1-element
   float64 device array) is the deterministic float64 sum of squares of all
   averaged gradients after `finish()`, the global-norm input of
   dtrain/train.py:155-156. It is one pass over the flat averaged buffer, so
@@ -135,8 +137,10 @@ class DDP:
     # once it holds MERGE_BYTES of gradients, or at finish(): the average is
     # elementwise with each element's own rank order, so the grouping changes
     # no value, and a 1 MiB bucket alone is too short a launch to reach the
-    # memory bandwidth. MAX_SEGS: the rank-order segments one launch takes.
-    MERGE_BYTES = 32 << 20
+    # memory bandwidth. The replicas share one GPU and one stream, so an
+    # earlier launch would overlap nothing: runs are as long as the rank-order
+    # segments allow. MAX_SEGS: the rank-order segments one launch takes.
+    MERGE_BYTES = 256 << 20
     MAX_SEGS = 16
 
     def _reduce(self, b: _Bucket):
