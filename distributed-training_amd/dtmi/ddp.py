@@ -150,7 +150,8 @@ class DDP:
         p = self._pend
         if p:
             lo, hi = min(x.lo for x in p), max(x.hi for x in p)
-            nseg = sum(len(x.segments or ((0, 0),)) for x in p) + len(b.segments or ((0, 0),))
+            # rank-order segments of the run (rank-0-first buckets carry none)
+            nseg = sum(len(x.segments) for x in p + [b] if x.segments)
             if not (b.hi == lo or b.lo == hi) or nseg > self.MAX_SEGS:
                 self._flush()
         self._pend.append(b)

@@ -74,6 +74,25 @@ def test_forward_over_many_key_tiles(dev, T):
             assert bits_equal(x, y)
 
 
+@pytest.mark.parametrize("T", [32, 64, 96, 160, 288, 352])
+def test_backward_paired_ranges_at_every_pair_count(dev, T):
+    """The float32 paired-range backward (16 x 16 tiles, key tile j with its
+    mirror, dQ-pass blocks of four query-tile pairs) at T / 32 = 1, 2, 3, 5,
+    9 and 11 pairs: blocks whose last waves have no pair, one and two key
+    tiles per dQ step, a single pair; dQ, dK and dV against the oracle, and
+    identical bits over repeated calls."""
+    D, K = _dev()
+    rng = np.random.default_rng(T + 7)
+    q, k, v, g = (rng.standard_normal((2, 3, T, 64)).astype(np.float32) for _ in range(4))
+    _check(D, K, q, k, v, g, np.float32)
+    dq_, dk_, dv_, dg_ = D.from_numpy(q), D.from_numpy(k), D.from_numpy(v), D.from_numpy(g)
+    o, rmax, rsum = K.attn_fwd(dq_, dk_, dv_)
+    runs = [tuple(x.numpy() for x in K.attn_bwd(dq_, dk_, dv_, o, dg_, rmax, rsum)) for _ in range(3)]
+    for r in runs[1:]:
+        for x, y in zip(runs[0], r):
+            assert bits_equal(x, y)
+
+
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
 def test_attention_golden_from_dtrain(dev, golden, dt):
     D, K = _dev()
