@@ -1026,9 +1026,9 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_kernel(AttnArgs a) {
 // products (autograd.py:226-246), one batch element at a time. One block per
 // row for the row passes, fixed reduction order.
 // ----------------------------- backward on 16 x 16 tiles over paired ranges
-// MFMA 16 x 16 x 4 in both dtypes: lane (g, c), g = lane / 16, supplies
-// column c (B operand) or row c (A operand) at k-slot g, and holds column c,
-// rows row(i, g) (i = 0..3) of the 16 x 16 result.
+// MFMA 16 x 16 x 4 (float32): lane (g, c), g = lane / 16, supplies column c
+// (B operand) or row c (A operand) at k-slot g, and holds column c, rows
+// row(i, g) = 4 g + i (i = 0..3) of the 16 x 16 result.
 template <typename T>
 struct A16;
 template <>
@@ -1041,29 +1041,12 @@ struct A16<float> {
   }
   static __device__ __forceinline__ int row(int i, int g) { return 4 * g + i; }
 };
-template <>
-struct A16<double> {
-  typedef double acc_t __attribute__((ext_vector_type(4)));
-  typedef double vec_t __attribute__((ext_vector_type(2)));
-  static constexpr int VEC = 2;
-  static __device__ __forceinline__ acc_t mma(double a, double b, acc_t c) {
-    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ int row(int i, int g) { return g + 4 * i; }
-};
 
 template <typename VT>
 __device__ __forceinline__ VT buf_load_v(Rsrc r, uint32_t voff, uint32_t soff) {
   static_assert(sizeof(VT) == 16, "16-byte vectors");
   return __builtin_bit_cast(VT, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
 }
-__device__ __forceinline__ float buf_load_s(Rsrc r, uint32_t voff, uint32_t soff, float) {
-  return buf_load1(r, voff, soff);
-}
-__device__ __forceinline__ double buf_load_s(Rsrc r, uint32_t voff, uint32_t soff, double) {
-  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
-}
-
 // dK (times the softmax scale) and dV of 16 keys from the key pass's
 // accumulators: lane (g, c), tile t, register i holds key k0 + c,
 // d = 4 row(i, g) + t.
@@ -1131,14 +1114,10 @@ __device__ __forceinline__ void store_q16(const AttnArgs& a, int64_t b, int64_t 
 
 // dS of the paired-range backward: per (batch, head) the causal 16 x 16
 // tiles (query tile qt >= key tile j) back to back, tile (qt, j) at index
-// qt (qt + 1) / 2 + j, each [query][kpos(key)]. kpos puts the four keys that
-// the dQ pass's lane group g multiplies in MFMA steps 0..3 (keys row(s, g))
-// at 4g .. 4g + 3, so that each lane reads its dS row as 16-byte vectors.
+// qt (qt + 1) / 2 + j, each [query][key], so that a dQ-pass lane (query c)
+// reads the four keys row(s, g) = 4g .. 4g + 3 it multiplies in MFMA steps
+// s = 0..3 as one 16-byte vector.
 __host__ __device__ inline int64_t ds16_tiles(int64_t nt) { return nt * (nt + 1) / 2; }
-template <typename T>
-__device__ __forceinline__ int ds16_kpos(int key) {
-  return sizeof(T) == 4 ? key : 4 * (key & 3) + (key >> 2);  // inverse of row(s, g) = 4g + s / g + 4s
-}
 
 // Key pass. Block (bh, p), two waves, for the key tiles j = p and
 // j' = nt - 1 - p of 16 keys (nt = T / 16 tiles, even): key tile j is seen by
@@ -1152,16 +1131,17 @@ __device__ __forceinline__ int ds16_kpos(int key) {
 // registers. For each tile pair: S = Q K^T and dP = dO V^T, P recomputed from
 // the forward's row max and sum, dS = P * (dP - rowsum(dO * O)) written to the
 // workspace, dV^T += dO^T P and dK^T += Q^T dS.
-// Aligned path only: D = 64, T a multiple of 32, 16-byte access.
+// Aligned float32 path only: D = 64, T a multiple of 32, 16-byte access.
 template <typename T>
-__global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(128, 3) attn_bwd_kvp_kernel(AttnArgs a) {
+  static_assert(sizeof(T) == 4, "float32 only");
   using M = A16<T>;
   typedef typename M::vec_t VT;
   typedef typename M::acc_t AT;
   constexpr int MT = 16, DP = 64, VEC = M::VEC;
   constexpr int LD = DP + VEC;                 // padded LDS row
   constexpr int TILE = MT * LD;
-  constexpr int WAVE_LDS = 2 * TILE + 3 * MT;  // Q rows, dO rows, 3 statistics per row
+  constexpr int WAVE_LDS = 2 * TILE + 2 * MT;  // Q rows, dO rows, 2 statistics per row
   constexpr int NV = MT * DP / VEC / 64;       // 16-byte vectors per lane per tile and operand
   constexpr int RPV = 64 * VEC / DP;           // rows covered by one vector index
   constexpr int NF = 16 / VEC;                 // vectors of a lane's 16-element K / V slice
@@ -1173,7 +1153,6 @@ __global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kern
   const int Tn = (int)a.T, nt = Tn / MT, half = nt / 2;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, c = lane & 15;
-  const int kp = ds16_kpos<T>(c);  // this lane's key's place in a dS row
   const T* Q = (const T*)a.q + b * a.sq.b + h * a.sq.h;
   const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
   const T* Vv = (const T*)a.v + b * a.sv.b + h * a.sv.h;
@@ -1192,7 +1171,7 @@ __global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kern
 
   T* Qs = lds + wave * WAVE_LDS;
   T* Gs = Qs + TILE;
-  T* ST = Qs + 2 * TILE;  // [0, 16): max term, [16, 32): 1 / sum (float64), [32, 48): rowsum(dO * O)
+  T* ST = Qs + 2 * TILE;  // [0, 16): max + log2(sum), [16, 32): rowsum(dO * O)
   T* stash = lds + 2 * WAVE_LDS;
 
   // this lane's share of a tile's loads: vector v is row RPV v + lrow, columns lcol ..
@@ -1207,9 +1186,9 @@ __global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kern
       rq[v] = buf_load_v<VT>(rQ, vq, (uint32_t)((qs + RPV * v) * a.sq.t) * S);
       rg[v] = buf_load_v<VT>(rG, vg, (uint32_t)((qs + RPV * v) * a.sdo.t) * S);
     }
-    rm = buf_load_s(rM, vs, (uint32_t)qs * S, T(0));
-    rl = buf_load_s(rL, vs, (uint32_t)qs * S, T(0));
-    rd = buf_load_s(rD, vs, (uint32_t)qs * S, T(0));
+    rm = buf_load1(rM, vs, (uint32_t)qs * S);
+    rl = buf_load1(rL, vs, (uint32_t)qs * S);
+    rd = buf_load1(rD, vs, (uint32_t)qs * S);
   };
   auto put = [&]() {
 #pragma unroll
@@ -1219,13 +1198,8 @@ __global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kern
       *reinterpret_cast<VT*>(Gs + r * LD + lcol) = rg[v];
     }
     if (lane < MT) {
-      if constexpr (sizeof(T) == 4) {
-        ST[lane] = rm + log2(rl);
-      } else {
-        ST[lane] = rm;
-        ST[MT + lane] = T(1) / rl;
-      }
-      ST[2 * MT + lane] = rd;
+      ST[lane] = rm + log2(rl);
+      ST[MT + lane] = rd;
     }
   };
   auto wave_sync = [] {
@@ -1276,32 +1250,20 @@ __global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kern
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = M::row(i, g);
-          T pr;
-          if constexpr (sizeof(T) == 4)
-            pr = ex2(__builtin_fmaf(s[i], sl2, -ST[r]));
-          else
-            pr = ex2(s[i] * sl2 - ST[r]) * ST[MT + r];
+          T pr = ex2(__builtin_fmaf(s[i], sl2, -ST[r]));
           if constexpr (MASK) pr = c > r ? T(0) : pr;  // key above the query: masked
           s[i] = pr;
-          dp[i] = pr * (dp[i] - ST[2 * MT + r]);
+          dp[i] = pr * (dp[i] - ST[MT + r]);
         }
       };
       if (qt == j)
         probs(std::true_type());
       else
         probs(std::false_type());
-      // dS tile (qt, j), [query][kpos(key)]: queries row(i, g), this lane's key
+      // dS tile (qt, j), [query][key]: queries row(i, g), this lane's key
       const uint32_t tb = (uint32_t)((qt * (qt + 1) / 2 + j) * (MT * MT)) * S;
-      if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) buf_store1(dp[i], rS, (uint32_t)(M::row(i, g) * MT + kp) * S, tb);
-      } else {
-        // float64: plain stores (a 64-bit buffer store of a vector element
-        // was lowered to four stores of one register)
-        T* dst = DS + (int64_t)(qt * (qt + 1) / 2 + j) * (MT * MT) + kp;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) dst[M::row(i, g) * MT] = dp[i];
-      }
+      for (int i = 0; i < 4; ++i) buf_store1(dp[i], rS, (uint32_t)(M::row(i, g) * MT + c) * S, tb);
       // dV^T += dO^T P ; dK^T += Q^T dS: result tile t, row r is d = 4 r + t,
       // column = this lane's key, so a lane's A operands are dO and Q rows
       // row(i, g), d = 4c .. 4c + 3 (16-byte reads)
@@ -1361,9 +1323,10 @@ __global__ void __launch_bounds__(128, sizeof(T) == 4 ? 3 : 2) attn_bwd_kvp_kern
 // step's K and dS tiles are loaded at the top of a step and consumed at the
 // next one. Output column c of the MFMA result tile t is d = 4 c + t, so that
 // a lane's B operands (a K row, d = 4c .. 4c + 3, from LDS), its A operands (a
-// dS row, stored [query][kpos(key)]) and its dQ rows are 16-byte vectors.
+// dS row, stored [query][key]) and its dQ rows are 16-byte vectors.
 template <typename T>
 __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
+  static_assert(sizeof(T) == 4, "float32 only");
   using M = A16<T>;
   typedef typename M::vec_t VT;
   typedef typename M::acc_t AT;
@@ -1400,7 +1363,7 @@ __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
     kro[v] = f / (DP / VEC);
     kco[v] = (f % (DP / VEC)) * VEC;
   }
-  const uint32_t svo = (uint32_t)(c * MT + 4 * g) * S;  // dS row c, kpos 4g .. 4g + 3
+  const uint32_t svo = (uint32_t)(c * MT + 4 * g) * S;  // dS row c, keys 4g .. 4g + 3
   // tiles clamped to ones that exist, so every step issues the same loads (a
   // non-live wave reads the block's longest tile)
   const int rq = live ? qt : jend;
@@ -1706,9 +1669,11 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
     }
     dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
     if (pair16 && a.ds) {
-      const unsigned pairs = (unsigned)(a.T / 32);
-      attn_bwd_kvp_kernel<T><<<dim3((unsigned)(a.B * a.H), pairs), 128, 0, stream()>>>(a);
-      attn_bwd_qp_kernel<T><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, 4)), 512, 0, stream()>>>(a);
+      if constexpr (std::is_same<T, float>::value) {
+        const unsigned pairs = (unsigned)(a.T / 32);
+        attn_bwd_kvp_kernel<T><<<dim3((unsigned)(a.B * a.H), pairs), 128, 0, stream()>>>(a);
+        attn_bwd_qp_kernel<T><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, 4)), 512, 0, stream()>>>(a);
+      }
     } else {
       // 128-key (128-query) blocks; the dQ pass reads dS, or recomputes it
       // above the workspace bound
