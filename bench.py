@@ -337,12 +337,25 @@ def _threads():
         return int(os.environ.get("OMP_NUM_THREADS", "1"))
 
 
+WARM_S = 0.5  # least warm-up time of a microbenchmark
+
+
 def _timed(a, fn, families):
     """Wall time of `steps` uninstrumented calls, then per-family kernel time
-    from `steps` more calls with HIP events around every launch."""
+    from `steps` more calls with HIP events around every launch. The warm-up
+    is `warmup` calls and at least WARM_S seconds: a GPU that comes out of
+    idle raises its clock over the first ~50 ms of work (the float32 attention
+    backward at B 8, H 12, T 1024 takes 288 us per call over its first 20
+    calls and 238 us from the second tenth of a second on), so a few short
+    calls would time the ramp instead of the kernel."""
     from dtmi import _lib
-    for _ in range(a.warmup):
+    t0 = time.perf_counter()
+    n = 0
+    while n < a.warmup or time.perf_counter() - t0 < WARM_S:
         fn()
+        n += 1
+        if n % 16 == 0:
+            _lib.sync()
     _lib.sync()
     t0 = time.perf_counter()
     for _ in range(a.steps):

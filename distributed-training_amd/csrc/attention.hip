@@ -1313,23 +1313,31 @@ __global__ void __launch_bounds__(128, 3) attn_bwd_kvp_kernel(AttnArgs a) {
   }
 }
 
-// dQ pass. Block (bh, bq) has eight waves for four pairs of query tiles:
+// dQ pass. Block (bh, bq) has eight waves for NDT pairs of query tiles, each
+// query tile taken by 4 / NDT waves of NDT d-tiles (16 d each). With NDT = 4:
 // wave w < 4 takes tile i = 4 bq + w, wave w + 4 its mirror i' = nt - 1 - i
-// (i < nt / 2). The two see i + 1 and nt - i key tiles, nt + 1 in all, and
-// waves w and w + 4 share a SIMD, so every SIMD carries the same work. The
-// block's waves walk the key tiles together, two per step (j = 2 it, 2 it + 1,
-// up to nt - 1 - 4 bq), the step's K tiles staged in LDS once for all eight;
-// a wave adds dS(q, j) K_j for the key tiles its query tile q sees. The next
-// step's K and dS tiles are loaded at the top of a step and consumed at the
-// next one. Output column c of the MFMA result tile t is d = 4 c + t, so that
-// a lane's B operands (a K row, d = 4c .. 4c + 3, from LDS), its A operands (a
-// dS row, stored [query][key]) and its dQ rows are 16-byte vectors.
-template <typename T>
+// (i < nt / 2); with NDT = 2, waves w and w ^ 1 (w < 4) split tile
+// i = 2 bq + w / 2 into d-tiles 0, 1 and 2, 3, and waves w + 4 its mirror.
+// Tile i and its mirror see i + 1 and nt - i key tiles, nt + 1 in all, and
+// waves w and w + 4 share a SIMD, so every SIMD carries the same work. NDT = 2
+// is for short sequences, where four pairs per block leave the CUs unevenly
+// loaded (B 16, H 12, T 256: 384 blocks on 256 CUs); it reads each dS tile
+// twice. The block's waves walk the key tiles together, two per step (j = 2 it,
+// 2 it + 1, up to the block's longest mirror tile), the step's K tiles staged
+// in LDS once for all eight; a wave adds dS(q, j) K_j for the key tiles its
+// query tile q sees. The next step's K and dS tiles are loaded at the top of a
+// step and consumed at the next one. Output column c of the MFMA result tile t
+// is d = 4 c + t, so that a lane's B operands (a K row, d = 4c + t for its
+// d-tiles t, from LDS), its A operands (a dS row, stored [query][key]) and its
+// dQ rows are vectors.
+template <typename T, int NDT>
 __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
   static_assert(sizeof(T) == 4, "float32 only");
+  static_assert(NDT == 4 || NDT == 2, "d-tiles per wave");
   using M = A16<T>;
   typedef typename M::vec_t VT;
   typedef typename M::acc_t AT;
+  typedef float HT __attribute__((ext_vector_type(NDT)));
   constexpr int MT = 16, DP = 64, VEC = M::VEC;
   constexpr int LD = DP + VEC;
   constexpr int KT = 2;                         // key tiles per step
@@ -1337,6 +1345,7 @@ __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
   constexpr int NTH = 512;
   constexpr int KV = KT * MT * DP / VEC / NTH;  // K vectors per thread per step
   constexpr int SL = 4 / VEC;                   // vectors of a lane's dS row per tile
+  constexpr int SPLIT = 4 / NDT;                // waves per query tile
   static_assert(KV * NTH * VEC == KT * MT * DP, "K rows: whole vectors per thread");
   __shared__ __attribute__((aligned(16))) T lds[2 * STEP];
 
@@ -1345,10 +1354,11 @@ __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
   const int Tn = (int)a.T, nt = Tn / MT, half = nt / 2;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, c = lane & 15;
-  const int i0 = 4 * bq + (wave & 3);
+  const int i0 = NDT * bq + (wave & 3) / SPLIT;
+  const int t0 = ((wave & 3) % SPLIT) * NDT;   // this wave's first d-tile
   const bool live = i0 < half;
   const int qt = wave < 4 ? i0 : nt - 1 - i0;  // this wave's query tile
-  const int jend = nt - 1 - 4 * bq;            // the block's last key tile (the longest mirror tile)
+  const int jend = nt - 1 - NDT * bq;          // the block's last key tile (the longest mirror tile)
   const int nstep = jend / KT + 1;
   constexpr uint32_t S = sizeof(T);
   const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
@@ -1364,13 +1374,10 @@ __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
     kco[v] = (f % (DP / VEC)) * VEC;
   }
   const uint32_t svo = (uint32_t)(c * MT + 4 * g) * S;  // dS row c, keys 4g .. 4g + 3
-  // tiles clamped to ones that exist, so every step issues the same loads (a
-  // non-live wave reads the block's longest tile)
   const int rq = live ? qt : jend;
   VT rk[KV], nx[KT][SL], xs[KT][SL];
   auto fetch = [&](int it) {
     const int j0 = KT * it;
-    // rows past the last key tile (odd tile counts) read the last tile again
 #pragma unroll
     for (int v = 0; v < KV; ++v) {
       const int row = j0 * MT + kro[v];
@@ -1393,9 +1400,9 @@ __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
 #pragma unroll
       for (int v = 0; v < SL; ++v) xs[u][v] = nx[u][v];
   };
-  AT dq[4];
+  AT dq[NDT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) dq[t] = AT(0);
+  for (int t = 0; t < NDT; ++t) dq[t] = AT(0);
   fetch(0);
   put(lds);
   __syncthreads();
@@ -1408,22 +1415,36 @@ __global__ void __launch_bounds__(512, 2) attn_bwd_qp_kernel(AttnArgs a) {
       const int j = KT * it + u;
       if (live && j <= qt) {
         // dQ(r, d = 4c + t) += sum over the tile's keys of dS(r, key) K(key, d)
-        VT kv[4][4 / VEC];
+        HT kv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          kv[q] = *reinterpret_cast<const HT*>(Ks + (u * MT + M::row(q, g)) * LD + 4 * c + t0);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
 #pragma unroll
-          for (int v = 0; v < 4 / VEC; ++v)
-            kv[q][v] = *reinterpret_cast<const VT*>(Ks + (u * MT + M::row(q, g)) * LD + 4 * c + VEC * v);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) dq[t] = M::mma(xs[u][q / VEC][q % VEC], kv[q][t / VEC][t % VEC], dq[t]);
+          for (int t = 0; t < NDT; ++t) dq[t] = M::mma(xs[u][q / VEC][q % VEC], kv[q][t], dq[t]);
       }
     }
     if (more) put(lds + ((it + 1) & 1) * STEP);
     __syncthreads();
   }
-  if (live) store_q16<T>(a, b, h, qt * MT, dq, g, c);
+  if (live) {
+    T* DQ = (T*)a.dq + b * a.sdq.b + h * a.sdq.h + 4 * c + t0;
+    const T scale = (T)a.scale;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      T* row = DQ + (int64_t)(qt * MT + M::row(i, g)) * a.sdq.t;
+      HT x;
+#pragma unroll
+      for (int t = 0; t < NDT; ++t) x[t] = dq[t][i] * scale;
+      if (a.ovec) {
+        *reinterpret_cast<HT*>(row) = x;
+      } else {
+#pragma unroll
+        for (int t = 0; t < NDT; ++t) row[t] = x[t];
+      }
+    }
+  }
 }
 
 template <typename T>
@@ -1672,7 +1693,11 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
       if constexpr (std::is_same<T, float>::value) {
         const unsigned pairs = (unsigned)(a.T / 32);
         attn_bwd_kvp_kernel<T><<<dim3((unsigned)(a.B * a.H), pairs), 128, 0, stream()>>>(a);
-        attn_bwd_qp_kernel<T><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, 4)), 512, 0, stream()>>>(a);
+        // fewer than two four-pair blocks per CU: split the d-tiles instead
+        if ((int64_t)a.B * a.H * cdiv(pairs, 4) < 2 * (int64_t)num_cus())
+          attn_bwd_qp_kernel<T, 2><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, 2)), 512, 0, stream()>>>(a);
+        else
+          attn_bwd_qp_kernel<T, 4><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, 4)), 512, 0, stream()>>>(a);
       }
     } else {
       // 128-key (128-query) blocks; the dQ pass reads dS, or recomputes it

@@ -77,7 +77,7 @@ def test_forward_over_many_key_tiles(dev, T):
 @pytest.mark.parametrize("T", [32, 64, 96, 160, 288, 352])
 def test_backward_paired_ranges_at_every_pair_count(dev, T):
     """The float32 paired-range backward (16 x 16 tiles, key tile j with its
-    mirror, dQ-pass blocks of four query-tile pairs) at T / 32 = 1, 2, 3, 5,
+    mirror, dQ-pass blocks of query-tile pairs) at T / 32 = 1, 2, 3, 5,
     9 and 11 pairs: blocks whose last waves have no pair, one and two key
     tiles per dQ step, a single pair; dQ, dK and dV against the oracle, and
     identical bits over repeated calls."""
@@ -91,6 +91,29 @@ def test_backward_paired_ranges_at_every_pair_count(dev, T):
     for r in runs[1:]:
         for x, y in zip(runs[0], r):
             assert bits_equal(x, y)
+
+
+def test_dq_pass_block_shapes_agree_bit_for_bit(dev):
+    """The float32 dQ pass takes four query-tile pairs per block when there are
+    at least two such blocks per CU, else two pairs with each query tile's
+    d-tiles split over two waves. Both add the key tiles in the same order, so
+    a (batch, head) gets the same bits either way: B 40, H 8, T 256 (640
+    four-pair blocks) against its first two batch elements alone (32 blocks),
+    and those against the oracle."""
+    D, K = _dev()
+    rng = np.random.default_rng(40)
+    q, k, v, g = (rng.standard_normal((40, 8, 256, 64)).astype(np.float32) for _ in range(4))
+
+    def bwd(sl):
+        x = [D.from_numpy(np.ascontiguousarray(t[sl])) for t in (q, k, v, g)]
+        o, rmax, rsum = K.attn_fwd(x[0], x[1], x[2])
+        return [t.numpy() for t in K.attn_bwd(x[0], x[1], x[2], o, x[3], rmax, rsum)]
+    full, part = bwd(slice(0, 40)), bwd(slice(0, 2))
+    for a, b in zip(full, part):
+        assert bits_equal(a[:2], b)
+    o_ref, p, scale = ops.attention_fwd(q[:2], k[:2], v[:2])
+    for a, ref in zip(part, ops.attention_bwd(g[:2], q[:2], k[:2], v[:2], p, scale)):
+        assert rel_err(a, ref) <= TOL[np.float32]
 
 
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
