@@ -1120,9 +1120,10 @@ __device__ __forceinline__ void store_q16(const AttnArgs& a, int64_t b, int64_t 
 __host__ __device__ inline int64_t ds16_tiles(int64_t nt) { return nt * (nt + 1) / 2; }
 
 // Key pass. Block (bh, p), two waves, for the key tiles j = p and
-// j' = nt - 1 - p of 16 keys (nt = T / 16 tiles, even): key tile j is seen by
-// the nt - p query tiles p .. nt - 1, key tile j' by p + 1, nt + 1 tile pairs
-// in all. Wave 0 takes key tile j with query tiles p .. p + nt/2 - 1; wave 1
+// j' = nt - 1 - p of 16 keys (nt = T / 16 tiles, even), then for the pairs
+// p + gridDim.y, ... when the grid is shortened to fit one round of resident
+// blocks: key tile j is seen by the nt - p query tiles p .. nt - 1, key tile
+// j' by p + 1, nt + 1 tile pairs in all. Wave 0 takes key tile j with query tiles p .. p + nt/2 - 1; wave 1
 // the rest of key tile j (query tiles p + nt/2 .. nt - 1), then all of key
 // tile j'. Every wave thus carries nt/2 or nt/2 + 1 tile pairs whatever p, and
 // one two-way sum (key tile j's partial dK and dV, wave 0's first) remains.
@@ -1148,7 +1149,7 @@ __global__ void __launch_bounds__(128, 3) attn_bwd_kvp_kernel(AttnArgs a) {
   constexpr int STASH = 2 * 4 * 4 * 64;        // wave 1's partial dK, dV of key tile j, register order
   __shared__ __attribute__((aligned(16))) T lds[2 * WAVE_LDS + STASH];
 
-  const int bh = blockIdx.x, p = blockIdx.y;
+  const int bh = blockIdx.x;
   const int64_t b = bh / a.H, h = bh % a.H;
   const int Tn = (int)a.T, nt = Tn / MT, half = nt / 2;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1208,108 +1209,113 @@ __global__ void __launch_bounds__(128, 3) attn_bwd_kvp_kernel(AttnArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
 
-  AT dk[4], dv[4];
-  const int nseg = wave == 0 ? 1 : 2;
-  for (int seg = 0; seg < nseg; ++seg) {
-    const int j = seg == 0 ? p : nt - 1 - p;
-    const int qa = seg == 1 ? j : (wave == 0 ? p : p + half);
-    const int qb = wave == 0 ? p + half - 1 : nt - 1;
-    const int k0 = j * MT;
-    // this lane's key k0 + c: elements 16 g .. 16 g + 15 of its K and V rows
-    VT kf[NF], vf[NF];
-    const uint32_t kl = (uint32_t)((k0 + c) * a.sk.t + 16 * g) * S, vl = (uint32_t)((k0 + c) * a.sv.t + 16 * g) * S;
-#pragma unroll
-    for (int f = 0; f < NF; ++f) {
-      kf[f] = buf_load_v<VT>(rK, kl, (uint32_t)(16 * f));
-      vf[f] = buf_load_v<VT>(rV, vl, (uint32_t)(16 * f));
-    }
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) dk[dt] = dv[dt] = AT(0);
-    fetch(qa * MT);
-    put();
-    drain_vm();  // K and V slices in: the loop's waits then cover only its own prefetch
-    wave_sync();
-    for (int qt = qa; qt <= qb; ++qt) {
-      const int qs = qt * MT;
-      const bool more = qt < qb;
-      if (more) fetch(qs + MT);
-      // S(r, key) and dP(r, key): rows r = the tile's queries, column c = this lane's key
-      AT s = AT(0), dp = AT(0);
+  // pairs p = blockIdx.y, + gridDim.y, ...: more than one when the grid would
+  // otherwise run in several rounds of resident blocks
+  for (int p = blockIdx.y; p < half; p += gridDim.y) {
+    AT dk[4], dv[4];
+    const int nseg = wave == 0 ? 1 : 2;
+    for (int seg = 0; seg < nseg; ++seg) {
+      const int j = seg == 0 ? p : nt - 1 - p;
+      const int qa = seg == 1 ? j : (wave == 0 ? p : p + half);
+      const int qb = wave == 0 ? p + half - 1 : nt - 1;
+      const int k0 = j * MT;
+      // this lane's key k0 + c: elements 16 g .. 16 g + 15 of its K and V rows
+      VT kf[NF], vf[NF];
+      const uint32_t kl = (uint32_t)((k0 + c) * a.sk.t + 16 * g) * S, vl = (uint32_t)((k0 + c) * a.sv.t + 16 * g) * S;
 #pragma unroll
       for (int f = 0; f < NF; ++f) {
-        const VT x = *reinterpret_cast<const VT*>(Qs + c * LD + 16 * g + VEC * f);
-        const VT y = *reinterpret_cast<const VT*>(Gs + c * LD + 16 * g + VEC * f);
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          s = M::mma(x[e], kf[f][e], s);
-          dp = M::mma(y[e], vf[f][e], dp);
-        }
+        kf[f] = buf_load_v<VT>(rK, kl, (uint32_t)(16 * f));
+        vf[f] = buf_load_v<VT>(rV, vl, (uint32_t)(16 * f));
       }
-      auto probs = [&](auto maskc) {
-        constexpr bool MASK = decltype(maskc)::value;  // the diagonal tile
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) dk[dt] = dv[dt] = AT(0);
+      fetch(qa * MT);
+      put();
+      drain_vm();  // K and V slices in: the loop's waits then cover only its own prefetch
+      wave_sync();
+      for (int qt = qa; qt <= qb; ++qt) {
+        const int qs = qt * MT;
+        const bool more = qt < qb;
+        if (more) fetch(qs + MT);
+        // S(r, key) and dP(r, key): rows r = the tile's queries, column c = this lane's key
+        AT s = AT(0), dp = AT(0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+          const VT x = *reinterpret_cast<const VT*>(Qs + c * LD + 16 * g + VEC * f);
+          const VT y = *reinterpret_cast<const VT*>(Gs + c * LD + 16 * g + VEC * f);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            s = M::mma(x[e], kf[f][e], s);
+            dp = M::mma(y[e], vf[f][e], dp);
+          }
+        }
+        auto probs = [&](auto maskc) {
+          constexpr bool MASK = decltype(maskc)::value;  // the diagonal tile
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = M::row(i, g);
+            T pr = ex2(__builtin_fmaf(s[i], sl2, -ST[r]));
+            if constexpr (MASK) pr = c > r ? T(0) : pr;  // key above the query: masked
+            s[i] = pr;
+            dp[i] = pr * (dp[i] - ST[MT + r]);
+          }
+        };
+        if (qt == j)
+          probs(std::true_type());
+        else
+          probs(std::false_type());
+        // dS tile (qt, j), [query][key]: queries row(i, g), this lane's key
+        const uint32_t tb = (uint32_t)((qt * (qt + 1) / 2 + j) * (MT * MT)) * S;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) buf_store1(dp[i], rS, (uint32_t)(M::row(i, g) * MT + c) * S, tb);
+        // dV^T += dO^T P ; dK^T += Q^T dS: result tile t, row r is d = 4 r + t,
+        // column = this lane's key, so a lane's A operands are dO and Q rows
+        // row(i, g), d = 4c .. 4c + 3 (16-byte reads)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = M::row(i, g);
-          T pr = ex2(__builtin_fmaf(s[i], sl2, -ST[r]));
-          if constexpr (MASK) pr = c > r ? T(0) : pr;  // key above the query: masked
-          s[i] = pr;
-          dp[i] = pr * (dp[i] - ST[MT + r]);
-        }
-      };
-      if (qt == j)
-        probs(std::true_type());
-      else
-        probs(std::false_type());
-      // dS tile (qt, j), [query][key]: queries row(i, g), this lane's key
-      const uint32_t tb = (uint32_t)((qt * (qt + 1) / 2 + j) * (MT * MT)) * S;
+          VT gv[4 / VEC], qv[4 / VEC];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) buf_store1(dp[i], rS, (uint32_t)(M::row(i, g) * MT + c) * S, tb);
-      // dV^T += dO^T P ; dK^T += Q^T dS: result tile t, row r is d = 4 r + t,
-      // column = this lane's key, so a lane's A operands are dO and Q rows
-      // row(i, g), d = 4c .. 4c + 3 (16-byte reads)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = M::row(i, g);
-        VT gv[4 / VEC], qv[4 / VEC];
-#pragma unroll
-        for (int v = 0; v < 4 / VEC; ++v) {
-          gv[v] = *reinterpret_cast<const VT*>(Gs + r * LD + 4 * c + VEC * v);
-          qv[v] = *reinterpret_cast<const VT*>(Qs + r * LD + 4 * c + VEC * v);
-        }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          dv[t] = M::mma(gv[t / VEC][t % VEC], s[i], dv[t]);
-          dk[t] = M::mma(qv[t / VEC][t % VEC], dp[i], dk[t]);
-        }
-      }
-      wave_sync();
-      if (more) put();
-      wave_sync();
-    }
-    if (wave == 1) {
-      if (seg == 0) {  // key tile j's later query tiles: handed to wave 0
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            stash[(dt * 4 + i) * 64 + lane] = dk[dt][i];
-            stash[(16 + dt * 4 + i) * 64 + lane] = dv[dt][i];
+          for (int v = 0; v < 4 / VEC; ++v) {
+            gv[v] = *reinterpret_cast<const VT*>(Gs + r * LD + 4 * c + VEC * v);
+            qv[v] = *reinterpret_cast<const VT*>(Qs + r * LD + 4 * c + VEC * v);
           }
-      } else {
-        store_kv16<T>(a, b, h, k0, dk, dv, g, c);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            dv[t] = M::mma(gv[t / VEC][t % VEC], s[i], dv[t]);
+            dk[t] = M::mma(qv[t / VEC][t % VEC], dp[i], dk[t]);
+          }
+        }
+        wave_sync();
+        if (more) put();
+        wave_sync();
+      }
+      if (wave == 1) {
+        if (seg == 0) {  // key tile j's later query tiles: handed to wave 0
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              stash[(dt * 4 + i) * 64 + lane] = dk[dt][i];
+              stash[(16 + dt * 4 + i) * 64 + lane] = dv[dt][i];
+            }
+        } else {
+          store_kv16<T>(a, b, h, k0, dk, dv, g, c);
+        }
       }
     }
-  }
-  __syncthreads();  // wave 1's partial of key tile j is in the stash
-  if (wave == 0) {
+    __syncthreads();  // wave 1's partial of key tile j is in the stash
+    if (wave == 0) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+      for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        dk[dt][i] += stash[(dt * 4 + i) * 64 + lane];
-        dv[dt][i] += stash[(16 + dt * 4 + i) * 64 + lane];
-      }
-    store_kv16<T>(a, b, h, p * MT, dk, dv, g, c);
+        for (int i = 0; i < 4; ++i) {
+          dk[dt][i] += stash[(dt * 4 + i) * 64 + lane];
+          dv[dt][i] += stash[(16 + dt * 4 + i) * 64 + lane];
+        }
+      store_kv16<T>(a, b, h, p * MT, dk, dv, g, c);
+    }
+    __syncthreads();  // the stash is read before the next pair writes it
   }
 }
 
@@ -1649,6 +1655,34 @@ static int attn_fwd_impl(AttnArgs& a) {
 // the recompute path can be exercised at any size.
 static int64_t g_max_ds_bytes = (int64_t)4 << 30;
 
+// Key-tile pairs per key-pass block. The key pass's blocks all take the same
+// time, so a grid of b blocks with s of them resident at once runs ceil(b / s)
+// rounds; k pairs per block cost ceil(b_k / s) * k pair-times, b_k = bh *
+// ceil(pairs / k). Take the cheapest k, the larger on a tie: each round
+// starts with every block loading its first tiles at once and ends with all
+// of them storing, which the rounds do not overlap (B 8, H 12, T 1024: two
+// rounds of one pair 236 us, one round of two pairs 225 us).
+static unsigned kvp_pairs_per_block(int64_t bh, unsigned pairs) {
+  static int resident = -1;  // blocks per CU
+  if (resident < 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_bwd_kvp_kernel<float>, 128, 0) != hipSuccess) n = 0;
+    resident = n;
+  }
+  const int64_t slots = (int64_t)resident * num_cus();
+  if (slots <= 0) return 1;
+  unsigned best = 1;
+  int64_t best_cost = INT64_MAX;
+  for (unsigned k = 1; k <= pairs && k <= 8; ++k) {
+    const int64_t cost = cdiv(bh * cdiv((int64_t)pairs, (int64_t)k), slots) * k;
+    if (cost <= best_cost) {
+      best_cost = cost;
+      best = k;
+    }
+  }
+  return best;
+}
+
 template <typename T>
 static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
   constexpr int MT = AM<T>::MT;
@@ -1692,7 +1726,8 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
     if (pair16 && a.ds) {
       if constexpr (std::is_same<T, float>::value) {
         const unsigned pairs = (unsigned)(a.T / 32);
-        attn_bwd_kvp_kernel<T><<<dim3((unsigned)(a.B * a.H), pairs), 128, 0, stream()>>>(a);
+        const unsigned per = kvp_pairs_per_block(a.B * a.H, pairs);
+        attn_bwd_kvp_kernel<T><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, per)), 128, 0, stream()>>>(a);
         // fewer than two four-pair blocks per CU: split the d-tiles instead
         if ((int64_t)a.B * a.H * cdiv(pairs, 4) < 2 * (int64_t)num_cus())
           attn_bwd_qp_kernel<T, 2><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, 2)), 512, 0, stream()>>>(a);
