@@ -596,24 +596,33 @@ __global__ void __launch_bounds__(256) attn_drow_kernel(AttnArgs a) {
 }
 
 // Rows of D = 64: 16 lanes per row, four consecutive elements of O and dO
-// each (one 16-byte vector in float32, two in float64), 16 rows per
-// 256-thread block.
+// each (one 16-byte vector in float32, two in float64), two rows per lane
+// group (both rows' loads in flight at once), 32 rows per 256-thread block.
 template <typename T>
 __global__ void __launch_bounds__(256) attn_drow64_kernel(AttnArgs a) {
   typedef T v4 __attribute__((ext_vector_type(4)));
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  constexpr int RPT = 2;
   const int q = threadIdx.x & 15;
   const int64_t total = a.B * a.H * a.T;
-  T s = T(0);
-  if (row < total) {
-    const int64_t t = row % a.T, bh = row / a.T, b = bh / a.H, h = bh % a.H;
-    const v4 o = *reinterpret_cast<const v4*>((const T*)a.o + b * a.so.b + h * a.so.h + t * a.so.t + 4 * q);
-    const v4 g = *reinterpret_cast<const v4*>((const T*)a.dO + b * a.sdo.b + h * a.sdo.h + t * a.sdo.t + 4 * q);
-    s = ((o[0] * g[0] + o[1] * g[1]) + o[2] * g[2]) + o[3] * g[3];
+  const int64_t row0 = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) * RPT;
+  v4 o[RPT], g[RPT];
+#pragma unroll
+  for (int u = 0; u < RPT; ++u) {
+    const int64_t row = row0 + u;
+    o[u] = g[u] = v4(0);
+    if (row < total) {
+      const int64_t t = row % a.T, bh = row / a.T, b = bh / a.H, h = bh % a.H;
+      o[u] = *reinterpret_cast<const v4*>((const T*)a.o + b * a.so.b + h * a.so.h + t * a.so.t + 4 * q);
+      g[u] = *reinterpret_cast<const v4*>((const T*)a.dO + b * a.sdo.b + h * a.sdo.h + t * a.sdo.t + 4 * q);
+    }
   }
 #pragma unroll
-  for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
-  if (q == 0 && row < total) ((T*)a.drow)[row] = s;
+  for (int u = 0; u < RPT; ++u) {
+    T s = ((o[u][0] * g[u][0] + o[u][1] * g[u][1]) + o[u][2] * g[u][2]) + o[u][3] * g[u][3];
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) s += __shfl_xor(s, off, 16);
+    if (q == 0 && row0 + u < total) ((T*)a.drow)[row0 + u] = s;
+  }
 }
 
 // ------------------------------------------------- backward A: dK and dV
@@ -1718,7 +1727,7 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
                         strides_vec(a.sdo, VE);
     if (drow_in) {
     } else if (drow64) {
-      attn_drow64_kernel<T><<<(unsigned)cdiv(rows, 16), 256, 0, stream()>>>(a);
+      attn_drow64_kernel<T><<<(unsigned)cdiv(rows, 32), 256, 0, stream()>>>(a);
     } else {
       attn_drow_kernel<T><<<(unsigned)cdiv(rows, 4), 256, 0, stream()>>>(a);
     }
