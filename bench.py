@@ -170,6 +170,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--warm-s", type=float, default=0.5,
+                    help="least warm-up time of a microbenchmark, seconds (the GPU clock leaves idle over ~50 ms)")
     ap.add_argument("--cpu-seq", type=int, default=8,
                     help="sequences of one replica in the CPU baseline sample (8: the whole replica batch)")
     ap.add_argument("--seed", type=int, default=5)
@@ -337,13 +339,10 @@ def _threads():
         return int(os.environ.get("OMP_NUM_THREADS", "1"))
 
 
-WARM_S = 0.5  # least warm-up time of a microbenchmark
-
-
 def _timed(a, fn, families):
     """Wall time of `steps` uninstrumented calls, then per-family kernel time
     from `steps` more calls with HIP events around every launch. The warm-up
-    is `warmup` calls and at least WARM_S seconds: a GPU that comes out of
+    is `warmup` calls and at least `--warm-s` seconds: a GPU that comes out of
     idle raises its clock over the first ~50 ms of work (the float32 attention
     backward at B 8, H 12, T 1024 takes 288 us per call over its first 20
     calls and 238 us from the second tenth of a second on), so a few short
@@ -351,7 +350,7 @@ def _timed(a, fn, families):
     from dtmi import _lib
     t0 = time.perf_counter()
     n = 0
-    while n < a.warmup or time.perf_counter() - t0 < WARM_S:
+    while n < a.warmup or time.perf_counter() - t0 < a.warm_s:
         fn()
         n += 1
         if n % 16 == 0:
