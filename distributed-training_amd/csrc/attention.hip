@@ -1132,10 +1132,11 @@ __host__ __device__ inline int64_t ds16_tiles(int64_t nt) { return nt * (nt + 1)
 // j' = nt - 1 - p of 16 keys (nt = T / 16 tiles, even), then for the pairs
 // p + gridDim.y, ... when the grid is shortened to fit one round of resident
 // blocks: key tile j is seen by the nt - p query tiles p .. nt - 1, key tile
-// j' by p + 1, nt + 1 tile pairs in all. Wave 0 takes key tile j with query tiles p .. p + nt/2 - 1; wave 1
-// the rest of key tile j (query tiles p + nt/2 .. nt - 1), then all of key
-// tile j'. Every wave thus carries nt/2 or nt/2 + 1 tile pairs whatever p, and
-// one two-way sum (key tile j's partial dK and dV, wave 0's first) remains.
+// j' by p + 1, nt + 1 tile pairs in all. Wave 0 takes key tile j with query
+// tiles p .. p + nt/2 - 1; wave 1 the rest of key tile j (query tiles
+// p + nt/2 .. nt - 1), then all of key tile j'. Every wave thus carries nt/2
+// or nt/2 + 1 tile pairs whatever p, and one two-way sum (key tile j's
+// partial dK and dV, wave 0's first) remains.
 // Each lane holds its key's K and V slices in registers; the query tiles'
 // Q and dO rows pass through the wave's own LDS, the next one prefetched into
 // registers. For each tile pair: S = Q K^T and dP = dO V^T, P recomputed from
