@@ -93,22 +93,26 @@ def test_backward_paired_ranges_at_every_pair_count(dev, T):
             assert bits_equal(x, y)
 
 
-def test_dq_pass_block_shapes_agree_bit_for_bit(dev):
-    """The float32 dQ pass takes four query-tile pairs per block when there are
-    at least two such blocks per CU, else two pairs with each query tile's
-    d-tiles split over two waves. Both add the key tiles in the same order, so
-    a (batch, head) gets the same bits either way: B 40, H 8, T 256 (640
-    four-pair blocks) against its first two batch elements alone (32 blocks),
-    and those against the oracle."""
+@pytest.mark.parametrize("B,H,T", [(40, 8, 256), (36, 4, 352)])
+def test_paired_grid_shapes_agree_bit_for_bit(dev, B, H, T):
+    """The float32 paired-range passes pick their grids by size: the dQ pass
+    takes four query-tile pairs per block when there are at least two such
+    blocks per CU, else two pairs with each query tile's d-tiles split over two
+    waves; the key pass takes several key-tile pairs per block when one pair
+    per block would need more than one round of resident blocks (at T 352 its
+    11 pairs do not divide evenly over the blocks). Each order of additions is
+    the same either way, so a (batch, head) gets the same bits: the full batch
+    against its first two batch elements alone (split d-tiles, one pair per
+    key-pass block), and those against the oracle."""
     D, K = _dev()
-    rng = np.random.default_rng(40)
-    q, k, v, g = (rng.standard_normal((40, 8, 256, 64)).astype(np.float32) for _ in range(4))
+    rng = np.random.default_rng(B + T)
+    q, k, v, g = (rng.standard_normal((B, H, T, 64)).astype(np.float32) for _ in range(4))
 
     def bwd(sl):
         x = [D.from_numpy(np.ascontiguousarray(t[sl])) for t in (q, k, v, g)]
         o, rmax, rsum = K.attn_fwd(x[0], x[1], x[2])
         return [t.numpy() for t in K.attn_bwd(x[0], x[1], x[2], o, x[3], rmax, rsum)]
-    full, part = bwd(slice(0, 40)), bwd(slice(0, 2))
+    full, part = bwd(slice(0, B)), bwd(slice(0, 2))
     for a, b in zip(full, part):
         assert bits_equal(a[:2], b)
     o_ref, p, scale = ops.attention_fwd(q[:2], k[:2], v[:2])
