@@ -74,6 +74,19 @@ def test_forward_over_many_key_tiles(dev, T):
             assert bits_equal(x, y)
 
 
+@pytest.mark.parametrize("T", [4096, 8192])
+def test_float32_attention_at_long_sequences(dev, T):
+    """The float32 kernels accumulate in float32 where dtrain (NumPy 2)
+    promotes to float64: at T = 4096 and 8192 (one batch element and head, so
+    the oracle's T x T arrays stay within a few GB) the outputs, the row
+    statistics and dQ, dK, dV stay within 1e-5 of the float64-promoted
+    oracle."""
+    D, K = _dev()
+    rng = np.random.default_rng(T + 1)
+    q, k, v, g = (rng.standard_normal((1, 1, T, 64)).astype(np.float32) for _ in range(4))
+    _check(D, K, q, k, v, g, np.float32)
+
+
 @pytest.mark.parametrize("T", [32, 64, 96, 160, 288, 352])
 def test_backward_paired_ranges_at_every_pair_count(dev, T):
     """The float32 paired-range backward (16 x 16 tiles, key tile j with its
