@@ -1647,38 +1647,158 @@ static int attn_bwd_wide(AttnArgs& a) {
   return DTMI_OK;
 }
 
-template <typename T>
-static int attn_fwd_impl(AttnArgs& a) {
-  constexpr int MT = AM<T>::MT;
-  const int dp = pick_dp<T>(a.D);
-  if (dp < 0) return attn_fwd_wide<T>(a);
-  dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
-  // causal-exact FLOP: 2 GEMMs of 2*D*T(T+1)/2 per (b, h)
-  TimedLaunch tl(DTMI_FAM_ATTN_FWD, 2.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
-  DP_SWITCH(dp, attn_fwd_kernel, T, grid)
-  LAUNCH_CHECK("attn_fwd_kernel");
-  return DTMI_OK;
+// Forward on 16 x 16 tiles over paired ranges (float32 with 16-byte aligned
+// Q, K and V, D = 64, T a multiple of 32): block (bh, p), one wave, query tile p and then its mirror
+// nt - 1 - p, which see p + 1 and nt - p key tiles, nt + 1 in all, so every
+// wave carries the same work (then the pairs p + gridDim.y, ... when the grid
+// is shortened to one round of resident blocks). The wave's queries are the
+// MFMA columns: S^T = K Q^T with K rows read from the wave's own LDS and the
+// lane's Q slice (its query c, d = 16 g .. 16 g + 15, times scale * log2(e))
+// in registers; P feeds O^T += V^T P^T from registers; the next key tile's K
+// and V rows are prefetched into registers while the current one is computed.
+// Lazy rescaling against a reference max as in attn_fwd_kernel.
+__global__ void __launch_bounds__(64) attn_fwd_p16_kernel(AttnArgs a) {
+  using M = A16<float>;
+  typedef M::vec_t VT;
+  typedef M::acc_t AT;
+  constexpr int MT = 16, DP = 64, VEC = 4, LD = DP + VEC, TILE = MT * LD;
+  constexpr int NV = MT * DP / VEC / 64;  // 16-byte vectors per lane per tile and operand
+  constexpr int RPV = 64 * VEC / DP;      // rows per vector index
+  constexpr int NF = 16 / VEC;            // vectors of a lane's 16-element Q slice
+  __shared__ __attribute__((aligned(16))) float lds[2 * TILE];
+  float* Ks = lds;
+  float* Vs = lds + TILE;
+  const int bh = blockIdx.x;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  const int Tn = (int)a.T, nt = Tn / MT;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, c = lane & 15;
+  const float* Q = (const float*)a.q + b * a.sq.b + h * a.sq.h;
+  const float* K = (const float*)a.k + b * a.sk.b + h * a.sk.h;
+  const float* V = (const float*)a.v + b * a.sv.b + h * a.sv.h;
+  float* O = (float*)a.out + b * a.so.b + h * a.so.h;
+  const float sl2 = (float)(a.scale * 1.4426950408889634);
+  constexpr uint32_t S = 4;
+  const Rsrc rK = make_rsrc(K, (uint64_t)Tn * a.sk.t * S), rV = make_rsrc(V, (uint64_t)Tn * a.sv.t * S);
+  const int lrow = lane / (DP / VEC), lcol = (lane % (DP / VEC)) * VEC;
+  const uint32_t vk = (uint32_t)(lrow * a.sk.t + lcol) * S, vv = (uint32_t)(lrow * a.sv.t + lcol) * S;
+  VT rk[NV], rv[NV];
+  auto fetch = [&](int j) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      rk[v] = buf_load_v<VT>(rK, vk, (uint32_t)((j * MT + RPV * v) * a.sk.t) * S);
+      rv[v] = buf_load_v<VT>(rV, vv, (uint32_t)((j * MT + RPV * v) * a.sv.t) * S);
+    }
+  };
+  auto put = [&]() {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const int r = RPV * v + lrow;
+      *reinterpret_cast<VT*>(Ks + r * LD + lcol) = rk[v];
+      *reinterpret_cast<VT*>(Vs + r * LD + lcol) = rv[v];
+    }
+  };
+  auto wave_sync = [] {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  auto gmax = [](float x) {
+    x = fmaxf(x, __shfl_xor(x, 16, 64));
+    return fmaxf(x, __shfl_xor(x, 32, 64));
+  };
+  // pairs p = blockIdx.y, + gridDim.y, ...: more than one when the grid would
+  // otherwise run in several rounds of resident blocks
+  for (int p = (int)blockIdx.y; p < nt / 2; p += (int)gridDim.y)
+  for (int seg = 0; seg < 2; ++seg) {
+    const int qt = seg == 0 ? p : nt - 1 - p;
+    const int q0 = qt * MT;
+    VT qf[NF];
+    const float* qrow = Q + (int64_t)(q0 + c) * a.sq.t + 16 * g;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) qf[f] = *reinterpret_cast<const VT*>(qrow + VEC * f) * sl2;
+    AT o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[t] = AT(0);
+    float mref = -INFINITY, mtop = -INFINITY, l = 0.f;
+    fetch(0);
+    put();
+    drain_vm();
+    wave_sync();
+    for (int j = 0; j <= qt; ++j) {
+      const bool more = j < qt;
+      if (more) fetch(j + 1);
+      // S^T(key 4g + i, query c) in base-2 units
+      AT s = AT(0);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const VT x = *reinterpret_cast<const VT*>(Ks + c * LD + 16 * g + VEC * f);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) s = M::mma(x[e], qf[f][e], s);
+      }
+      if (j == qt) {  // the diagonal tile: keys after the query masked
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[i] = 4 * g + i > c ? -INFINITY : s[i];
+      }
+      float bmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      mtop = fmaxf(mtop, bmax);
+      if (__any(bmax > mref + kLazyLog2)) {
+        const float mnew = fmaxf(mref, gmax(bmax));
+        const float alpha = ex2(mref - mnew);  // mref = -inf on the first tile: 0
+        l *= alpha;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] *= alpha;
+        mref = mnew;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[i] = ex2(s[i] - mref);
+        l += s[i];
+      }
+      // O^T(d = 4 m + t, query c) += sum over the tile's keys of V(key, d) P(key, query)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const VT vr = *reinterpret_cast<const VT*>(Vs + (4 * g + i) * LD + 4 * c);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] = M::mma(vr[t], s[i], o[t]);
+      }
+      wave_sync();
+      if (more) put();
+      wave_sync();
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    mtop = gmax(mtop);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    // lane (g, c) register i of tile t: d = 4 (4 g + i) + t of query c
+    float* orow = O + (int64_t)(q0 + c) * a.so.t + 16 * g;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const VT x = {o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv};
+      if (a.ovec) {
+        *reinterpret_cast<VT*>(orow + 4 * i) = x;
+      } else {  // O not 16-byte aligned: element stores, same values
+#pragma unroll
+        for (int t = 0; t < 4; ++t) orow[4 * i + t] = x[t];
+      }
+    }
+    if (g == 0) {
+      ((float*)a.rowmax)[(int64_t)bh * Tn + q0 + c] = mtop;
+      ((float*)a.rowsum)[(int64_t)bh * Tn + q0 + c] = l * ex2(mref - mtop);
+    }
+    wave_sync();  // the last tile's rows are read before the next segment's put
+  }
 }
 
-// Largest dS workspace (bytes) the backward takes from the pool; above it the
-// dQ pass recomputes S, P and dP itself. 4 GiB by default; settable so that
-// the recompute path can be exercised at any size.
-static int64_t g_max_ds_bytes = (int64_t)4 << 30;
-
-// Key-tile pairs per key-pass block. The key pass's blocks all take the same
-// time, so a grid of b blocks with s of them resident at once runs ceil(b / s)
-// rounds; k pairs per block cost ceil(b_k / s) * k pair-times, b_k = bh *
-// ceil(pairs / k). Take the cheapest k, the larger on a tie: each round
-// starts with every block loading its first tiles at once and ends with all
-// of them storing, which the rounds do not overlap (B 8, H 12, T 1024: two
-// rounds of one pair 236 us, one round of two pairs 225 us).
-static unsigned kvp_pairs_per_block(int64_t bh, unsigned pairs) {
-  static int resident = -1;  // blocks per CU
-  if (resident < 0) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_bwd_kvp_kernel<float>, 128, 0) != hipSuccess) n = 0;
-    resident = n;
-  }
+// Tile pairs per block of the paired-range forward and key pass. Their blocks
+// all take the same time, so a grid of b blocks with s of them resident at
+// once runs ceil(b / s) rounds; k pairs per block cost ceil(b_k / s) * k
+// pair-times, b_k = bh * ceil(pairs / k). Take the cheapest k, the larger on a
+// tie: each round starts with every block loading its first tiles at once and
+// ends with all of them storing, which the rounds do not overlap (key pass at
+// B 8, H 12, T 1024: two rounds of one pair 236 us, one round of two pairs
+// 225 us). resident: blocks per CU (0 if unknown: one pair per block).
+static unsigned pairs_per_block(int64_t bh, unsigned pairs, int resident) {
   const int64_t slots = (int64_t)resident * num_cus();
   if (slots <= 0) return 1;
   unsigned best = 1;
@@ -1692,6 +1812,43 @@ static unsigned kvp_pairs_per_block(int64_t bh, unsigned pairs) {
   }
   return best;
 }
+
+template <typename F>
+static int resident_blocks(F kernel, int threads) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, 0) != hipSuccess) n = 0;
+  return n;
+}
+
+template <typename T>
+static int attn_fwd_impl(AttnArgs& a) {
+  constexpr int MT = AM<T>::MT;
+  const int dp = pick_dp<T>(a.D);
+  if (dp < 0) return attn_fwd_wide<T>(a);
+  dim3 grid((unsigned)cdiv(a.T, 4 * MT), (unsigned)(a.B * a.H));
+  // causal-exact FLOP: 2 GEMMs of 2*D*T(T+1)/2 per (b, h)
+  TimedLaunch tl(DTMI_FAM_ATTN_FWD, 2.0 * 2.0 * a.B * a.H * a.D * (double)a.T * (a.T + 1) / 2.0);
+  if constexpr (std::is_same<T, float>::value) {
+    // D = 64, T a multiple of 32, 16-byte reads of Q, K and V: the
+    // paired-range forward on 16 x 16 tiles (O aligned or not, same bits)
+    if (a.vec && a.D == 64 && a.T % 32 == 0) {
+      static const int resident = resident_blocks(attn_fwd_p16_kernel, 64);
+      const unsigned pairs = (unsigned)(a.T / 32);
+      const unsigned per = pairs_per_block(a.B * a.H, pairs, resident);
+      attn_fwd_p16_kernel<<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, per)), 64, 0, stream()>>>(a);
+      LAUNCH_CHECK("attn_fwd_p16_kernel");
+      return DTMI_OK;
+    }
+  }
+  DP_SWITCH(dp, attn_fwd_kernel, T, grid)
+  LAUNCH_CHECK("attn_fwd_kernel");
+  return DTMI_OK;
+}
+
+// Largest dS workspace (bytes) the backward takes from the pool; above it the
+// dQ pass recomputes S, P and dP itself. 4 GiB by default; settable so that
+// the recompute path can be exercised at any size.
+static int64_t g_max_ds_bytes = (int64_t)4 << 30;
 
 template <typename T>
 static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
@@ -1736,7 +1893,8 @@ static int attn_bwd_impl(AttnArgs& a, const void* drow_in) {
     if (pair16 && a.ds) {
       if constexpr (std::is_same<T, float>::value) {
         const unsigned pairs = (unsigned)(a.T / 32);
-        const unsigned per = kvp_pairs_per_block(a.B * a.H, pairs);
+        static const int resident = resident_blocks(attn_bwd_kvp_kernel<float>, 128);
+        const unsigned per = pairs_per_block(a.B * a.H, pairs, resident);
         attn_bwd_kvp_kernel<T><<<dim3((unsigned)(a.B * a.H), (unsigned)cdiv(pairs, per)), 128, 0, stream()>>>(a);
         // fewer than two four-pair blocks per CU: split the d-tiles instead
         if ((int64_t)a.B * a.H * cdiv(pairs, 4) < 2 * (int64_t)num_cus())

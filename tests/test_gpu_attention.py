@@ -106,17 +106,18 @@ def test_backward_paired_ranges_at_every_pair_count(dev, T):
             assert bits_equal(x, y)
 
 
-@pytest.mark.parametrize("B,H,T", [(40, 8, 256), (36, 4, 352)])
+@pytest.mark.parametrize("B,H,T", [(40, 8, 256), (36, 4, 352), (40, 8, 512)])
 def test_paired_grid_shapes_agree_bit_for_bit(dev, B, H, T):
     """The float32 paired-range passes pick their grids by size: the dQ pass
     takes four query-tile pairs per block when there are at least two such
     blocks per CU, else two pairs with each query tile's d-tiles split over two
-    waves; the key pass takes several key-tile pairs per block when one pair
-    per block would need more than one round of resident blocks (at T 352 its
-    11 pairs do not divide evenly over the blocks). Each order of additions is
+    waves; the key pass and the forward take several tile pairs per block when
+    one pair per block would need more than one round of resident blocks (at
+    T 352 the key pass's 11 pairs do not divide evenly over the blocks; at
+    T 512 the forward takes two pairs per block). Each order of additions is
     the same either way, so a (batch, head) gets the same bits: the full batch
     against its first two batch elements alone (split d-tiles, one pair per
-    key-pass block), and those against the oracle."""
+    block), and those against the oracle."""
     D, K = _dev()
     rng = np.random.default_rng(B + T)
     q, k, v, g = (rng.standard_normal((B, H, T, 64)).astype(np.float32) for _ in range(4))
@@ -124,8 +125,11 @@ def test_paired_grid_shapes_agree_bit_for_bit(dev, B, H, T):
     def bwd(sl):
         x = [D.from_numpy(np.ascontiguousarray(t[sl])) for t in (q, k, v, g)]
         o, rmax, rsum = K.attn_fwd(x[0], x[1], x[2])
-        return [t.numpy() for t in K.attn_bwd(x[0], x[1], x[2], o, x[3], rmax, rsum)]
+        return [t.numpy() for t in K.attn_bwd(x[0], x[1], x[2], o, x[3], rmax, rsum) + (o, rmax, rsum)]
     full, part = bwd(slice(0, B)), bwd(slice(0, 2))
+    assert bits_equal(full[3][:2], part[3])  # the forward's output
+    assert bits_equal(full[4][:2], part[4]) and bits_equal(full[5][:2], part[5])  # its row statistics
+    full, part = full[:3], part[:3]
     for a, b in zip(full, part):
         assert bits_equal(a[:2], b)
     o_ref, p, scale = ops.attention_fwd(q[:2], k[:2], v[:2])
