@@ -41,6 +41,11 @@
 
 namespace dtmi {
 
+// One float64 through a buffer resource.
+__device__ __forceinline__ double buf_load_f64(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0));
+}
+
 template <typename T>
 struct AM;
 template <>
@@ -663,8 +668,9 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
   T* DS = a.ds ? (T*)a.ds + (int64_t)bh * Tn * Tn : nullptr;
   const T sl2 = (T)(a.scale * 1.4426950408889634);
   const bool vec = a.vec != 0;
-  // this lane's dS byte offset from a tile's first row: row 4g, column kj
-  const unsigned ds_lane = (unsigned)(4 * g * Tn + kj) * (unsigned)sizeof(T);
+  // this lane's dS byte offset from a tile's first row: row 4g (float32) or g
+  // (float64), column kj
+  const unsigned ds_lane = (unsigned)((F32 ? 4 * g : g) * Tn + kj) * (unsigned)sizeof(T);
 
   typename M::vec_t kf[DP / 8], vf[DP / 8];
   load_frag_rows<T, DP>(kf, K, a.sk.t, kj, Tn, D, g, vec);
@@ -802,10 +808,35 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_kv_kernel(AttnArgs a) {
         mma_ldsT_regs<DP, LDT>(dv, Qs + 2 * TILE + TILE_T, 0, s, g, c);
         mma_ldsT_regs<DP, LDT>(dk, Qs + 2 * TILE, 0, dp, g, c);
       } else {
+        if constexpr (FAST) {
+          // Every row of the tile and every key of the block lie inside
+          // [0, T): no bounds tests; dS rows qs + g + 4i are addressed from a
+          // wave-uniform row pointer plus this lane's fixed offset, so the
+          // stores take no vector address arithmetic (same values as prob).
+          T* dsb = DS + (int64_t)qs * Tn;
+          auto probs = [&](auto maskc) {
+            constexpr bool MASK = decltype(maskc)::value;
 #pragma unroll
-        for (int i = 0; i < NACC; ++i) {
-          const int rl = M::row(i, g);
-          prob(i, stats[cur][0][rl], stats[cur][1][rl], stats[cur][2][rl]);
+            for (int i = 0; i < NACC; ++i) {
+              const int rl = M::row(i, g);
+              T p = ex2(s[i] * sl2 - stats[cur][0][rl]) * stats[cur][1][rl];
+              if constexpr (MASK) p = kj <= qs + rl ? p : T(0);
+              s[i] = p;
+              const T v = p * (dp[i] - stats[cur][2][rl]);
+              dp[i] = v;
+              *(T*)((char*)(dsb + (int64_t)(4 * i) * Tn) + ds_lane) = v;
+            }
+          };
+          if (mask)
+            probs(std::true_type());
+          else
+            probs(std::false_type());
+        } else {
+#pragma unroll
+          for (int i = 0; i < NACC; ++i) {
+            const int rl = M::row(i, g);
+            prob(i, stats[cur][0][rl], stats[cur][1][rl], stats[cur][2][rl]);
+          }
         }
         mma_lds_t_regs<T, DP>(dv, Gs, 0, s, g, c);
         mma_lds_t_regs<T, DP>(dk, Qs, 0, dp, g, c);
@@ -853,6 +884,11 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
   const T* K = (const T*)a.k + b * a.sk.b + h * a.sk.h;
   const T* DS = (const T*)a.ds + (int64_t)bh * Tn * Tn;
   const bool vec = a.vec != 0;
+  // float64, aligned: dS through a buffer resource over the (batch, head)
+  // block when its byte offsets fit in 32 bits (T <= 23170)
+  const bool ds_buf = !F32 && FAST && (uint64_t)Tn * Tn * sizeof(T) <= 0xFFFFFFFFull;
+  const Rsrc rS = make_rsrc(DS, (uint64_t)Tn * Tn * sizeof(T));
+  const uint32_t ds_lane = ds_buf ? (uint32_t)(((int64_t)qr * Tn + g) * (int64_t)sizeof(T)) : 0u;
 
   typename M::acc_t dq[DP / MT];
 #pragma unroll
@@ -878,6 +914,16 @@ __global__ void __launch_bounds__(256, 2) attn_bwd_q_ds_kernel(AttnArgs a) {
         for (int e = 0; e < 4; ++e) r[4 * a4 + e] = v[e];
       }
     } else {
+      if constexpr (!F32 && FAST) {
+        if (ds_buf) {
+          // row qr, columns j0 + g + 4 i (every one inside [0, T) on the
+          // aligned path): this lane's byte offset fixed, the tile's and the
+          // register's wave-uniform
+#pragma unroll
+          for (int i = 0; i < NACC; ++i) r[i] = buf_load_f64(rS, ds_lane, (uint32_t)(j0 + 4 * i) * (uint32_t)sizeof(T));
+          return;
+        }
+      }
 #pragma unroll
       for (int i = 0; i < NACC; ++i) {
         const int j = j0 + M::row(i, g);
