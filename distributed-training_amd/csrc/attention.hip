@@ -1694,10 +1694,11 @@ static int attn_bwd_wide(AttnArgs& a) {
 }
 
 // Forward on 16 x 16 tiles over paired ranges (float32 with 16-byte aligned
-// Q, K and V, D = 64, T a multiple of 32): block (bh, p), one wave, query tile p and then its mirror
-// nt - 1 - p, which see p + 1 and nt - p key tiles, nt + 1 in all, so every
-// wave carries the same work (then the pairs p + gridDim.y, ... when the grid
-// is shortened to one round of resident blocks). The wave's queries are the
+// Q, K and V, D = 64, T a multiple of 32): block (bh, p), one wave, query
+// tile p and then its mirror nt - 1 - p, which see p + 1 and nt - p key
+// tiles, nt + 1 in all, so every wave carries the same work (then the pairs
+// p + gridDim.y, ... when the grid is shortened to one round of resident
+// blocks). The wave's queries are the
 // MFMA columns: S^T = K Q^T with K rows read from the wave's own LDS and the
 // lane's Q slice (its query c, d = 16 g .. 16 g + 15, times scale * log2(e))
 // in registers; P feeds O^T += V^T P^T from registers; the next key tile's K
