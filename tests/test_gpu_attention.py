@@ -46,11 +46,13 @@ def test_attention_forward_backward(dev, dt, shape):
     _check(D, K, q, k, v, g, dt)
 
 
-@pytest.mark.parametrize("shape", [(1, 2, 16, 64), (2, 3, 208, 64), (3, 2, 512, 64)])
+@pytest.mark.parametrize("shape", [(1, 2, 16, 64), (2, 3, 208, 64), (3, 2, 512, 64), (1, 2, 2048, 64)])
 def test_float64_backward_at_head_dim_64(dev, shape):
-    """float64, D = 64 on the aligned path (64-key blocks of 16 per wave, the
-    dQ pass reading dS; one tile, T not a multiple of 32 or of 64), against
-    the oracle at 1e-12."""
+    """float64, D = 64 on the aligned path (64-key blocks of 16 per wave, dS
+    stored at wave-uniform row offsets and read back through a buffer
+    resource by the dQ pass; one tile, T not a multiple of 32 or of 64, and
+    T 2048, where a (batch, head)'s dS spans 32 MB), against the oracle at
+    1e-12."""
     D, K = _dev()
     rng = np.random.default_rng(sum(shape) + 64)
     q, k, v, g = (rng.standard_normal(shape) for _ in range(4))
@@ -59,10 +61,11 @@ def test_float64_backward_at_head_dim_64(dev, shape):
 
 @pytest.mark.parametrize("T", [512, 640, 768, 896, 1024, 2048])
 def test_forward_over_many_key_tiles(dev, T):
-    """T of 4 to 8 query blocks of 128 on the aligned float32 path, where the
-    forward's reference max moves only when a score exceeds it by 2^8: oracle
-    parity of the output, of the row statistics (the true max) and of the
-    backward that reads them; identical bits over repeated calls."""
+    """T of 512 to 2048 on the aligned float32 path (the paired-range
+    forward, 33 to 129 key tiles of 16 per query tile pair), where the forward's
+    reference max moves only when a score exceeds it by 2^8: oracle parity of
+    the output, of the row statistics (the true max) and of the backward that
+    reads them; identical bits over repeated calls."""
     D, K = _dev()
     rng = np.random.default_rng(T)
     q, k, v, g = (rng.standard_normal((2, 3, T, 64)).astype(np.float32) for _ in range(4))
