@@ -38,7 +38,8 @@ def _check(D, K, q, k, v, g, dt):
 
 @pytest.mark.parametrize("dt", [np.float64, np.float32])
 @pytest.mark.parametrize("shape", [(1, 2, 4, 3), (1, 2, 8, 4), (2, 2, 5, 4), (8, 4, 32, 16), (2, 3, 100, 64),
-                                   (1, 1, 257, 33), (16, 12, 256, 64)])
+                                   (1, 1, 257, 33), (16, 12, 256, 64), (2, 3, 32, 64), (1, 2, 64, 64),
+                                   (2, 2, 96, 64)])
 def test_attention_forward_backward(dev, dt, shape):
     D, K = _dev()
     rng = np.random.default_rng(sum(shape))
